@@ -1,0 +1,138 @@
+/*
+ * xLLM paged-decode attention for AMD MI355X (gfx950) -- operator C-ABI.
+ *
+ * Drop-in for the paged-attention part of the reference's operator API
+ * (include/operator_api.h:29-116 of ahua2020qq/xLLMs): same symbol names, same
+ * argument order and meaning, `void*` tensors, opaque stream.  All three
+ * reference entry points map to ONE implementation (hand-written gfx950
+ * kernels in libxllm_hip_backend.so); there is no per-entry-point kernel
+ * family and no multi-backend dispatch.
+ *
+ * Semantics (what every entry point computes), with G = num_heads/num_kv_heads:
+ *   for s < num_seqs, h < num_heads, L = seq_lens[s]:
+ *     O[s,h,:] = sum_{t<L} softmax_t(scale * <Q[s,h,:], K_t>) * V_t
+ *   where K_t / V_t is row (t % block_size) of kv head h/G in physical block
+ *   block_tables[s*max_num_blocks_per_seq + t/block_size], i.e. at element
+ *   offset blk*kv_block_stride + (h/G)*kv_head_stride + (t%block_size)*head_size.
+ *   Q and O are [num_seqs][num_heads][head_size].  Arithmetic is fp32; O is
+ *   written in the input dtype.
+ * Contract points the reference leaves undefined, fixed here:
+ *   - seq_lens[s] <= 0 writes a zero row; seq_lens[s] is clamped to
+ *     max_num_blocks_per_seq*block_size.
+ *   - block-table entries are read only for t < L; a negative entry is never
+ *     dereferenced and its tokens contribute nothing.
+ *   - K/V slots past L in the last block are never read (they may hold NaN).
+ *   - Unsupported shapes never compute a wrong size silently: the call does
+ *     nothing on the device and records an error, readable through
+ *     nxt_attn_last_status()/nxt_attn_last_error() on the calling thread.
+ * Supported: head_size in {32,64,80,96,112,128,192,256}; G = 1..32 with
+ * num_heads % num_kv_heads == 0; block_size a power of two in [1, 1024];
+ * 16-byte aligned tensors and strides (every real KV cache layout).
+ *
+ * Calls are asynchronous on `stream` (NULL = the default stream) and never
+ * synchronise, except the rare call that must grow the split-K workspace of
+ * that stream, which first waits for the stream.  Calls on different streams
+ * are independent (one workspace per (device, stream)).
+ */
+#ifndef XLLM_HIP_OPERATOR_API_H_
+#define XLLM_HIP_OPERATOR_API_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#ifndef XLLM_OPERATOR_API_H_
+/* Opaque stream handle: a hipStream_t.  Same type as the reference's
+ * include/operator_api.h:29. */
+typedef void *nxt_stream_t;
+#endif
+
+/* Replaces nxt_paged_attention, include/operator_api.h:63-72 (implemented
+ * there by operators/page_attention.cu:170-322).  dtype_size 2 = fp16,
+ * 4 = fp32, as the reference header documents (operator_api.h:14-16, :59). */
+void nxt_paged_attention(void *out, const void *query, const void *key_cache,
+                         const void *value_cache, const int *block_tables,
+                         const int *seq_lens, int num_seqs, int num_heads, int head_size,
+                         int num_kv_heads, float scale, int max_num_blocks_per_seq,
+                         int block_size, int dtype_size, int kv_block_stride,
+                         int kv_head_stride, nxt_stream_t stream);
+
+/* Replaces nxt_paged_attention_v2, include/operator_api.h:84-93 (implemented
+ * there by operators/page_attention_v2.cu:262-348).  Same computation. */
+void nxt_paged_attention_v2(void *out, const void *query, const void *key_cache,
+                            const void *value_cache, const int *block_tables,
+                            const int *seq_lens, int num_seqs, int num_heads,
+                            int head_size, int num_kv_heads, float scale,
+                            int max_num_blocks_per_seq, int block_size, int dtype_size,
+                            int kv_block_stride, int kv_head_stride, nxt_stream_t stream);
+
+/* Replaces nxt_paged_attention_flash, include/operator_api.h:106-115
+ * (implemented there by operators/flashinfer_adapter.cu:329-433, only under
+ * USE_FLASHINFER).  Exported unconditionally; same computation. */
+void nxt_paged_attention_flash(void *out, const void *query, const void *key_cache,
+                               const void *value_cache, const int *block_tables,
+                               const int *seq_lens, int num_seqs, int num_heads,
+                               int head_size, int num_kv_heads, float scale,
+                               int max_num_blocks_per_seq, int block_size,
+                               int dtype_size, int kv_block_stride, int kv_head_stride,
+                               nxt_stream_t stream);
+
+/* ---- Additive extensions (no counterpart in the reference) -------------- */
+
+/* KV / query / output element type.  The reference's dtype_size cannot name
+ * bf16 (operator_api.h:14-16; NxtDataType in include/backend.h:13-27 has no
+ * BF16), so the extended entry point takes an explicit code. */
+typedef enum {
+    NXT_KV_FP16 = 1,
+    NXT_KV_BF16 = 2,
+    NXT_KV_FP32 = 3,
+} NxtKvDtype;
+
+/* Status codes returned by the extended entry points and recorded for the
+ * void ones. */
+enum {
+    NXT_ATTN_OK = 0,
+    NXT_ATTN_E_INVALID = -1,     /* NULL pointer / negative or inconsistent size */
+    NXT_ATTN_E_UNSUPPORTED = -2, /* head_size, group, block_size, alignment     */
+    NXT_ATTN_E_HIP = -3,         /* HIP runtime / launch failure                */
+    NXT_ATTN_E_NOMEM = -4,       /* split-K workspace allocation failed         */
+};
+
+/* Same computation as nxt_paged_attention, with the dtype named explicitly
+ * (dtype_size must agree: 2 for FP16/BF16, 4 for FP32) and the split-K
+ * partition length in tokens (0 = automatic; otherwise a power of two >= 16
+ * used as given, e.g. to check that results do not depend on it).
+ * Returns NXT_ATTN_OK or a negative status. */
+int nxt_paged_attention_ex(void *out, const void *query, const void *key_cache,
+                           const void *value_cache, const int *block_tables,
+                           const int *seq_lens, int num_seqs, int num_heads,
+                           int head_size, int num_kv_heads, float scale,
+                           int max_num_blocks_per_seq, int block_size, int dtype_size,
+                           int kv_block_stride, int kv_head_stride, nxt_stream_t stream,
+                           int kv_dtype, int partition_tokens);
+
+/* Partition length nxt_paged_attention_ex would use for this shape with
+ * partition_tokens = 0 (needs a current HIP device for its CU count), or a
+ * negative status. */
+int nxt_paged_attention_auto_partition(int num_seqs, int num_heads, int head_size,
+                                       int num_kv_heads, int max_num_blocks_per_seq,
+                                       int block_size, int kv_dtype);
+
+/* Status and message of the last paged-attention call made by this thread. */
+int nxt_attn_last_status(void);
+const char *nxt_attn_last_error(void);
+
+/* Waits for and frees every cached split-K workspace of this process. */
+int nxt_attn_release_workspaces(void);
+
+/* Library version string, e.g. "xllm-hip-attn 0.1.0 gfx950". */
+const char *nxt_attn_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XLLM_HIP_OPERATOR_API_H_ */

@@ -1,0 +1,155 @@
+"""ctypes wrapper of the C oracle (oracle/paged_attention_oracle.c) and of the
+reference's own compiled CPU attention (oracle/_ref, built from
+examples/run_gpt2.c by `make -C oracle ref`).  TEST INFRASTRUCTURE ONLY.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libref_gpt2_attn.so")
+REFERENCE_ROOT = os.environ.get("XLLM_REFERENCE_ROOT", "/root/reference")
+
+_lib = None
+_ref = None
+
+FP16, BF16, FP32 = 1, 2, 3
+
+
+def build(ref: bool = True) -> None:
+    """Compile the oracle (and oracle/_ref when the reference tree exists)."""
+    subprocess.run(["make", "-s", "-C", HERE, "all"], check=True)
+    if ref and os.path.isdir(os.path.join(REFERENCE_ROOT, "examples")):
+        subprocess.run(["make", "-s", "-C", HERE, "ref", f"REF={REFERENCE_ROOT}"], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(ORACLE_SO):
+            build(ref=False)
+        L = ctypes.CDLL(ORACLE_SO)
+        vp, ci, cf, ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_longlong
+        common = [vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, cf, ci, ci, ci, ll, ll]
+        L.oracle_paged_attention_f32.argtypes = common
+        L.oracle_paged_attention_f32.restype = ci
+        L.oracle_paged_attention_f64.argtypes = common
+        L.oracle_paged_attention_f64.restype = ci
+        L.oracle_paged_attention_f32_mt.argtypes = common + [ci]
+        L.oracle_paged_attention_f32_mt.restype = ci
+        L.oracle_num_threads.argtypes = []
+        L.oracle_num_threads.restype = ci
+        L.oracle_gpt2_paged_attention.argtypes = [vp, vp, vp, vp, ci, ci, ci, ci, vp]
+        L.oracle_gpt2_paged_attention.restype = None
+        L.oracle_half_to_float.argtypes = [ctypes.c_uint16]
+        L.oracle_half_to_float.restype = cf
+        L.oracle_bf16_to_float.argtypes = [ctypes.c_uint16]
+        L.oracle_bf16_to_float.restype = cf
+        _lib = L
+    return _lib
+
+
+def ref_lib():
+    """The reference's compiled run_gpt2.c paged_attention, or None."""
+    global _ref
+    if _ref is None and os.path.exists(REF_SO):
+        R = ctypes.CDLL(REF_SO)
+        vp, ci = ctypes.c_void_p, ctypes.c_int
+        R.ref_gpt2_paged_attention.argtypes = [vp, vp, vp, vp, ci, ci, ci, ci, vp]
+        R.ref_gpt2_paged_attention.restype = None
+        _ref = R
+    return _ref
+
+
+def _c(a: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(a)
+
+
+def _args(q, k, v, bt, sl, num_kv_heads, scale, block_size, dtype, kv_block_stride,
+          kv_head_stride):
+    q, k, v, bt, sl = _c(q), _c(k), _c(v), _c(bt.astype(np.int32)), _c(sl.astype(np.int32))
+    B, H, D = q.shape
+    keep = (q, k, v, bt, sl)
+    args = [q.ctypes.data, k.ctypes.data, v.ctypes.data, bt.ctypes.data, sl.ctypes.data,
+            B, H, D, num_kv_heads, ctypes.c_float(scale), bt.shape[1], block_size, dtype,
+            kv_block_stride, kv_head_stride]
+    return keep, args, (B, H, D)
+
+
+def paged_attention(q, k, v, block_tables, seq_lens, *, num_kv_heads, scale, block_size,
+                    dtype, kv_block_stride=None, kv_head_stride=None, precision="f32",
+                    threads=0) -> np.ndarray:
+    """Reference CPU decode attention over operator-API buffers.  q/k/v are
+    numpy arrays holding the element bits (uint16 for fp16/bf16).  Returns fp32
+    (or fp64 for precision='f64') [B][H][D]."""
+    D = q.shape[2]
+    if kv_head_stride is None:
+        kv_head_stride = block_size * D
+    if kv_block_stride is None:
+        kv_block_stride = num_kv_heads * block_size * D
+    keep, args, shape = _args(q, k, v, block_tables, seq_lens, num_kv_heads, scale, block_size,
+                              dtype, kv_block_stride, kv_head_stride)
+    L = lib()
+    if precision == "f64":
+        out = np.empty(shape, dtype=np.float64)
+        rc = L.oracle_paged_attention_f64(out.ctypes.data, *args)
+    elif precision == "mt":
+        out = np.empty(shape, dtype=np.float32)
+        rc = L.oracle_paged_attention_f32_mt(out.ctypes.data, *args, threads)
+    else:
+        out = np.empty(shape, dtype=np.float32)
+        rc = L.oracle_paged_attention_f32(out.ctypes.data, *args)
+    del keep
+    if rc != 0:
+        raise ValueError("oracle rejected the arguments")
+    return out
+
+
+def run_workload(wl, precision="f32", threads=0, seqs=None) -> np.ndarray:
+    """Oracle output for a xllms_amd.workloads.Workload (optionally only the
+    sequences in `seqs`, a slice or index array)."""
+    q, bt, sl = wl.query, wl.block_tables, wl.seq_lens
+    if seqs is not None:
+        q, bt, sl = q[seqs], bt[seqs], sl[seqs]
+    return paged_attention(q, wl.key_cache, wl.value_cache, bt, sl,
+                           num_kv_heads=wl.num_kv_heads, scale=wl.scale,
+                           block_size=wl.block_size, dtype=wl.kv_dtype,
+                           kv_block_stride=wl.kv_block_stride,
+                           kv_head_stride=wl.kv_head_stride, precision=precision,
+                           threads=threads)
+
+
+def gpt2_paged_attention(query, key_cache, value_cache, page_table, seq_len, num_heads,
+                         head_dim, page_size, use_reference=False) -> np.ndarray:
+    """examples/run_gpt2.c:46-83 semantics (MHA, per-token page table, KV
+    layout [page][slot][head][d]).  use_reference=True calls the reference's
+    own compiled function from oracle/_ref instead of the restatement."""
+    q = _c(query.astype(np.float32))
+    k = _c(key_cache.astype(np.float32))
+    v = _c(value_cache.astype(np.float32))
+    pt = _c(np.asarray(page_table, dtype=np.int32))
+    out = np.empty((num_heads, head_dim), dtype=np.float32)
+    if use_reference:
+        R = ref_lib()
+        if R is None:
+            raise FileNotFoundError(REF_SO)
+        fn = R.ref_gpt2_paged_attention
+    else:
+        fn = lib().oracle_gpt2_paged_attention
+    fn(q.ctypes.data, k.ctypes.data, v.ctypes.data, pt.ctypes.data, seq_len, num_heads,
+       head_dim, page_size, out.ctypes.data)
+    return out
+
+
+def widen(bits: np.ndarray, dtype: int) -> np.ndarray:
+    """Element bits -> float32 (exact), matching the oracle's widening."""
+    if dtype == FP32:
+        return bits.astype(np.float32)
+    if dtype == FP16:
+        return bits.view(np.float16).astype(np.float32)
+    return (bits.astype(np.uint32) << 16).view(np.float32)

@@ -1,0 +1,263 @@
+"""GPU parity of the gfx950 paged-decode attention against the CPU oracle.
+
+Every case runs the HIP kernels through the C-ABI (libxllm_hip_backend.so)
+and compares with oracle/ (the C restatement of the reference CPU attention,
+examples/text_gen.c:1284-1310 over include/operator_api.h paged addressing)
+on identical seeded host buffers.  Tolerances are the task's: rel 1e-5 per
+(seq, head) for fp32, atol 2e-3 + rtol 1e-2 elementwise for fp16/bf16.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.helpers import assert_close
+from xllms_amd import paged_attention as PA
+from xllms_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+DT = {"fp16": W.FP16, "bf16": W.BF16, "fp32": W.FP32}
+
+
+def run_gpu(wl, dev=None, *, partition_tokens=0, entry=None, tensors=None, **over):
+    import torch
+    dw = tensors or W.upload(wl)
+    kw = dict(num_kv_heads=wl.num_kv_heads, scale=wl.scale, block_size=wl.block_size,
+              partition_tokens=partition_tokens, kv_dtype=wl.kv_dtype, entry=entry)
+    kw.update(over)
+    PA.paged_attention(dw.out, dw.query, dw.key_cache, dw.value_cache, dw.block_tables,
+                       dw.seq_lens, **kw)
+    torch.cuda.synchronize()
+    return dw.out.float().cpu().numpy()
+
+
+def oracle(wl, seqs=None):
+    return O.run_workload(wl, precision="mt", seqs=seqs)
+
+
+# ---------------------------------------------------------------- shapes
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("head_size", [32, 64, 80, 96, 112, 128, 192, 256])
+def test_head_sizes(cuda, dtype, head_size):
+    wl = W.small_case(num_seqs=3, H=4, KVH=2, D=head_size, kv_dtype=DT[dtype],
+                      seed=100 + head_size, max_len=150)
+    print(f"case head_size={head_size} {dtype} lens={wl.seq_lens.tolist()}", flush=True)
+    assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"d={head_size} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("heads", [(8, 8), (8, 4), (6, 2), (8, 2), (12, 4), (16, 2), (40, 8),
+                                   (32, 2), (64, 4), (64, 2)])
+def test_gqa_groups(cuda, dtype, heads):
+    H, KVH = heads
+    wl = W.small_case(num_seqs=3, H=H, KVH=KVH, D=128, kv_dtype=DT[dtype], seed=H * 7 + KVH,
+                      max_len=180)
+    print(f"case H={H} KVH={KVH} {dtype} lens={wl.seq_lens.tolist()}", flush=True)
+    assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"H={H} KVH={KVH} {dtype}")
+
+
+@pytest.mark.parametrize("block_size", [1, 2, 4, 8, 16, 32, 64, 256])
+@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
+def test_block_sizes(cuda, block_size, dtype):
+    wl = W.small_case(num_seqs=3, H=8, KVH=2, D=64, bs=block_size, kv_dtype=DT[dtype],
+                      seed=block_size, max_len=300)
+    print(f"case block_size={block_size} {dtype} lens={wl.seq_lens.tolist()}", flush=True)
+    assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"bs={block_size}")
+
+
+@pytest.mark.parametrize("part", [16, 64, 512, 4096])
+def test_split_k_partition_independent(cuda, part):
+    """Output does not depend on the split-K partition length (vs the oracle
+    and vs one-partition-per-sequence)."""
+    wl = W.small_case(num_seqs=4, H=32, KVH=8, D=128, kv_dtype=W.FP16, seed=11,
+                      lens=[1, 17, 1500, 3000])
+    print(f"case partition={part}", flush=True)
+    got = run_gpu(wl, partition_tokens=part)
+    assert_close(got, oracle(wl), wl.kv_dtype, f"part={part}")
+    whole = run_gpu(wl, partition_tokens=4096)
+    assert np.abs(got - whole).max() <= 2e-3
+
+
+# --------------------------------------------------------- entry points
+def test_entry_points_identical(cuda):
+    """nxt_paged_attention, _v2 and _flash (operator_api.h:63-115) are one
+    implementation: bit-identical outputs."""
+    wl = W.small_case(num_seqs=5, H=32, KVH=8, D=128, kv_dtype=W.FP16, seed=3, max_len=900)
+    dw = W.upload(wl)
+    outs = [run_gpu(wl, entry=e, tensors=dw, kv_dtype=None).copy() for e in PA.ENTRY_POINTS]
+    assert_close(outs[0], oracle(wl), wl.kv_dtype, "nxt_paged_attention")
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+
+
+def test_fp32_entry_point(cuda):
+    wl = W.config1()
+    got = run_gpu(wl, entry="nxt_paged_attention", kv_dtype=None)
+    assert_close(got, oracle(wl), W.FP32, "config1 via nxt_paged_attention")
+
+
+# ------------------------------------------------------- invariants
+def test_single_token_returns_v_exactly(cuda):
+    """L = 1: softmax weight 1, output = V row bit-for-bit."""
+    for dt in (W.FP16, W.BF16, W.FP32):
+        wl = W.small_case(num_seqs=4, H=8, KVH=2, D=128, kv_dtype=dt, seed=5, lens=[1, 1, 1, 1])
+        got = run_gpu(wl)
+        v = O.widen(wl.value_cache, dt)
+        G = wl.group
+        for s in range(wl.num_seqs):
+            blk = wl.block_tables[s, 0]
+            for h in range(wl.num_heads):
+                assert np.array_equal(got[s, h], v[blk, h // G, 0]), (dt, s, h)
+
+
+def test_constant_keys_give_mean_of_v(cuda):
+    wl = W.small_case(num_seqs=2, H=8, KVH=2, D=64, kv_dtype=W.FP32, seed=9, lens=[37, 300],
+                      poison=False)
+    wl.key_cache[...] = 0.5
+    got = run_gpu(wl)
+    v = wl.value_cache
+    G = wl.group
+    for s, L in enumerate(wl.seq_lens):
+        rows = np.stack([v[wl.block_tables[s, t // 16], :, t % 16, :] for t in range(L)])
+        mean = rows.astype(np.float64).mean(axis=0)  # [KVH][D]
+        for h in range(wl.num_heads):
+            np.testing.assert_allclose(got[s, h], mean[h // G], rtol=1e-5, atol=2e-5)
+
+
+def test_page_permutation_invariance(cuda):
+    """Relabelling physical pages together with the table: identical bits."""
+    wl = W.small_case(num_seqs=4, H=16, KVH=4, D=128, kv_dtype=W.BF16, seed=21, max_len=700)
+    a = run_gpu(wl).copy()
+    perm = np.random.default_rng(1).permutation(wl.num_blocks).astype(np.int32)
+    wl.key_cache = np.ascontiguousarray(wl.key_cache[np.argsort(perm)])
+    wl.value_cache = np.ascontiguousarray(wl.value_cache[np.argsort(perm)])
+    bt = wl.block_tables.copy()
+    bt[bt >= 0] = perm[bt[bt >= 0]]
+    wl.block_tables = bt
+    b = run_gpu(wl)
+    assert np.array_equal(a, b)
+
+
+def test_garbage_isolation(cuda):
+    """NaN/Inf in unused pages and in tail slots never reach the output."""
+    clean = W.small_case(num_seqs=6, H=32, KVH=8, D=128, kv_dtype=W.FP16, seed=33,
+                         max_len=400, poison=False)
+    dirty = W.small_case(num_seqs=6, H=32, KVH=8, D=128, kv_dtype=W.FP16, seed=33,
+                         max_len=400, poison=True)
+    a, b = run_gpu(clean), run_gpu(dirty)
+    assert np.isfinite(b).all()
+    assert np.array_equal(a, b)
+
+
+def test_identical_heads_in_group(cuda):
+    """Query heads h of one group share kv head h/G (not h % KVH): equal Q rows
+    in a group give equal outputs, and each group follows its own kv head."""
+    wl = W.small_case(num_seqs=2, H=8, KVH=2, D=128, kv_dtype=W.FP16, seed=44, max_len=200)
+    G = wl.group
+    for s in range(wl.num_seqs):
+        for h in range(wl.num_heads):
+            wl.query[s, h] = wl.query[s, (h // G) * G]
+    got = run_gpu(wl)
+    for h in range(wl.num_heads):
+        assert np.array_equal(got[:, h], got[:, (h // G) * G])
+    assert not np.array_equal(got[:, 0], got[:, G])
+    assert_close(got, oracle(wl), wl.kv_dtype, "grouped heads")
+
+
+def test_empty_and_negative_entries(cuda):
+    """seq_len 0 -> zero row; a negative table entry inside the context is
+    skipped (never dereferenced), as in the oracle."""
+    wl = W.small_case(num_seqs=4, H=8, KVH=2, D=128, kv_dtype=W.FP16, seed=55,
+                      lens=[0, 40, 100, 64])
+    wl.block_tables[2, 2] = -1
+    got = run_gpu(wl)
+    assert (got[0] == 0).all()
+    assert_close(got, oracle(wl), wl.kv_dtype, "negative entries")
+
+
+def test_padded_strides(cuda):
+    """Non-default kv_block_stride / kv_head_stride are honoured."""
+    import torch
+    wl = W.small_case(num_seqs=3, H=8, KVH=2, D=64, kv_dtype=W.FP16, seed=66, max_len=250)
+    pad_head, pad_block = 8 * 64, 3 * 64
+    nb, KVH, bs, D = wl.key_cache.shape
+    hs = bs * D + pad_head
+    bsd = KVH * hs + pad_block
+    def padded(a):
+        buf = np.full(nb * bsd, 0x7E00, dtype=np.uint16)  # NaN filler
+        for h in range(KVH):
+            for b in range(nb):
+                buf[b * bsd + h * hs:b * bsd + h * hs + bs * D] = a[b, h].reshape(-1)
+        return buf
+    dw = W.upload(wl)
+    dw.key_cache = W.to_torch(padded(wl.key_cache), wl.kv_dtype)
+    dw.value_cache = W.to_torch(padded(wl.value_cache), wl.kv_dtype)
+    got = run_gpu(wl, tensors=dw, kv_block_stride=bsd, kv_head_stride=hs,
+                  max_num_blocks_per_seq=wl.max_num_blocks_per_seq)
+    assert_close(got, oracle(wl), wl.kv_dtype, "padded strides")
+    del torch
+
+
+# ---------------------------------------------------- benchmark configs
+def test_config1_full(cuda):
+    wl = W.config1()
+    assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, "config1")
+
+
+def test_config2_full(cuda):
+    wl = W.config2()
+    stats = assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, "config2")
+    print("config2", stats)
+
+
+def test_config3_long_context(cuda):
+    wl = W.config3()
+    stats = assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, "config3")
+    print("config3", stats)
+
+
+@pytest.mark.parametrize("kvh", [8, 4])
+def test_config4_bf16(cuda, kvh):
+    wl = W.config4(num_kv_heads=kvh, num_seqs=32)
+    stats = assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"config4 kvh={kvh}")
+    print("config4", kvh, stats)
+
+
+def test_config5_shared_prefix(cuda):
+    wl = W.config5()
+    stats = assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, "config5")
+    print("config5", stats)
+
+
+# ------------------------------------------------------ error handling
+def test_unsupported_shapes_leave_output_untouched(cuda):
+    import torch
+    wl = W.small_case(num_seqs=2, H=8, KVH=2, D=128, kv_dtype=W.FP16, seed=77, max_len=64)
+    dw = W.upload(wl)
+    sentinel = dw.out.clone()
+    lib = PA._lib.backend()
+    import ctypes
+    base = [dw.out.data_ptr(), dw.query.data_ptr(), dw.key_cache.data_ptr(),
+            dw.value_cache.data_ptr(), dw.block_tables.data_ptr(), dw.seq_lens.data_ptr()]
+    def call(**kw):
+        a = dict(num_seqs=2, num_heads=8, head_size=128, num_kv_heads=2, scale=0.1,
+                 maxb=wl.max_num_blocks_per_seq, bs=16, dtype_size=2, kbs=wl.kv_block_stride,
+                 khs=wl.kv_head_stride)
+        a.update(kw)
+        lib.nxt_paged_attention(*base, a["num_seqs"], a["num_heads"], a["head_size"],
+                                a["num_kv_heads"], ctypes.c_float(a["scale"]), a["maxb"], a["bs"],
+                                a["dtype_size"], a["kbs"], a["khs"],
+                                torch.cuda.current_stream().cuda_stream)
+        return lib.nxt_attn_last_status()
+    assert call(head_size=100) == PA.NXT_ATTN_E_UNSUPPORTED
+    assert call(dtype_size=3) == PA.NXT_ATTN_E_UNSUPPORTED
+    assert call(num_heads=7) == PA.NXT_ATTN_E_INVALID
+    assert call(bs=12) == PA.NXT_ATTN_E_UNSUPPORTED
+    assert call(kbs=wl.kv_block_stride + 3) == PA.NXT_ATTN_E_UNSUPPORTED
+    assert call(num_seqs=-1) == PA.NXT_ATTN_E_INVALID
+    torch.cuda.synchronize()
+    assert torch.equal(dw.out.view(torch.int16), sentinel.view(torch.int16))
+    assert call() == PA.NXT_ATTN_OK
+    assert call(num_seqs=0) == PA.NXT_ATTN_OK

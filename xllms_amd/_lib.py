@@ -1,0 +1,106 @@
+"""Locate and load the native libraries of this package (ctypes).
+
+The product path is libxllm_hip_backend.so: the gfx950 kernels plus the
+reference-compatible C-ABI.  There is no fallback: if the library is missing
+every entry point raises, so nothing can silently compute on the CPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(_HERE, "lib")
+BACKEND_SO = os.path.join(LIB_DIR, "libxllm_hip_backend.so")
+WORKLOAD_SO = os.path.join(LIB_DIR, "libxllm_workload.so")
+
+_lock = threading.Lock()
+_cache: dict[str, ctypes.CDLL] = {}
+
+c_int = ctypes.c_int
+c_void_p = ctypes.c_void_p
+c_float = ctypes.c_float
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+def _load(path: str) -> ctypes.CDLL:
+    with _lock:
+        lib = _cache.get(path)
+        if lib is not None:
+            return lib
+        if not os.path.exists(path):
+            raise NativeLibraryMissing(
+                f"{path} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+                "or `make -C xllms_amd/csrc`")
+        lib = ctypes.CDLL(path, mode=os.RTLD_NOW | os.RTLD_LOCAL)
+        _cache[path] = lib
+        return lib
+
+
+# Exported symbols of libxllm_hip_backend.so, exactly the declarations of
+# include/xllm_hip_operator_api.h and include/xllm_hip_backend.h.
+OPERATOR_SYMBOLS = (
+    "nxt_paged_attention",
+    "nxt_paged_attention_v2",
+    "nxt_paged_attention_flash",
+    "nxt_paged_attention_ex",
+    "nxt_paged_attention_auto_partition",
+    "nxt_attn_last_status",
+    "nxt_attn_last_error",
+    "nxt_attn_release_workspaces",
+    "nxt_attn_version",
+)
+PLUGIN_SYMBOLS = ("nxt_backend_init", "nxt_backend_run", "nxt_backend_fini", "nxt_backend_run_ex")
+
+_LEGACY_ARGS = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                c_int, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_int, c_void_p]
+
+
+def backend() -> ctypes.CDLL:
+    lib = _load(BACKEND_SO)
+    if not getattr(lib, "_xllm_typed", False):
+        for name in ("nxt_paged_attention", "nxt_paged_attention_v2", "nxt_paged_attention_flash"):
+            fn = getattr(lib, name)
+            fn.argtypes = _LEGACY_ARGS
+            fn.restype = None
+        lib.nxt_paged_attention_ex.argtypes = _LEGACY_ARGS + [c_int, c_int]
+        lib.nxt_paged_attention_ex.restype = c_int
+        lib.nxt_paged_attention_auto_partition.argtypes = [c_int] * 7
+        lib.nxt_paged_attention_auto_partition.restype = c_int
+        lib.nxt_attn_last_status.argtypes = []
+        lib.nxt_attn_last_status.restype = c_int
+        lib.nxt_attn_last_error.argtypes = []
+        lib.nxt_attn_last_error.restype = ctypes.c_char_p
+        lib.nxt_attn_release_workspaces.argtypes = []
+        lib.nxt_attn_release_workspaces.restype = c_int
+        lib.nxt_attn_version.argtypes = []
+        lib.nxt_attn_version.restype = ctypes.c_char_p
+        lib._xllm_typed = True
+    return lib
+
+
+def workload() -> ctypes.CDLL:
+    lib = _load(WORKLOAD_SO)
+    if not getattr(lib, "_xllm_typed", False):
+        u64 = ctypes.c_uint64
+        lib.xw_fill_normal.argtypes = [c_void_p, ctypes.c_size_t, c_int, u64, u64, c_float, c_int]
+        lib.xw_fill_normal.restype = None
+        lib.xw_scale_rows.argtypes = [c_void_p, c_void_p, ctypes.c_size_t, ctypes.c_size_t, c_int,
+                                      u64, u64, c_float, c_int]
+        lib.xw_scale_rows.restype = None
+        lib.xw_normal.argtypes = [u64, u64]
+        lib.xw_normal.restype = c_float
+        lib.xw_uniform_u64.argtypes = [u64, u64]
+        lib.xw_uniform_u64.restype = u64
+        lib.xw_float_to_half.argtypes = [c_float]
+        lib.xw_float_to_half.restype = ctypes.c_uint16
+        lib.xw_float_to_bf16.argtypes = [c_float]
+        lib.xw_float_to_bf16.restype = ctypes.c_uint16
+        lib.xw_num_threads.argtypes = []
+        lib.xw_num_threads.restype = c_int
+        lib._xllm_typed = True
+    return lib

@@ -1,0 +1,423 @@
+// C-ABI of the paged-decode attention: argument validation, the split-K plan,
+// per-(device, stream) workspace, and the launch of the gfx950 kernels.
+//
+// Entry points replace include/operator_api.h:63-115 of the reference (see
+// include/xllm_hip_operator_api.h for the contract).  Host-side only; the
+// kernels live in paged_decode_{f16,bf16,f32}.hip.
+#include <hip/hip_runtime_api.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "paged_decode_launch.h"
+#include "paged_decode_params.h"
+#include "xllm_hip_operator_api.h"
+
+namespace {
+
+using xhip::DecodeParams;
+
+thread_local int t_status = NXT_ATTN_OK;
+thread_local char t_message[512] = "ok";
+
+int set_status(int status, const char *fmt, ...) {
+    t_status = status;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(t_message, sizeof(t_message), fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int ok() {
+    t_status = NXT_ATTN_OK;
+    snprintf(t_message, sizeof(t_message), "ok");
+    return NXT_ATTN_OK;
+}
+
+// ---------------------------------------------------------------- workspace
+struct Workspace {
+    int device;
+    hipStream_t stream;
+    void *ptr;
+    size_t bytes;
+};
+
+std::mutex g_ws_mu;
+std::vector<Workspace> g_ws;
+
+// Returns a workspace of at least `bytes` for (device, stream).  Growing one
+// waits for the stream first, so no kernel still in flight on it can touch
+// the old buffer.
+int get_workspace(int device, hipStream_t stream, size_t bytes, void **out) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    for (Workspace &w : g_ws) {
+        if (w.device != device || w.stream != stream) continue;
+        if (w.bytes >= bytes) {
+            *out = w.ptr;
+            return NXT_ATTN_OK;
+        }
+        hipError_t e = hipStreamSynchronize(stream);
+        if (e != hipSuccess)
+            return set_status(NXT_ATTN_E_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+        (void)hipFree(w.ptr);
+        w.ptr = nullptr;
+        w.bytes = 0;
+        e = hipMalloc(&w.ptr, bytes);
+        if (e != hipSuccess) {
+            w.ptr = nullptr;
+            return set_status(NXT_ATTN_E_NOMEM, "split-K workspace of %zu bytes: %s", bytes,
+                              hipGetErrorString(e));
+        }
+        w.bytes = bytes;
+        *out = w.ptr;
+        return NXT_ATTN_OK;
+    }
+    Workspace w{device, stream, nullptr, 0};
+    hipError_t e = hipMalloc(&w.ptr, bytes);
+    if (e != hipSuccess)
+        return set_status(NXT_ATTN_E_NOMEM, "split-K workspace of %zu bytes: %s", bytes,
+                          hipGetErrorString(e));
+    w.bytes = bytes;
+    g_ws.push_back(w);
+    *out = w.ptr;
+    return NXT_ATTN_OK;
+}
+
+// ------------------------------------------------------------- device info
+constexpr int kMaxDevices = 64;
+std::mutex g_dev_mu;
+int g_cu_count[kMaxDevices];
+
+int cu_count(int device) {
+    if (device < 0 || device >= kMaxDevices) return 256;
+    std::lock_guard<std::mutex> lock(g_dev_mu);
+    if (g_cu_count[device] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        g_cu_count[device] = n;
+    }
+    return g_cu_count[device];
+}
+
+// ---------------------------------------------------------------- geometry
+bool supported_head_size(int d) {
+    switch (d) {
+    case 32: case 64: case 80: case 96: case 112: case 128: case 192: case 256: return true;
+    default: return false;
+    }
+}
+
+int pow2_ceil(int x) {
+    int r = 1;
+    while (r < x) r <<= 1;
+    return r;
+}
+
+bool is_pow2(long long x) { return x > 0 && (x & (x - 1)) == 0; }
+
+int ilog2(int x) {
+    int r = 0;
+    while ((1 << r) < x) r++;
+    return r;
+}
+
+int elem_bytes(int kv_dtype) { return kv_dtype == NXT_KV_FP32 ? 4 : 2; }
+
+// Tokens per tile of the kernel instantiation (kLoadsPerTile loads of
+// 64/lanes-per-row rows); mirrors xhip::Geometry.
+int tile_tokens(int head_size, int kv_dtype) {
+    const int vec = 16 / elem_bytes(kv_dtype);
+    const int row_lanes = pow2_ceil(head_size / vec);
+    return (64 / row_lanes) * xhip::kLoadsPerTile;
+}
+
+struct HeadTiling {
+    int head_tile;   // query heads per wavefront
+    int head_tiles;  // wavefronts per (seq, kv head, partition)
+};
+
+bool head_tiling(int group, HeadTiling *t) {
+    if (group <= 0) return false;
+    if (group <= xhip::kMaxHeadTile) {
+        t->head_tile = pow2_ceil(group);
+        t->head_tiles = 1;
+        return true;
+    }
+    t->head_tile = xhip::kMaxHeadTile;
+    t->head_tiles = pow2_ceil((group + xhip::kMaxHeadTile - 1) / xhip::kMaxHeadTile);
+    return t->head_tiles <= xhip::kWavesPerGroup;
+}
+
+// Automatic partition length: enough wavefront items to give every CU
+// kItemsPerCu of them, assuming sequences use about half of their block table
+// on average; a power of two in [max(tile, 64), 1024].
+constexpr int kItemsPerCu = 16;
+
+int auto_partition(int num_seqs, int num_kv_heads, int head_tiles, long long max_ctx, int tile,
+                   int cus) {
+    const long long pairs = (long long)num_seqs * num_kv_heads * head_tiles;
+    const long long mean_ctx = max_ctx / 2 > 0 ? max_ctx / 2 : 1;
+    const long long want_items = (long long)cus * kItemsPerCu;
+    long long c = (pairs * mean_ctx + want_items - 1) / want_items;
+    int lo = tile > 64 ? tile : 64;
+    int part = lo;
+    while (part < c && part < 1024) part <<= 1;
+    return part;
+}
+
+constexpr int kMaxParts = 16384;  // reduce kernel stages one float per partition in LDS
+
+const char *dtype_name(int kv_dtype) {
+    switch (kv_dtype) {
+    case NXT_KV_FP16: return "fp16";
+    case NXT_KV_BF16: return "bf16";
+    case NXT_KV_FP32: return "fp32";
+    default: return "?";
+    }
+}
+
+int run(void *out, const void *query, const void *key_cache, const void *value_cache,
+        const int *block_tables, const int *seq_lens, int num_seqs, int num_heads, int head_size,
+        int num_kv_heads, float scale, int max_num_blocks_per_seq, int block_size, int dtype_size,
+        int kv_block_stride, int kv_head_stride, nxt_stream_t stream_handle, int kv_dtype,
+        int partition_tokens) {
+    // ---- argument checks (host only; nothing is read from the device)
+    if (kv_dtype != NXT_KV_FP16 && kv_dtype != NXT_KV_BF16 && kv_dtype != NXT_KV_FP32)
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "kv_dtype %d is not FP16/BF16/FP32", kv_dtype);
+    if (dtype_size != elem_bytes(kv_dtype))
+        return set_status(NXT_ATTN_E_INVALID, "dtype_size %d does not match %s", dtype_size,
+                          dtype_name(kv_dtype));
+    if (num_seqs < 0) return set_status(NXT_ATTN_E_INVALID, "num_seqs %d < 0", num_seqs);
+    if (num_heads <= 0 || num_kv_heads <= 0)
+        return set_status(NXT_ATTN_E_INVALID, "num_heads %d / num_kv_heads %d must be > 0",
+                          num_heads, num_kv_heads);
+    if (num_heads % num_kv_heads)
+        return set_status(NXT_ATTN_E_INVALID, "num_heads %d is not a multiple of num_kv_heads %d",
+                          num_heads, num_kv_heads);
+    if (!supported_head_size(head_size))
+        return set_status(NXT_ATTN_E_UNSUPPORTED,
+                          "head_size %d not in {32,64,80,96,112,128,192,256}", head_size);
+    if (max_num_blocks_per_seq <= 0)
+        return set_status(NXT_ATTN_E_INVALID, "max_num_blocks_per_seq %d must be > 0",
+                          max_num_blocks_per_seq);
+    if (block_size <= 0) return set_status(NXT_ATTN_E_INVALID, "block_size %d", block_size);
+    if (!is_pow2(block_size) || block_size > 1024)
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "block_size %d is not a power of two <= 1024",
+                          block_size);
+    if (kv_block_stride < 0 || kv_head_stride < 0)
+        return set_status(NXT_ATTN_E_INVALID, "negative kv stride (%d, %d)", kv_block_stride,
+                          kv_head_stride);
+    if (!isfinite(scale)) return set_status(NXT_ATTN_E_INVALID, "scale is not finite");
+    const long long max_ctx = (long long)max_num_blocks_per_seq * block_size;
+    if (max_ctx > (1LL << 30))
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "context bound %lld tokens too large", max_ctx);
+    const int group = num_heads / num_kv_heads;
+    HeadTiling tiling;
+    if (!head_tiling(group, &tiling))
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "GQA group %d > %d", group,
+                          xhip::kMaxHeadTile * xhip::kWavesPerGroup);
+    if (num_seqs == 0) return ok();
+    if (!out || !query || !key_cache || !value_cache || !block_tables || !seq_lens)
+        return set_status(NXT_ATTN_E_INVALID, "NULL tensor pointer");
+    const int eb = elem_bytes(kv_dtype);
+    if (((uintptr_t)out | (uintptr_t)query | (uintptr_t)key_cache | (uintptr_t)value_cache) & 15)
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "tensors must be 16-byte aligned");
+    if ((((long long)kv_block_stride * eb) & 15) || (((long long)kv_head_stride * eb) & 15))
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "kv strides must be multiples of 16 bytes");
+    if ((uintptr_t)block_tables & 3 || (uintptr_t)seq_lens & 3)
+        return set_status(NXT_ATTN_E_INVALID, "int32 tables must be 4-byte aligned");
+
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return set_status(NXT_ATTN_E_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    hipStream_t stream = (hipStream_t)stream_handle;
+
+    // ---- split-K plan
+    const int tile = tile_tokens(head_size, kv_dtype);
+    int part = partition_tokens;
+    if (part == 0) {
+        part = auto_partition(num_seqs, num_kv_heads, tiling.head_tiles, max_ctx, tile,
+                              cu_count(device));
+    } else if (!is_pow2(part) || part < tile) {
+        return set_status(NXT_ATTN_E_UNSUPPORTED,
+                          "partition_tokens %d must be a power of two >= %d for head_size %d %s",
+                          partition_tokens, tile, head_size, dtype_name(kv_dtype));
+    }
+    long long max_parts = (max_ctx + part - 1) / part;
+    if (max_parts > kMaxParts)
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "%lld partitions exceed %d; raise partition_tokens",
+                          max_parts, kMaxParts);
+    const long long items = (long long)num_seqs * num_kv_heads * tiling.head_tiles * max_parts;
+    const long long grid = (items + xhip::kWavesPerGroup - 1) / xhip::kWavesPerGroup;
+    if (items > 0x7FFFFFFFLL || grid > 0x7FFFFFFFLL)
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "work grid of %lld items too large", items);
+    if (num_seqs > 65535 || num_heads > 65535)
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "num_seqs/num_heads above 65535");
+
+    DecodeParams p;
+    memset(&p, 0, sizeof(p));
+    p.out = out;
+    p.q = query;
+    p.k = key_cache;
+    p.v = value_cache;
+    p.block_tables = block_tables;
+    p.seq_lens = seq_lens;
+    p.kv_block_stride = kv_block_stride;
+    p.kv_head_stride = kv_head_stride;
+    p.num_seqs = num_seqs;
+    p.num_heads = num_heads;
+    p.num_kv_heads = num_kv_heads;
+    p.group = group;
+    p.head_tiles = tiling.head_tiles;
+    p.max_blocks = max_num_blocks_per_seq;
+    p.block_size = block_size;
+    p.bs_shift = ilog2(block_size);
+    p.part_tokens = part;
+    p.max_parts = (int)max_parts;
+    p.max_ctx = (int)max_ctx;
+    p.scale_log2 = scale * 1.4426950408889634f;
+
+    const bool reduce = max_parts > 1;
+    if (reduce) {
+        const size_t rows = (size_t)num_seqs * num_heads * (size_t)max_parts;
+        const size_t o_bytes = (rows * head_size * sizeof(float) + 255) & ~(size_t)255;
+        const size_t bytes = o_bytes + rows * 2 * sizeof(float);
+        void *ws = nullptr;
+        int st = get_workspace(device, stream, bytes, &ws);
+        if (st != NXT_ATTN_OK) return st;
+        p.ws_o = (float *)ws;
+        p.ws_ml = (float *)((char *)ws + o_bytes);
+    }
+
+    switch (kv_dtype) {
+    case NXT_KV_FP16:
+        e = xhip::launch_decode_f16(p, head_size, tiling.head_tile, (unsigned)grid, reduce, stream);
+        break;
+    case NXT_KV_BF16:
+        e = xhip::launch_decode_bf16(p, head_size, tiling.head_tile, (unsigned)grid, reduce, stream);
+        break;
+    default:
+        e = xhip::launch_decode_f32(p, head_size, tiling.head_tile, (unsigned)grid, reduce, stream);
+        break;
+    }
+    if (e != hipSuccess)
+        return set_status(NXT_ATTN_E_HIP, "kernel launch: %s", hipGetErrorString(e));
+    return ok();
+}
+
+int dtype_from_size(int dtype_size) {
+    if (dtype_size == 2) return NXT_KV_FP16;
+    if (dtype_size == 4) return NXT_KV_FP32;
+    return 0;
+}
+
+void run_legacy(void *out, const void *query, const void *key_cache, const void *value_cache,
+                const int *block_tables, const int *seq_lens, int num_seqs, int num_heads,
+                int head_size, int num_kv_heads, float scale, int max_num_blocks_per_seq,
+                int block_size, int dtype_size, int kv_block_stride, int kv_head_stride,
+                nxt_stream_t stream) {
+    const int kv_dtype = dtype_from_size(dtype_size);
+    if (!kv_dtype) {
+        set_status(NXT_ATTN_E_UNSUPPORTED, "dtype_size %d is not 2 (fp16) or 4 (fp32)", dtype_size);
+        return;
+    }
+    (void)run(out, query, key_cache, value_cache, block_tables, seq_lens, num_seqs, num_heads,
+              head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size, dtype_size,
+              kv_block_stride, kv_head_stride, stream, kv_dtype, 0);
+}
+
+}  // namespace
+
+extern "C" {
+
+__attribute__((visibility("default"))) void nxt_paged_attention(
+    void *out, const void *query, const void *key_cache, const void *value_cache,
+    const int *block_tables, const int *seq_lens, int num_seqs, int num_heads, int head_size,
+    int num_kv_heads, float scale, int max_num_blocks_per_seq, int block_size, int dtype_size,
+    int kv_block_stride, int kv_head_stride, nxt_stream_t stream) {
+    run_legacy(out, query, key_cache, value_cache, block_tables, seq_lens, num_seqs, num_heads,
+               head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size, dtype_size,
+               kv_block_stride, kv_head_stride, stream);
+}
+
+__attribute__((visibility("default"))) void nxt_paged_attention_v2(
+    void *out, const void *query, const void *key_cache, const void *value_cache,
+    const int *block_tables, const int *seq_lens, int num_seqs, int num_heads, int head_size,
+    int num_kv_heads, float scale, int max_num_blocks_per_seq, int block_size, int dtype_size,
+    int kv_block_stride, int kv_head_stride, nxt_stream_t stream) {
+    run_legacy(out, query, key_cache, value_cache, block_tables, seq_lens, num_seqs, num_heads,
+               head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size, dtype_size,
+               kv_block_stride, kv_head_stride, stream);
+}
+
+__attribute__((visibility("default"))) void nxt_paged_attention_flash(
+    void *out, const void *query, const void *key_cache, const void *value_cache,
+    const int *block_tables, const int *seq_lens, int num_seqs, int num_heads, int head_size,
+    int num_kv_heads, float scale, int max_num_blocks_per_seq, int block_size, int dtype_size,
+    int kv_block_stride, int kv_head_stride, nxt_stream_t stream) {
+    run_legacy(out, query, key_cache, value_cache, block_tables, seq_lens, num_seqs, num_heads,
+               head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size, dtype_size,
+               kv_block_stride, kv_head_stride, stream);
+}
+
+__attribute__((visibility("default"))) int nxt_paged_attention_ex(
+    void *out, const void *query, const void *key_cache, const void *value_cache,
+    const int *block_tables, const int *seq_lens, int num_seqs, int num_heads, int head_size,
+    int num_kv_heads, float scale, int max_num_blocks_per_seq, int block_size, int dtype_size,
+    int kv_block_stride, int kv_head_stride, nxt_stream_t stream, int kv_dtype,
+    int partition_tokens) {
+    return run(out, query, key_cache, value_cache, block_tables, seq_lens, num_seqs, num_heads,
+               head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size, dtype_size,
+               kv_block_stride, kv_head_stride, stream, kv_dtype, partition_tokens);
+}
+
+__attribute__((visibility("default"))) int nxt_paged_attention_auto_partition(
+    int num_seqs, int num_heads, int head_size, int num_kv_heads, int max_num_blocks_per_seq,
+    int block_size, int kv_dtype) {
+    if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads ||
+        !supported_head_size(head_size) || max_num_blocks_per_seq <= 0 || block_size <= 0 ||
+        (kv_dtype != NXT_KV_FP16 && kv_dtype != NXT_KV_BF16 && kv_dtype != NXT_KV_FP32))
+        return NXT_ATTN_E_INVALID;
+    HeadTiling tiling;
+    if (!head_tiling(num_heads / num_kv_heads, &tiling)) return NXT_ATTN_E_UNSUPPORTED;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return NXT_ATTN_E_HIP;
+    return auto_partition(num_seqs, num_kv_heads, tiling.head_tiles,
+                          (long long)max_num_blocks_per_seq * block_size,
+                          tile_tokens(head_size, kv_dtype), cu_count(device));
+}
+
+__attribute__((visibility("default"))) int nxt_attn_last_status(void) { return t_status; }
+
+__attribute__((visibility("default"))) const char *nxt_attn_last_error(void) { return t_message; }
+
+__attribute__((visibility("default"))) int nxt_attn_release_workspaces(void) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    int rc = NXT_ATTN_OK;
+    for (Workspace &w : g_ws) {
+        int cur = 0;
+        if (hipGetDevice(&cur) == hipSuccess && hipSetDevice(w.device) == hipSuccess) {
+            if (hipDeviceSynchronize() != hipSuccess) rc = NXT_ATTN_E_HIP;
+            if (hipFree(w.ptr) != hipSuccess) rc = NXT_ATTN_E_HIP;
+            (void)hipSetDevice(cur);
+        } else {
+            rc = NXT_ATTN_E_HIP;
+        }
+    }
+    g_ws.clear();
+    return rc;
+}
+
+__attribute__((visibility("default"))) const char *nxt_attn_version(void) {
+    return "xllm-hip-attn 0.1.0 gfx950";
+}
+
+}  // extern "C"

@@ -1,0 +1,509 @@
+// gfx950 (CDNA4) kernels of the paged-decode attention.
+//
+// Memory-bound by design: every K/V byte of a (sequence, kv head) is read
+// once, with 16-byte per-lane global loads that cover whole rows of a page,
+// and the whole GQA group of query heads is served from that one read.
+//
+// Wavefront layout (wave64).  A K or V row of one token is head_size elements,
+// i.e. NCH = head_size*elem_bytes/16 sixteen-byte chunks.  RL = next pow2 of
+// NCH lanes share a row (lane `col` owns chunk col), and the wavefront holds
+// TPL = 64/RL rows per load instruction, so one instruction reads TPL whole
+// contiguous rows.  A tile is kLoadsPerTile such loads (TT = 4*TPL tokens; 16
+// tokens = one 16-token page for fp16/bf16 d=128).  Each row group of lanes
+// (the RL lanes of one `row`) keeps its own online-softmax state (running max
+// m, running sum l, unnormalised output o) for every query head of the head
+// tile, so the main loop needs no cross-row traffic at all: QK^T is a per-lane
+// dot product (v_dot2_f32_f16 / v_dot2_f32_bf16 for 16-bit data, FMA for fp32)
+// finished by a DPP butterfly inside the row (quad_perm, row_half_mirror,
+// row_mirror), the softmax update is per lane, and PV is per-lane FMAs into the
+// lane's own output columns.  The row states are merged once, at the end of
+// the partition, with xor shuffles.
+//
+// Split-K.  A sequence's tokens are cut into partitions of part_tokens; each
+// (sequence, kv head, head tile, partition) is one wavefront work item.  A
+// sequence with one partition writes its output directly; otherwise every
+// partition writes (m, l, o) in fp32 to the workspace and
+// paged_decode_reduce_kernel merges them with the usual log-sum-exp rescale:
+//   M = max_p m_p,  O = sum_p 2^(m_p-M) o_p / sum_p 2^(m_p-M) l_p.
+// Scores are kept in log2 units (scale*log2(e) folded into the score) so the
+// exponentials are single v_exp_f32 instructions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "paged_decode_params.h"
+
+namespace xhip {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+template <int KV> struct KvTraits;
+template <> struct KvTraits<KV_F16> { static constexpr int kBytes = 2; };
+template <> struct KvTraits<KV_BF16> { static constexpr int kBytes = 2; };
+template <> struct KvTraits<KV_F32> { static constexpr int kBytes = 4; };
+
+constexpr int pow2_ceil(int x) {
+    int r = 1;
+    while (r < x) r <<= 1;
+    return r;
+}
+
+// Compile-time geometry of one (dtype, head_size) instantiation.
+template <int KV, int D> struct Geometry {
+    static constexpr int kElemBytes = KvTraits<KV>::kBytes;
+    static constexpr int kVec = 16 / kElemBytes;           // elements per lane chunk
+    static constexpr int kChunks = D / kVec;               // chunks per row
+    static constexpr int kRowLanes = pow2_ceil(kChunks);   // lanes per row
+    static constexpr int kRows = 64 / kRowLanes;           // rows per load
+    static constexpr int kTileTokens = kRows * kLoadsPerTile;
+    static_assert(D % kVec == 0, "head_size must fill whole 16-byte chunks");
+    static_assert(kRowLanes <= 64, "row wider than a wavefront");
+};
+
+template <int CTRL> __device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the RL lanes of a row (RL a power of two), result in every lane,
+// for N independent values at once: each butterfly step is applied to all N
+// before the next, so consecutive DPP instructions never read a register the
+// previous instruction wrote (no DPP read-after-write stall).
+template <int RL, int N> __device__ __forceinline__ void row_sum_n(float (&v)[N]) {
+    if constexpr (RL >= 2) {
+#pragma unroll
+        for (int i = 0; i < N; i++) v[i] += dpp_mov<0xB1>(v[i]);  // quad_perm [1,0,3,2]: lane ^ 1
+    }
+    if constexpr (RL >= 4) {
+#pragma unroll
+        for (int i = 0; i < N; i++) v[i] += dpp_mov<0x4E>(v[i]);  // quad_perm [2,3,0,1]: lane ^ 2
+    }
+    if constexpr (RL >= 8) {
+#pragma unroll
+        for (int i = 0; i < N; i++) v[i] += dpp_mov<0x141>(v[i]); // row_half_mirror: other quad
+    }
+    if constexpr (RL >= 16) {
+#pragma unroll
+        for (int i = 0; i < N; i++) v[i] += dpp_mov<0x140>(v[i]); // row_mirror: other half row
+    }
+    if constexpr (RL >= 32) {
+#pragma unroll
+        for (int i = 0; i < N; i++) v[i] += __shfl_xor(v[i], 16);
+    }
+    if constexpr (RL >= 64) {
+#pragma unroll
+        for (int i = 0; i < N; i++) v[i] += __shfl_xor(v[i], 32);
+    }
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Element i of a 16-byte chunk, by value.  (__builtin_bit_cast applied
+// directly to a subscripted ext_vector element reads element 0 whatever i
+// is, so every reinterpretation below goes through this copy.)
+__device__ __forceinline__ uint32_t lane_word(u32x4 v, int i) {
+    const uint32_t w = v[i];
+    return w;
+}
+
+// acc + <k chunk, q chunk> over one 16-byte chunk.
+template <int KV> __device__ __forceinline__ float chunk_dot(u32x4 k, u32x4 q, float acc) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if constexpr (KV == KV_F16)
+            acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, lane_word(k, i)),
+                                         __builtin_bit_cast(f16x2, lane_word(q, i)), acc, false);
+        else if constexpr (KV == KV_BF16)
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, lane_word(k, i)),
+                                                  __builtin_bit_cast(bf16x2, lane_word(q, i)), acc,
+                                                  false);
+        else
+            acc = fmaf(__builtin_bit_cast(float, lane_word(k, i)),
+                       __builtin_bit_cast(float, lane_word(q, i)), acc);
+    }
+    return acc;
+}
+
+// Widen one 16-byte chunk to fp32 (exact for every dtype).
+template <int KV, int VEC>
+__device__ __forceinline__ void chunk_to_float(u32x4 v, float (&f)[VEC]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if constexpr (KV == KV_F16) {
+            f16x2 h = __builtin_bit_cast(f16x2, lane_word(v, i));
+            f[2 * i] = (float)h.x;
+            f[2 * i + 1] = (float)h.y;
+        } else if constexpr (KV == KV_BF16) {
+            const uint32_t w = lane_word(v, i);
+            f[2 * i] = __builtin_bit_cast(float, w << 16);
+            f[2 * i + 1] = __builtin_bit_cast(float, w & 0xFFFF0000u);
+        } else {
+            f[i] = __builtin_bit_cast(float, lane_word(v, i));
+        }
+    }
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN stays NaN).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
+    uint32_t u = __builtin_bit_cast(uint32_t, x);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Narrow VEC fp32 values to one 16-byte chunk of the element type (RNE).
+template <int KV, int VEC> __device__ __forceinline__ u32x4 float_to_chunk(const float (&f)[VEC]) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if constexpr (KV == KV_F16) {
+            f16x2 h;
+            h.x = (_Float16)f[2 * i];
+            h.y = (_Float16)f[2 * i + 1];
+            r[i] = __builtin_bit_cast(uint32_t, h);
+        } else if constexpr (KV == KV_BF16) {
+            r[i] = f32_to_bf16_bits(f[2 * i]) | (f32_to_bf16_bits(f[2 * i + 1]) << 16);
+        } else {
+            r[i] = __builtin_bit_cast(uint32_t, f[i]);
+        }
+    }
+    return r;
+}
+
+template <int KV> __device__ __forceinline__ void store_elem(void *base, size_t idx, float x) {
+    if constexpr (KV == KV_F16)
+        ((_Float16 *)base)[idx] = (_Float16)x;
+    else if constexpr (KV == KV_BF16)
+        ((uint16_t *)base)[idx] = (uint16_t)f32_to_bf16_bits(x);
+    else
+        ((float *)base)[idx] = x;
+}
+
+__device__ __forceinline__ u32x4 load16(const char *p) { return *(const u32x4 *)p; }
+
+// Per-wavefront state of one work item.
+template <int KV, int D, int GT> struct ItemState {
+    static constexpr int VEC = Geometry<KV, D>::kVec;
+    u32x4 q[GT];
+    float m[GT];     // running max, log2 units
+    float l[GT];     // running sum of 2^(s - m)
+    float o[GT][VEC];
+};
+
+// One tile: kLoadsPerTile loads of TPL rows each.  UNI: the TPL rows of every
+// load sit in one page (block_size >= TPL), whose id blk[k] was read with a
+// scalar load.  MASK: some token of the tile is past t_end or in a page with a
+// negative id; such tokens are neither loaded nor counted.
+template <int KV, int D, int GT, bool UNI, bool MASK>
+__device__ __forceinline__ void decode_tile(const DecodeParams &p, const int *bt, const char *kb,
+                                            const char *vb, int t0, int t_end, int row, int col,
+                                            bool col_ok, const int (&blk)[kLoadsPerTile],
+                                            ItemState<KV, D, GT> &st) {
+    using Geo = Geometry<KV, D>;
+    constexpr int VEC = Geo::kVec;
+    constexpr int EB = Geo::kElemBytes;
+    constexpr int RL = Geo::kRowLanes;
+    constexpr int TPL = Geo::kRows;
+    constexpr int LPT = kLoadsPerTile;
+    const int bmask = p.block_size - 1;
+
+    u32x4 kr[LPT], vr[LPT];
+    bool tv[LPT];
+    long long eoff[LPT];
+#pragma unroll
+    for (int k = 0; k < LPT; k++) {
+        const int tok = t0 + k * TPL + row;
+        if constexpr (UNI) {
+            const int tk0 = t0 + k * TPL;
+            tv[k] = !MASK || (tok < t_end && blk[k] >= 0);
+            eoff[k] = (long long)blk[k] * p.kv_block_stride +
+                      (long long)((((tk0 & bmask) + row) * D) + col * VEC);
+        } else {
+            const int bi = (tok < t_end ? tok : t_end - 1) >> p.bs_shift;
+            const int b = bt[bi];
+            tv[k] = tok < t_end && b >= 0;
+            eoff[k] = (long long)b * p.kv_block_stride + (long long)(((tok & bmask) * D) + col * VEC);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < LPT; k++) {
+        if ((!MASK || tv[k]) && col_ok)
+            kr[k] = load16(kb + eoff[k] * EB);
+        else
+            kr[k] = u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int k = 0; k < LPT; k++) {
+        if ((!MASK || tv[k]) && col_ok)
+            vr[k] = load16(vb + eoff[k] * EB);
+        else
+            vr[k] = u32x4{0, 0, 0, 0};
+    }
+
+    // Scores, log2 units: per-lane partial dots, then one interleaved row
+    // reduction over all LPT*GT of them.
+    float s[LPT][GT];
+    float part[LPT * GT];
+#pragma unroll
+    for (int k = 0; k < LPT; k++) {
+#pragma unroll
+        for (int g = 0; g < GT; g++) part[k * GT + g] = chunk_dot<KV>(kr[k], st.q[g], 0.0f);
+    }
+    row_sum_n<RL, LPT * GT>(part);
+#pragma unroll
+    for (int k = 0; k < LPT; k++) {
+#pragma unroll
+        for (int g = 0; g < GT; g++) {
+            const float acc = part[k * GT + g] * p.scale_log2;
+            s[k][g] = (MASK && !tv[k]) ? -INFINITY : acc;
+        }
+    }
+
+    // Online softmax update of this row's state.
+#pragma unroll
+    for (int g = 0; g < GT; g++) {
+        float mx = st.m[g];
+#pragma unroll
+        for (int k = 0; k < LPT; k++) mx = fmaxf(mx, s[k][g]);
+        const float ms = (mx == -INFINITY) ? 0.0f : mx;
+        const float alpha = fast_exp2(st.m[g] - ms);
+        float ps = 0.0f;
+#pragma unroll
+        for (int k = 0; k < LPT; k++) {
+            const float e = fast_exp2(s[k][g] - ms);
+            s[k][g] = e;
+            ps += e;
+        }
+        st.l[g] = st.l[g] * alpha + ps;
+        st.m[g] = mx;
+#pragma unroll
+        for (int e = 0; e < VEC; e++) st.o[g][e] *= alpha;
+    }
+
+    // o += p * V.
+#pragma unroll
+    for (int k = 0; k < LPT; k++) {
+        float vf[VEC];
+        chunk_to_float<KV, VEC>(vr[k], vf);
+#pragma unroll
+        for (int g = 0; g < GT; g++) {
+#pragma unroll
+            for (int e = 0; e < VEC; e++) st.o[g][e] = fmaf(s[k][g], vf[e], st.o[g][e]);
+        }
+    }
+}
+
+// Block ids of the kLoadsPerTile loads of the tile at t0 (UNI geometry):
+// indices are clamped to the last valid token so that a table entry past the
+// sequence is never read.
+template <int TPL>
+__device__ __forceinline__ void tile_blocks(const int *bt, int t0, int t_end, int bs_shift,
+                                            int (&blk)[kLoadsPerTile]) {
+#pragma unroll
+    for (int k = 0; k < kLoadsPerTile; k++) {
+        const int tk0 = t0 + k * TPL;
+        blk[k] = bt[(tk0 < t_end ? tk0 : t_end - 1) >> bs_shift];
+    }
+}
+
+template <int KV, int D, int GT, bool UNI>
+__device__ __forceinline__ void decode_partition(const DecodeParams &p, const int *bt,
+                                                 const char *kb, const char *vb, int t_begin,
+                                                 int t_end, int row, int col, bool col_ok,
+                                                 ItemState<KV, D, GT> &st) {
+    using Geo = Geometry<KV, D>;
+    constexpr int TPL = Geo::kRows;
+    constexpr int TT = Geo::kTileTokens;
+    constexpr int LPT = kLoadsPerTile;
+    int blk[LPT], nxt[LPT];
+    if constexpr (UNI) tile_blocks<TPL>(bt, t_begin, t_end, p.bs_shift, nxt);
+    for (int t0 = t_begin; t0 < t_end; t0 += TT) {
+        if constexpr (UNI) {
+            // Consume the ids fetched one tile ago, then fetch the next tile's
+            // so their latency hides behind this tile.
+            bool neg = false;
+#pragma unroll
+            for (int k = 0; k < LPT; k++) {
+                blk[k] = __builtin_amdgcn_readfirstlane(nxt[k]);
+                neg |= blk[k] < 0;
+            }
+            if (t0 + TT < t_end) tile_blocks<TPL>(bt, t0 + TT, t_end, p.bs_shift, nxt);
+            if (t0 + TT <= t_end && !neg)
+                decode_tile<KV, D, GT, true, false>(p, bt, kb, vb, t0, t_end, row, col, col_ok, blk, st);
+            else
+                decode_tile<KV, D, GT, true, true>(p, bt, kb, vb, t0, t_end, row, col, col_ok, blk, st);
+        } else {
+            decode_tile<KV, D, GT, false, true>(p, bt, kb, vb, t0, t_end, row, col, col_ok, blk, st);
+        }
+    }
+}
+
+// Main kernel: one wavefront per (sequence, kv head, head tile, partition).
+template <int KV, int D, int GT>
+__global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_kernel(
+    const DecodeParams p) {
+    using Geo = Geometry<KV, D>;
+    constexpr int VEC = Geo::kVec;
+    constexpr int EB = Geo::kElemBytes;
+    constexpr int NCH = Geo::kChunks;
+    constexpr int RL = Geo::kRowLanes;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    unsigned item = blockIdx.x * kWavesPerGroup + wave;
+    const int ht = item % p.head_tiles;
+    item /= p.head_tiles;
+    const int part = item % p.max_parts;
+    item /= p.max_parts;
+    const int kvh = item % p.num_kv_heads;
+    const int seq = item / p.num_kv_heads;
+    if (seq >= p.num_seqs) return;
+
+    int L = p.seq_lens[seq];
+    L = L < 0 ? 0 : (L > p.max_ctx ? p.max_ctx : L);
+    const int nparts = (L + p.part_tokens - 1) / p.part_tokens;
+    if (part >= (nparts > 0 ? nparts : 1)) return;
+
+    const int col = lane % RL;
+    const int row = lane / RL;
+    const bool col_ok = (NCH == RL) || (col < NCH);
+    const int g0 = ht * GT;
+    const int nh = min(GT, p.group - g0);
+    const size_t qrow0 = ((size_t)seq * p.num_heads + (size_t)kvh * p.group + g0) * D;
+
+    if (L == 0) {  // empty sequence: zero rows
+        if (row == 0 && col_ok) {
+#pragma unroll
+            for (int g = 0; g < GT; g++)
+                if (g < nh)
+                    *(u32x4 *)((char *)p.out + (qrow0 + (size_t)g * D + col * VEC) * EB) =
+                        u32x4{0, 0, 0, 0};
+        }
+        return;
+    }
+
+    ItemState<KV, D, GT> st;
+#pragma unroll
+    for (int g = 0; g < GT; g++) {
+        st.q[g] = (g < nh && col_ok)
+                      ? load16((const char *)p.q + (qrow0 + (size_t)g * D + col * VEC) * EB)
+                      : u32x4{0, 0, 0, 0};
+        st.m[g] = -INFINITY;
+        st.l[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < VEC; e++) st.o[g][e] = 0.0f;
+    }
+
+    const int t_begin = part * p.part_tokens;
+    const int t_end = min(L, t_begin + p.part_tokens);
+    const int *bt = p.block_tables + (size_t)seq * p.max_blocks;
+    const char *kb = (const char *)p.k + (size_t)kvh * (size_t)p.kv_head_stride * EB;
+    const char *vb = (const char *)p.v + (size_t)kvh * (size_t)p.kv_head_stride * EB;
+    if (p.block_size >= Geo::kRows)
+        decode_partition<KV, D, GT, true>(p, bt, kb, vb, t_begin, t_end, row, col, col_ok, st);
+    else
+        decode_partition<KV, D, GT, false>(p, bt, kb, vb, t_begin, t_end, row, col, col_ok, st);
+
+    // Merge the row states of the wavefront (rows differ in lane bits >= log2 RL).
+#pragma unroll
+    for (int off = RL; off < 64; off <<= 1) {
+#pragma unroll
+        for (int g = 0; g < GT; g++) {
+            const float mo = __shfl_xor(st.m[g], off);
+            const float lo = __shfl_xor(st.l[g], off);
+            const float M = fmaxf(st.m[g], mo);
+            const float Ms = (M == -INFINITY) ? 0.0f : M;
+            const float a = fast_exp2(st.m[g] - Ms);
+            const float b = fast_exp2(mo - Ms);
+            st.l[g] = st.l[g] * a + lo * b;
+            st.m[g] = M;
+#pragma unroll
+            for (int e = 0; e < VEC; e++)
+                st.o[g][e] = st.o[g][e] * a + __shfl_xor(st.o[g][e], off) * b;
+        }
+    }
+
+    if (row != 0 || !col_ok) return;
+    if (nparts == 1) {
+#pragma unroll
+        for (int g = 0; g < GT; g++) {
+            if (g >= nh) continue;
+            const float inv = st.l[g] > 0.0f ? 1.0f / st.l[g] : 0.0f;
+            float f[VEC];
+#pragma unroll
+            for (int e = 0; e < VEC; e++) f[e] = st.o[g][e] * inv;
+            *(u32x4 *)((char *)p.out + (qrow0 + (size_t)g * D + col * VEC) * EB) =
+                float_to_chunk<KV, VEC>(f);
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < GT; g++) {
+            if (g >= nh) continue;
+            const size_t pi =
+                ((size_t)seq * p.num_heads + (size_t)kvh * p.group + g0 + g) * p.max_parts + part;
+            float *dst = p.ws_o + pi * D + col * VEC;
+#pragma unroll
+            for (int e = 0; e < VEC; e += 4)
+                *(f32x4 *)(dst + e) = f32x4{st.o[g][e], st.o[g][e + 1], st.o[g][e + 2], st.o[g][e + 3]};
+            if (col == 0) {
+                p.ws_ml[2 * pi] = st.m[g];
+                p.ws_ml[2 * pi + 1] = st.l[g];
+            }
+        }
+    }
+}
+
+// Merge the partitions of one (sequence, query head).  One wavefront; the
+// per-partition weights 2^(m_p - M) are staged in LDS (max_parts floats).
+template <int KV, int D>
+__global__ __launch_bounds__(64) void paged_decode_reduce_kernel(const DecodeParams p) {
+    extern __shared__ float wsh[];
+    const int h = blockIdx.x;
+    const int seq = blockIdx.y;
+    const int lane = threadIdx.x;
+    int L = p.seq_lens[seq];
+    L = L < 0 ? 0 : (L > p.max_ctx ? p.max_ctx : L);
+    const int nparts = (L + p.part_tokens - 1) / p.part_tokens;
+    if (nparts < 2) return;
+
+    const size_t base = ((size_t)seq * p.num_heads + h) * p.max_parts;
+    const float *ml = p.ws_ml + 2 * base;
+    float M = -INFINITY;
+    for (int i = lane; i < nparts; i += 64) M = fmaxf(M, ml[2 * i]);
+    M = wave_max(M);
+    const float Ms = (M == -INFINITY) ? 0.0f : M;
+    float den = 0.0f;
+    for (int i = lane; i < nparts; i += 64) {
+        const float w = fast_exp2(ml[2 * i] - Ms);
+        wsh[i] = w;
+        den += w * ml[2 * i + 1];
+    }
+    den = wave_sum(den);
+    __syncthreads();
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+    const float *po = p.ws_o + base * D;
+    const size_t orow = ((size_t)seq * p.num_heads + h) * D;
+    for (int d = lane; d < D; d += 64) {
+        float acc = 0.0f;
+        for (int i = 0; i < nparts; i++) acc = fmaf(wsh[i], po[(size_t)i * D + d], acc);
+        store_elem<KV>(p.out, orow + d, acc * inv);
+    }
+}
+
+}  // namespace xhip
