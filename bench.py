@@ -1,0 +1,297 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X paged-decode attention (one GPU).
+
+Default workload: BASELINE config 2, the Llama-3-8B GQA ragged decode batch
+(32 q / 8 kv heads, d=128, fp16, bs=16, B=64, L ~ U[512, 4096], 2x page pool
+with garbage).  A step is one call of the reference entry point
+nxt_paged_attention over the whole batch, with every input already resident in
+HBM.  Steps rotate over several independent copies of the K/V pool (>= 3 and
+>= 768 MB in total) so no step is served from the 256 MB MALL of the previous
+one.
+
+Prints ONE JSON line:
+  value        seqs/s = num_seqs / (GPU time per step), whole job on 1 GPU
+  roofline     algorithmic bytes of one launch / average duration of the
+               partition kernel (HIP events on its stream), against 8 TB/s;
+               `traffic` = HBM bytes per launch from the committed rocprofv3
+               PMC summary for this workload (profiles/), else null
+  cpu_baseline the oracle (C restatement of the reference CPU attention)
+               on the host cores, all threads; single-thread figure alongside
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "paged-decode attn seqs/s + achieved HBM GB/s (% peak), Llama-3-8B GQA shape"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class HipEvents:
+    """hipEvent_t handles through the HIP runtime torch already loaded."""
+
+    def __init__(self):
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.events = []
+
+    def create(self) -> int:
+        ev = ctypes.c_void_p()
+        rc = self.hip.hipEventCreate(ctypes.byref(ev))
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreate failed: {rc}")
+        self.events.append(ev.value)
+        return ev.value
+
+    def record(self, ev: int, stream: int) -> None:
+        rc = self.hip.hipEventRecord(ev, stream)
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed: {rc}")
+
+    def elapsed_ms(self, a: int, b: int) -> float:
+        ms = ctypes.c_float()
+        rc = self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed: {rc}")
+        return ms.value
+
+    def destroy_all(self) -> None:
+        for ev in self.events:
+            self.hip.hipEventDestroy(ev)
+        self.events.clear()
+
+
+def load_traffic(workload_name: str):
+    """HBM bytes per launch of the partition kernel from the committed PMC
+    summary (profiles/<workload>_pmc.json), or None."""
+    path = os.path.join(ROOT, "profiles", f"{workload_name}_pmc.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        d = json.load(f)
+    return d.get("hbm_bytes_per_launch")
+
+
+def cpu_baseline(wl, budget_s: float) -> dict:
+    """Time the oracle on the host: all threads, then one thread, each on as
+    many whole copies of the batch (or leading sequences) as fit the budget."""
+    from oracle import oracle as O
+    threads = O.lib().oracle_num_threads()
+    res = {}
+    for name, prec, nthr in (("all", "mt", threads), ("single", "f32", 1)):
+        # probe with the first few sequences to size the sample
+        t0 = time.perf_counter()
+        probe = min(wl.num_seqs, 4)
+        O.run_workload(wl, precision=prec, threads=nthr, seqs=slice(0, probe))
+        dt = max(time.perf_counter() - t0, 1e-6)
+        per_seq = dt / probe
+        nseq = int(max(1, min(wl.num_seqs, budget_s / 2 / per_seq)))
+        reps = 1 if nseq < wl.num_seqs else int(max(1, budget_s / 2 / (per_seq * wl.num_seqs)))
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            O.run_workload(wl, precision=prec, threads=nthr, seqs=slice(0, nseq))
+        dt = time.perf_counter() - t0
+        res[name] = {"seqs": nseq * reps, "seconds": dt, "threads": nthr,
+                     "seqs_per_s": nseq * reps / dt}
+    return res
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=2, help="1..5, 6 = config 4b (GQA16)")
+    ap.add_argument("--partition", type=int, default=0,
+                    help="split-K tokens per wavefront (0 = automatic stream-K plan)")
+    ap.add_argument("--pools", type=int, default=0, help="K/V pool copies to rotate (0 = auto)")
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-check", action="store_true", help="skip the post-run oracle check")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="instead of the benchmark, run 5 plain device copies of MIB MiB "
+                         "(the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "the paged-decode path is sharded by sequence or kv head with no exchange, so the "
+              "per-GPU figure is the one to report", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    if args.copy_calibration:
+        n = args.copy_calibration * 2**20 // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4,
+                          "copies": 5}))
+        return 0
+
+    from xllms_amd import paged_attention as PA
+    from xllms_amd import workloads as W
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda:0")
+
+    t0 = time.perf_counter()
+    wl = W.make(args.config)
+    log(f"[bench] workload {wl.name}: {wl.describe()} built in {time.perf_counter() - t0:.1f}s")
+    alg_bytes = wl.algorithmic_bytes()
+    logical_bytes = wl.logical_bytes()
+
+    dw = W.upload(wl, dev)
+    pool_bytes = 2 * dw.key_cache.numel() * dw.key_cache.element_size()
+    pools = args.pools or max(3, -(-768 * 2**20 // pool_bytes))
+    kpools, vpools = [dw.key_cache], [dw.value_cache]
+    for _ in range(pools - 1):
+        kpools.append(dw.key_cache.clone())
+        vpools.append(dw.value_cache.clone())
+    torch.cuda.synchronize()
+    log(f"[bench] {pools} K/V pools of {pool_bytes / 2**20:.0f} MiB each resident in HBM")
+
+    stream = torch.cuda.current_stream().cuda_stream
+    lib = PA._lib.backend()
+    entry = "nxt_paged_attention" if args.partition == 0 and wl.kv_dtype != W.BF16 else None
+    waves = PA.auto_waves(wl.num_seqs, wl.num_heads, wl.head_size, wl.num_kv_heads,
+                          wl.max_num_blocks_per_seq, wl.block_size, wl.kv_dtype)
+
+    # Pre-marshalled arguments: the timed loop is one ctypes call per step.
+    fn = getattr(lib, entry) if entry else lib.nxt_paged_attention_ex
+    def args_for(kc, vc):
+        a = (dw.out.data_ptr(), dw.query.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+             dw.block_tables.data_ptr(), dw.seq_lens.data_ptr(), wl.num_seqs, wl.num_heads,
+             wl.head_size, wl.num_kv_heads, ctypes.c_float(wl.scale), wl.max_num_blocks_per_seq,
+             wl.block_size, wl.elem_bytes, wl.kv_block_stride, wl.kv_head_stride, stream)
+        return a if entry else a + (wl.kv_dtype, args.partition)
+    call_args = [args_for(k, v) for k, v in zip(kpools, vpools)]
+
+    def step(i: int) -> None:
+        fn(*call_args[i % pools])
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    st, msg = PA.last_status()
+    if st != 0:
+        raise RuntimeError(f"launch failed: {msg}")
+
+    ev = HipEvents()
+    begin, end = ev.create(), ev.create()
+    k_start = [ev.create() for _ in range(args.steps)]
+    k_done = [ev.create() for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    ev.record(begin, stream)
+    for i in range(args.steps):
+        lib.nxt_attn_set_trace_events(k_start[i], k_done[i])
+        step(args.warmup + i)
+    lib.nxt_attn_set_trace_events(None, None)
+    ev.record(end, stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    st, msg = PA.last_status()
+    if st != 0:
+        raise RuntimeError(f"launch failed: {msg}")
+    total_ms = ev.elapsed_ms(begin, end)
+    kern_ms = np.array([ev.elapsed_ms(a, b) for a, b in zip(k_start, k_done)])
+    ev.destroy_all()
+
+    ms_per_step = total_ms / args.steps
+    kernel_avg_ms = float(kern_ms.mean())
+    value = wl.num_seqs / (ms_per_step / 1e3)
+    achieved = alg_bytes / (kernel_avg_ms / 1e3) / 1e9
+    log(f"[bench] {args.steps} steps: {ms_per_step * 1e3:.1f} us/step (wall {wall / args.steps * 1e6:.1f}"
+        f" us), partition kernel {kernel_avg_ms * 1e3:.1f} us avg "
+        f"(min {kern_ms.min() * 1e3:.1f}, max {kern_ms.max() * 1e3:.1f}), "
+        f"{achieved:.0f} GB/s = {achieved / HBM_PEAK_GBS:.1%} of 8 TB/s, "
+        f"step {alg_bytes / (ms_per_step / 1e3) / 1e9:.0f} GB/s")
+
+    check = None
+    if not args.no_check:
+        from oracle import oracle as O
+        from tests.helpers import assert_close
+        got = dw.out.float().cpu().numpy()
+        idx = np.arange(0, wl.num_seqs, max(1, wl.num_seqs // 8))
+        ref = O.run_workload(wl, precision="mt", seqs=idx)
+        stats = assert_close(got[idx], ref, wl.kv_dtype, "bench output")
+        check = {"seqs_checked": int(len(idx)), **stats}
+        log(f"[bench] output matches the oracle on {len(idx)} sequences: {stats}")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        c = cpu_baseline(wl, args.cpu_budget)
+        tok_per_seq = wl.tokens() / wl.num_seqs
+        cpu = {"value": round(c["all"]["seqs_per_s"], 2), "unit": "seqs/s",
+               "cores": c["all"]["threads"], "kind": "port",
+               "sample": (f"oracle/paged_attention_oracle.c (C restatement of text_gen.c:1284-1310"
+                          f" over the operator-API buffers, gcc -O2, OpenMP over (seq, head)) on "
+                          f"{c['all']['seqs']} sequences of this batch in {c['all']['seconds']:.1f}s"),
+               "single_thread": {"value": round(c["single"]["seqs_per_s"], 3), "cores": 1,
+                                 "sample": f"{c['single']['seqs']} sequences in "
+                                           f"{c['single']['seconds']:.1f}s"},
+               "gbs_all_threads": round(c["all"]["seqs_per_s"] * alg_bytes / wl.num_seqs / 1e9, 2),
+               "tokens_per_seq": round(tok_per_seq, 1)}
+        log(f"[bench] cpu baseline: {cpu}")
+
+    traffic = load_traffic(wl.name)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "seqs/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {W.FP16: "fp16", W.BF16: "bf16", W.FP32: "fp32"}[wl.kv_dtype],
+        "data": "synthetic (seeded N(0,1) Q/K/V, seeded ragged lengths and page tables)",
+        "config": {"workload": wl.name, "num_seqs": wl.num_seqs, "num_heads": wl.num_heads,
+                   "num_kv_heads": wl.num_kv_heads, "head_size": wl.head_size,
+                   "block_size": wl.block_size, "tokens": wl.tokens(),
+                   "context_range": [int(wl.seq_lens.min()), int(wl.seq_lens.max())],
+                   "split_k": ("stream-K, %d wavefronts" % waves) if args.partition == 0
+                   else f"{args.partition} tokens per wavefront", "kv_pools_rotated": pools,
+                   "entry_point": entry or "nxt_paged_attention_ex", "seed": wl.seed},
+        "achieved_gbs_step": round(alg_bytes / (ms_per_step / 1e3) / 1e9, 1),
+        "algorithmic_bytes": alg_bytes,
+        "logical_bytes": logical_bytes,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "kernel": "paged_decode_partition_kernel",
+                     "kernel_avg_us": round(kernel_avg_ms * 1e3, 2)},
+        "cpu_baseline": cpu,
+        "check": check,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -27,7 +27,8 @@
  *     nxt_attn_last_status()/nxt_attn_last_error() on the calling thread.
  * Supported: head_size in {32,64,80,96,112,128,192,256}; G = 1..32 with
  * num_heads % num_kv_heads == 0; block_size a power of two in [1, 1024];
- * 16-byte aligned tensors and strides (every real KV cache layout).
+ * max_num_blocks_per_seq*block_size <= 2^28; 16-byte aligned tensors and
+ * strides (every real KV cache layout).
  *
  * Calls are asynchronous on `stream` (NULL = the default stream) and never
  * synchronise, except the rare call that must grow the split-K workspace of
@@ -103,9 +104,11 @@ enum {
 
 /* Same computation as nxt_paged_attention, with the dtype named explicitly
  * (dtype_size must agree: 2 for FP16/BF16, 4 for FP32) and the split-K
- * partition length in tokens (0 = automatic; otherwise a power of two >= 16
- * used as given, e.g. to check that results do not depend on it).
- * Returns NXT_ATTN_OK or a negative status. */
+ * granularity: partition_tokens = 0 lets the library spread the batch
+ * evenly over one resident round of wavefronts; otherwise it is the token
+ * range each wavefront streams (a power of two >= the kernel tile, 16 tokens
+ * for fp16/bf16 head_size 128), e.g. to check that results do not depend on
+ * where sequences are cut.  Returns NXT_ATTN_OK or a negative status. */
 int nxt_paged_attention_ex(void *out, const void *query, const void *key_cache,
                            const void *value_cache, const int *block_tables,
                            const int *seq_lens, int num_seqs, int num_heads,
@@ -114,16 +117,23 @@ int nxt_paged_attention_ex(void *out, const void *query, const void *key_cache,
                            int kv_block_stride, int kv_head_stride, nxt_stream_t stream,
                            int kv_dtype, int partition_tokens);
 
-/* Partition length nxt_paged_attention_ex would use for this shape with
- * partition_tokens = 0 (needs a current HIP device for its CU count), or a
+/* Wavefronts the automatic split-K plan launches for this shape (needs a
+ * current HIP device for its CU count and the kernel occupancy), or a
  * negative status. */
-int nxt_paged_attention_auto_partition(int num_seqs, int num_heads, int head_size,
-                                       int num_kv_heads, int max_num_blocks_per_seq,
-                                       int block_size, int kv_dtype);
+int nxt_paged_attention_auto_waves(int num_seqs, int num_heads, int head_size,
+                                   int num_kv_heads, int max_num_blocks_per_seq,
+                                   int block_size, int kv_dtype);
 
 /* Status and message of the last paged-attention call made by this thread. */
 int nxt_attn_last_status(void);
 const char *nxt_attn_last_error(void);
+
+/* Profiling hook: when set, every later launch from the calling thread
+ * records `start_event` on its stream just before the partition kernel and
+ * `partition_done_event` right after it (hipEvent_t handles owned by the
+ * caller), so the partition kernel can be timed on the stream it runs on.
+ * NULL, NULL clears the hook.  Meant for benchmarks and tracing. */
+void nxt_attn_set_trace_events(void *start_event, void *partition_done_event);
 
 /* Waits for and frees every cached split-K workspace of this process. */
 int nxt_attn_release_workspaces(void);

@@ -1,0 +1,179 @@
+"""The drop-in boundary, checked on the CPU (no GPU calls that compute).
+
+- libxllm_hip_backend.so loads and exports exactly the functions that
+  include/*.h declares (operator API of the reference's include/operator_api.h
+  plus the plugin ABI of backends/cuda_backend.h, plus the additive ones);
+- the plugin ABI structs have the reference's layouts (compile-time asserts
+  in tests/c/layout_check.c, and the ctypes mirrors of xllms_amd.backend);
+- the plugin conventions of the reference's tests/test_backend_load.c:83-163
+  hold (tests/c/plugin_contract.c, driven like backend_manager.c loads it);
+- argument validation rejects unsupported shapes without launching.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from xllms_amd import _lib
+from xllms_amd import backend as B
+from xllms_amd import paged_attention as PA
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(ROOT, "include")
+
+
+def declared_functions() -> set[str]:
+    names = set()
+    for fn in os.listdir(INCLUDE):
+        if not fn.endswith(".h"):
+            continue
+        text = open(os.path.join(INCLUDE, fn)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][\w ]*?[\s\*]+(nxt_\w+)\s*\(", text, re.M):
+            names.add(m.group(1))
+    return names
+
+
+def exported_functions(path: str) -> set[str]:
+    out = subprocess.run(["nm", "-D", "--defined-only", path], check=True, capture_output=True,
+                         text=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if " T " in line}
+
+
+def test_headers_declare_the_reference_entry_points():
+    names = declared_functions()
+    for ref in ("nxt_paged_attention", "nxt_paged_attention_v2", "nxt_paged_attention_flash",
+                "nxt_backend_init", "nxt_backend_run", "nxt_backend_fini"):
+        assert ref in names
+
+
+def test_library_exports_exactly_the_declared_symbols():
+    exported = exported_functions(_lib.BACKEND_SO)
+    declared = declared_functions()
+    assert exported == declared, (sorted(exported - declared), sorted(declared - exported))
+    assert set(_lib.OPERATOR_SYMBOLS) | set(_lib.PLUGIN_SYMBOLS) == declared
+
+
+def test_library_loads_and_resolves_every_symbol():
+    lib = _lib.backend()
+    for name in declared_functions():
+        assert getattr(lib, name) is not None
+    assert PA.version().startswith("xllm-hip-attn")
+
+
+def test_discovery_name_links_to_the_plugin():
+    """The reference manager discovers libxllm_cuda_backend.so by default
+    (cmake/xllm_config.h.in:18); the build provides that name too."""
+    alias = os.path.join(_lib.LIB_DIR, "libxllm_cuda_backend.so")
+    assert os.path.realpath(alias) == os.path.realpath(_lib.BACKEND_SO)
+
+
+def test_struct_layouts_compile_time():
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", f"-I{INCLUDE}", "-fsyntax-only",
+                    os.path.join(ROOT, "tests", "c", "layout_check.c")], check=True)
+
+
+def test_struct_layouts_ctypes_mirror():
+    assert ctypes.sizeof(B.NxtBackendAPI) == 64
+    assert ctypes.sizeof(B.NxtBackend) == 120
+    offs = {f[0]: getattr(B.NxtBackend, f[0]).offset for f in B.NxtBackend._fields_}
+    assert offs == {"name": 0, "so_path": 8, "dl_handle": 16, "api": 24, "state": 88,
+                    "priority": 92, "model_count": 96, "models": 104, "backend_state": 112}
+    assert ctypes.sizeof(B.NxtPagedAttentionInput) == 88
+    assert B.NxtPagedAttentionInput.scale.offset == 56
+    assert B.NxtPagedAttentionInput.stream.offset == 80
+    assert ctypes.sizeof(B.NxtPagedAttentionInputEx) == 104
+
+
+@pytest.fixture(scope="module")
+def contract_binary(tmp_path_factory):
+    exe = str(tmp_path_factory.mktemp("c") / "plugin_contract")
+    subprocess.run(["gcc", "-std=c11", "-O1", "-Wall", "-D__HIP_PLATFORM_AMD__",
+                    "-I/opt/rocm/include", f"-I{INCLUDE}", "-o", exe,
+                    os.path.join(ROOT, "tests", "c", "plugin_contract.c"), "-ldl", "-lm",
+                    "-L/opt/rocm/lib", "-Wl,-rpath,/opt/rocm/lib", "-lamdhip64"], check=True)
+    return exe
+
+
+def test_plugin_contract_c_harness(contract_binary):
+    r = subprocess.run([contract_binary, _lib.BACKEND_SO], capture_output=True, text=True,
+                       timeout=120)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0, r.stdout
+
+
+def test_plugin_null_conventions_python_loader():
+    b = B.LoadedBackend()
+    assert b.init_fn(None) == -1
+    assert b.run_fn(None, None, None) == -1
+    assert b.fini_fn(None) == -1
+    fresh = B.NxtBackend()
+    assert b.fini_fn(ctypes.byref(fresh)) == 0
+    assert fresh.state == B.STATE_UNINITIALIZED
+    assert b.fini_fn(ctypes.byref(fresh)) == 0
+
+
+def _call_ex(**kw):
+    lib = _lib.backend()
+    a = dict(num_seqs=2, num_heads=8, head_size=128, num_kv_heads=2, scale=0.1, maxb=4, bs=16,
+             dtype_size=2, kbs=2 * 16 * 128, khs=16 * 128, kv_dtype=PA.NXT_KV_FP16, part=0)
+    a.update(kw)
+    p = 256  # any 16-byte aligned non-null address: validation fails before any use
+    return lib.nxt_paged_attention_ex(p, p, p, p, p, p, a["num_seqs"], a["num_heads"],
+                                      a["head_size"], a["num_kv_heads"],
+                                      ctypes.c_float(a["scale"]), a["maxb"], a["bs"],
+                                      a["dtype_size"], a["kbs"], a["khs"], None, a["kv_dtype"],
+                                      a["part"])
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(head_size=100), PA.NXT_ATTN_E_UNSUPPORTED),
+    (dict(head_size=0), PA.NXT_ATTN_E_UNSUPPORTED),
+    (dict(num_heads=7), PA.NXT_ATTN_E_INVALID),
+    (dict(num_kv_heads=0), PA.NXT_ATTN_E_INVALID),
+    (dict(num_seqs=-1), PA.NXT_ATTN_E_INVALID),
+    (dict(dtype_size=4), PA.NXT_ATTN_E_INVALID),
+    (dict(kv_dtype=9), PA.NXT_ATTN_E_UNSUPPORTED),
+    (dict(bs=12), PA.NXT_ATTN_E_UNSUPPORTED),
+    (dict(bs=0), PA.NXT_ATTN_E_INVALID),
+    (dict(maxb=0), PA.NXT_ATTN_E_INVALID),
+    (dict(kbs=2 * 16 * 128 + 1), PA.NXT_ATTN_E_UNSUPPORTED),
+    (dict(khs=-16), PA.NXT_ATTN_E_INVALID),
+    (dict(scale=float("inf")), PA.NXT_ATTN_E_INVALID),
+    (dict(num_heads=66, num_kv_heads=1), PA.NXT_ATTN_E_UNSUPPORTED),
+    (dict(part=24), PA.NXT_ATTN_E_UNSUPPORTED),
+    (dict(part=8), PA.NXT_ATTN_E_UNSUPPORTED),
+    (dict(num_seqs=0), PA.NXT_ATTN_OK),
+])
+def test_validation_without_launch(kw, status):
+    assert _call_ex(**kw) == status
+    st, msg = PA.last_status()
+    assert st == status and msg
+
+
+def test_void_entry_points_record_status():
+    lib = _lib.backend()
+    p = 256
+    lib.nxt_paged_attention(p, p, p, p, p, p, 1, 8, 100, 2, ctypes.c_float(0.1), 4, 16, 2, 4096,
+                            2048, None)
+    assert lib.nxt_attn_last_status() == PA.NXT_ATTN_E_UNSUPPORTED
+    lib.nxt_paged_attention_v2(p, p, p, p, p, p, 1, 8, 128, 2, ctypes.c_float(0.1), 4, 16, 3,
+                               4096, 2048, None)
+    assert lib.nxt_attn_last_status() == PA.NXT_ATTN_E_UNSUPPORTED
+    lib.nxt_paged_attention_flash(p, p, p, p, p, p, 0, 8, 128, 2, ctypes.c_float(0.1), 4, 16, 2,
+                                  4096, 2048, None)
+    assert lib.nxt_attn_last_status() == PA.NXT_ATTN_OK
+
+
+def test_product_never_imports_the_oracle():
+    """The product path (package + native sources) has no route to oracle/."""
+    pkg = os.path.join(ROOT, "xllms_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for fn in files:
+            if fn.endswith((".py", ".c", ".cpp", ".h", ".hip", "Makefile")):
+                text = open(os.path.join(dirpath, fn)).read()
+                assert not re.search(r"\boracle\b", text.replace("no route to oracle", "")), fn

@@ -48,9 +48,10 @@ OPERATOR_SYMBOLS = (
     "nxt_paged_attention_v2",
     "nxt_paged_attention_flash",
     "nxt_paged_attention_ex",
-    "nxt_paged_attention_auto_partition",
+    "nxt_paged_attention_auto_waves",
     "nxt_attn_last_status",
     "nxt_attn_last_error",
+    "nxt_attn_set_trace_events",
     "nxt_attn_release_workspaces",
     "nxt_attn_version",
 )
@@ -69,14 +70,16 @@ def backend() -> ctypes.CDLL:
             fn.restype = None
         lib.nxt_paged_attention_ex.argtypes = _LEGACY_ARGS + [c_int, c_int]
         lib.nxt_paged_attention_ex.restype = c_int
-        lib.nxt_paged_attention_auto_partition.argtypes = [c_int] * 7
-        lib.nxt_paged_attention_auto_partition.restype = c_int
+        lib.nxt_paged_attention_auto_waves.argtypes = [c_int] * 7
+        lib.nxt_paged_attention_auto_waves.restype = c_int
         lib.nxt_attn_last_status.argtypes = []
         lib.nxt_attn_last_status.restype = c_int
         lib.nxt_attn_last_error.argtypes = []
         lib.nxt_attn_last_error.restype = ctypes.c_char_p
         lib.nxt_attn_release_workspaces.argtypes = []
         lib.nxt_attn_release_workspaces.restype = c_int
+        lib.nxt_attn_set_trace_events.argtypes = [c_void_p, c_void_p]
+        lib.nxt_attn_set_trace_events.restype = None
         lib.nxt_attn_version.argtypes = []
         lib.nxt_attn_version.restype = ctypes.c_char_p
         lib._xllm_typed = True

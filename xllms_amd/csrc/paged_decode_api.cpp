@@ -24,6 +24,8 @@ using xhip::DecodeParams;
 
 thread_local int t_status = NXT_ATTN_OK;
 thread_local char t_message[512] = "ok";
+thread_local hipEvent_t t_trace_start = nullptr;
+thread_local hipEvent_t t_trace_partition = nullptr;
 
 int set_status(int status, const char *fmt, ...) {
     t_status = status;
@@ -156,24 +158,34 @@ bool head_tiling(int group, HeadTiling *t) {
     return t->head_tiles <= xhip::kWavesPerGroup;
 }
 
-// Automatic partition length: enough wavefront items to give every CU
-// kItemsPerCu of them, assuming sequences use about half of their block table
-// on average; a power of two in [max(tile, 64), 1024].
-constexpr int kItemsPerCu = 16;
+// Smallest stream-K range, in tiles, the automatic plan gives a wavefront:
+// below this the per-range setup (prefix lookup, Q load, merge) dominates.
+constexpr int kMinTilesPerWave = 4;
 
-int auto_partition(int num_seqs, int num_kv_heads, int head_tiles, long long max_ctx, int tile,
-                   int cus) {
-    const long long pairs = (long long)num_seqs * num_kv_heads * head_tiles;
-    const long long mean_ctx = max_ctx / 2 > 0 ? max_ctx / 2 : 1;
-    const long long want_items = (long long)cus * kItemsPerCu;
-    long long c = (pairs * mean_ctx + want_items - 1) / want_items;
-    int lo = tile > 64 ? tile : 64;
-    int part = lo;
-    while (part < c && part < 1024) part <<= 1;
-    return part;
+int partition_occupancy(int kv_dtype, int head_size, int head_tile, size_t lds) {
+    switch (kv_dtype) {
+    case NXT_KV_FP16: return xhip::partition_occupancy_f16(head_size, head_tile, lds);
+    case NXT_KV_BF16: return xhip::partition_occupancy_bf16(head_size, head_tile, lds);
+    default: return xhip::partition_occupancy_f32(head_size, head_tile, lds);
+    }
 }
 
-constexpr int kMaxParts = 16384;  // reduce kernel stages one float per partition in LDS
+// Wavefronts of the automatic plan: one resident round of the partition
+// kernel on every CU, but no more than the batch could keep busy with
+// kMinTilesPerWave tiles each.
+long long auto_waves(int kv_dtype, int head_size, int head_tile, int nseq, long long ub_tiles,
+                     int cus) {
+    const size_t lds = (size_t)(nseq + 1) * sizeof(int);
+    const int occ = partition_occupancy(kv_dtype, head_size, head_tile, lds);
+    if (occ <= 0) return 0;
+    long long w = (long long)cus * occ * xhip::kWavesPerGroup;
+    const long long need = (ub_tiles + kMinTilesPerWave - 1) / kMinTilesPerWave;
+    if (need < w) w = need;
+    w = (w + xhip::kWavesPerGroup - 1) / xhip::kWavesPerGroup * xhip::kWavesPerGroup;
+    return w > 0 ? w : xhip::kWavesPerGroup;
+}
+
+constexpr long long kMaxWaves = 1LL << 22;  // bounds the partial workspace of explicit plans
 
 const char *dtype_name(int kv_dtype) {
     switch (kv_dtype) {
@@ -217,7 +229,7 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
                           kv_head_stride);
     if (!isfinite(scale)) return set_status(NXT_ATTN_E_INVALID, "scale is not finite");
     const long long max_ctx = (long long)max_num_blocks_per_seq * block_size;
-    if (max_ctx > (1LL << 30))
+    if (max_ctx > (1LL << 28))
         return set_status(NXT_ATTN_E_UNSUPPORTED, "context bound %lld tokens too large", max_ctx);
     const int group = num_heads / num_kv_heads;
     HeadTiling tiling;
@@ -235,81 +247,100 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
     if ((uintptr_t)block_tables & 3 || (uintptr_t)seq_lens & 3)
         return set_status(NXT_ATTN_E_INVALID, "int32 tables must be 4-byte aligned");
 
+    const int tile = tile_tokens(head_size, kv_dtype);
+    if (partition_tokens != 0 && (!is_pow2(partition_tokens) || partition_tokens < tile))
+        return set_status(NXT_ATTN_E_UNSUPPORTED,
+                          "partition_tokens %d must be a power of two >= %d for head_size %d %s",
+                          partition_tokens, tile, head_size, dtype_name(kv_dtype));
+
     int device = 0;
     hipError_t e = hipGetDevice(&device);
     if (e != hipSuccess) return set_status(NXT_ATTN_E_HIP, "hipGetDevice: %s", hipGetErrorString(e));
     hipStream_t stream = (hipStream_t)stream_handle;
+    const int cus = cu_count(device);
+    const int segs = num_kv_heads * tiling.head_tiles;
+    const long long tiles_per_seg = (max_ctx + tile - 1) / tile;
 
-    // ---- split-K plan
-    const int tile = tile_tokens(head_size, kv_dtype);
-    int part = partition_tokens;
-    if (part == 0) {
-        part = auto_partition(num_seqs, num_kv_heads, tiling.head_tiles, max_ctx, tile,
-                              cu_count(device));
-    } else if (!is_pow2(part) || part < tile) {
-        return set_status(NXT_ATTN_E_UNSUPPORTED,
-                          "partition_tokens %d must be a power of two >= %d for head_size %d %s",
-                          partition_tokens, tile, head_size, dtype_name(kv_dtype));
-    }
-    long long max_parts = (max_ctx + part - 1) / part;
-    if (max_parts > kMaxParts)
-        return set_status(NXT_ATTN_E_UNSUPPORTED, "%lld partitions exceed %d; raise partition_tokens",
-                          max_parts, kMaxParts);
-    const long long items = (long long)num_seqs * num_kv_heads * tiling.head_tiles * max_parts;
-    const long long grid = (items + xhip::kWavesPerGroup - 1) / xhip::kWavesPerGroup;
-    if (items > 0x7FFFFFFFLL || grid > 0x7FFFFFFFLL)
-        return set_status(NXT_ATTN_E_UNSUPPORTED, "work grid of %lld items too large", items);
-    if (num_seqs > 65535 || num_heads > 65535)
-        return set_status(NXT_ATTN_E_UNSUPPORTED, "num_seqs/num_heads above 65535");
+    // Batches beyond kMaxSeqsPerLaunch go in consecutive launches (the
+    // per-workgroup prefix scan of the partition kernel lives in LDS).
+    for (int s0 = 0; s0 < num_seqs; s0 += xhip::kMaxSeqsPerLaunch) {
+        const int nseq = num_seqs - s0 < xhip::kMaxSeqsPerLaunch ? num_seqs - s0
+                                                                 : xhip::kMaxSeqsPerLaunch;
+        const long long ub_tiles = (long long)nseq * segs * tiles_per_seg;
+        long long waves;
+        int min_tpw;
+        if (partition_tokens == 0) {
+            waves = auto_waves(kv_dtype, head_size, tiling.head_tile, nseq, ub_tiles, cus);
+            if (waves <= 0)
+                return set_status(NXT_ATTN_E_HIP, "no occupancy for head_size %d %s", head_size,
+                                  dtype_name(kv_dtype));
+            min_tpw = kMinTilesPerWave;
+        } else {
+            min_tpw = partition_tokens / tile;
+            waves = (ub_tiles + min_tpw - 1) / min_tpw;
+            waves = (waves + xhip::kWavesPerGroup - 1) / xhip::kWavesPerGroup *
+                    xhip::kWavesPerGroup;
+            if (waves > kMaxWaves)
+                return set_status(NXT_ATTN_E_UNSUPPORTED,
+                                  "partition_tokens %d gives %lld wavefronts; raise it",
+                                  partition_tokens, waves);
+        }
 
-    DecodeParams p;
-    memset(&p, 0, sizeof(p));
-    p.out = out;
-    p.q = query;
-    p.k = key_cache;
-    p.v = value_cache;
-    p.block_tables = block_tables;
-    p.seq_lens = seq_lens;
-    p.kv_block_stride = kv_block_stride;
-    p.kv_head_stride = kv_head_stride;
-    p.num_seqs = num_seqs;
-    p.num_heads = num_heads;
-    p.num_kv_heads = num_kv_heads;
-    p.group = group;
-    p.head_tiles = tiling.head_tiles;
-    p.max_blocks = max_num_blocks_per_seq;
-    p.block_size = block_size;
-    p.bs_shift = ilog2(block_size);
-    p.part_tokens = part;
-    p.max_parts = (int)max_parts;
-    p.max_ctx = (int)max_ctx;
-    p.scale_log2 = scale * 1.4426950408889634f;
-
-    const bool reduce = max_parts > 1;
-    if (reduce) {
-        const size_t rows = (size_t)num_seqs * num_heads * (size_t)max_parts;
-        const size_t o_bytes = (rows * head_size * sizeof(float) + 255) & ~(size_t)255;
-        const size_t bytes = o_bytes + rows * 2 * sizeof(float);
+        const size_t eb_total = (size_t)elem_bytes(kv_dtype);
+        const size_t slots = (size_t)waves * 2 * tiling.head_tile;
+        const size_t o_bytes = (slots * head_size * sizeof(float) + 255) & ~(size_t)255;
+        const size_t ml_bytes = (slots * 2 * sizeof(float) + 255) & ~(size_t)255;
+        const size_t pre_bytes = (size_t)(nseq + 1) * sizeof(int);
         void *ws = nullptr;
-        int st = get_workspace(device, stream, bytes, &ws);
+        int st = get_workspace(device, stream, o_bytes + ml_bytes + pre_bytes, &ws);
         if (st != NXT_ATTN_OK) return st;
+
+        const size_t row0 = (size_t)s0 * num_heads * head_size * eb_total;
+        DecodeParams p;
+        memset(&p, 0, sizeof(p));
+        p.out = (char *)out + row0;
+        p.q = (const char *)query + row0;
+        p.k = key_cache;
+        p.v = value_cache;
+        p.block_tables = block_tables + (size_t)s0 * max_num_blocks_per_seq;
+        p.seq_lens = seq_lens + s0;
         p.ws_o = (float *)ws;
         p.ws_ml = (float *)((char *)ws + o_bytes);
-    }
+        p.ws_prefix = (int *)((char *)ws + o_bytes + ml_bytes);
+        p.kv_block_stride = kv_block_stride;
+        p.kv_head_stride = kv_head_stride;
+        p.num_seqs = nseq;
+        p.num_heads = num_heads;
+        p.num_kv_heads = num_kv_heads;
+        p.group = group;
+        p.head_tiles = tiling.head_tiles;
+        p.max_blocks = max_num_blocks_per_seq;
+        p.block_size = block_size;
+        p.bs_shift = ilog2(block_size);
+        p.max_ctx = (int)max_ctx;
+        p.num_waves = (int)waves;
+        p.min_tiles_per_wave = min_tpw;
+        p.scale_log2 = scale * 1.4426950408889634f;
 
-    switch (kv_dtype) {
-    case NXT_KV_FP16:
-        e = xhip::launch_decode_f16(p, head_size, tiling.head_tile, (unsigned)grid, reduce, stream);
-        break;
-    case NXT_KV_BF16:
-        e = xhip::launch_decode_bf16(p, head_size, tiling.head_tile, (unsigned)grid, reduce, stream);
-        break;
-    default:
-        e = xhip::launch_decode_f32(p, head_size, tiling.head_tile, (unsigned)grid, reduce, stream);
-        break;
+        if (t_trace_start) {
+            e = hipEventRecord(t_trace_start, stream);
+            if (e != hipSuccess)
+                return set_status(NXT_ATTN_E_HIP, "hipEventRecord: %s", hipGetErrorString(e));
+        }
+        switch (kv_dtype) {
+        case NXT_KV_FP16:
+            e = xhip::launch_decode_f16(p, head_size, tiling.head_tile, stream, t_trace_partition);
+            break;
+        case NXT_KV_BF16:
+            e = xhip::launch_decode_bf16(p, head_size, tiling.head_tile, stream, t_trace_partition);
+            break;
+        default:
+            e = xhip::launch_decode_f32(p, head_size, tiling.head_tile, stream, t_trace_partition);
+            break;
+        }
+        if (e != hipSuccess)
+            return set_status(NXT_ATTN_E_HIP, "kernel launch: %s", hipGetErrorString(e));
     }
-    if (e != hipSuccess)
-        return set_status(NXT_ATTN_E_HIP, "kernel launch: %s", hipGetErrorString(e));
     return ok();
 }
 
@@ -379,10 +410,10 @@ __attribute__((visibility("default"))) int nxt_paged_attention_ex(
                kv_block_stride, kv_head_stride, stream, kv_dtype, partition_tokens);
 }
 
-__attribute__((visibility("default"))) int nxt_paged_attention_auto_partition(
+__attribute__((visibility("default"))) int nxt_paged_attention_auto_waves(
     int num_seqs, int num_heads, int head_size, int num_kv_heads, int max_num_blocks_per_seq,
     int block_size, int kv_dtype) {
-    if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads ||
+    if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads ||
         !supported_head_size(head_size) || max_num_blocks_per_seq <= 0 || block_size <= 0 ||
         (kv_dtype != NXT_KV_FP16 && kv_dtype != NXT_KV_BF16 && kv_dtype != NXT_KV_FP32))
         return NXT_ATTN_E_INVALID;
@@ -390,14 +421,24 @@ __attribute__((visibility("default"))) int nxt_paged_attention_auto_partition(
     if (!head_tiling(num_heads / num_kv_heads, &tiling)) return NXT_ATTN_E_UNSUPPORTED;
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess) return NXT_ATTN_E_HIP;
-    return auto_partition(num_seqs, num_kv_heads, tiling.head_tiles,
-                          (long long)max_num_blocks_per_seq * block_size,
-                          tile_tokens(head_size, kv_dtype), cu_count(device));
+    const int nseq = num_seqs < xhip::kMaxSeqsPerLaunch ? num_seqs : xhip::kMaxSeqsPerLaunch;
+    const int tile = tile_tokens(head_size, kv_dtype);
+    const long long ub = (long long)nseq * num_kv_heads * tiling.head_tiles *
+                         (((long long)max_num_blocks_per_seq * block_size + tile - 1) / tile);
+    const long long w = auto_waves(kv_dtype, head_size, tiling.head_tile, nseq, ub,
+                                   cu_count(device));
+    return w > 0 ? (int)w : NXT_ATTN_E_HIP;
 }
 
 __attribute__((visibility("default"))) int nxt_attn_last_status(void) { return t_status; }
 
 __attribute__((visibility("default"))) const char *nxt_attn_last_error(void) { return t_message; }
+
+__attribute__((visibility("default"))) void nxt_attn_set_trace_events(void *start_event,
+                                                                    void *partition_done_event) {
+    t_trace_start = (hipEvent_t)start_event;
+    t_trace_partition = (hipEvent_t)partition_done_event;
+}
 
 __attribute__((visibility("default"))) int nxt_attn_release_workspaces(void) {
     std::lock_guard<std::mutex> lock(g_ws_mu);

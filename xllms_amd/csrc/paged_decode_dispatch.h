@@ -6,36 +6,77 @@
 
 namespace xhip {
 
+template <int KV, int D, int GT> static const void *partition_fn() {
+    return reinterpret_cast<const void *>(&paged_decode_partition_kernel<KV, D, GT>);
+}
+
 template <int KV, int D>
-static hipError_t launch_for_head_size(const DecodeParams &p, int head_tile, unsigned grid,
-                                       bool reduce, hipStream_t st) {
-    const dim3 block(64 * kWavesPerGroup);
+static const void *partition_fn_for(int head_tile) {
     switch (head_tile) {
-    case 1: paged_decode_partition_kernel<KV, D, 1><<<grid, block, 0, st>>>(p); break;
-    case 2: paged_decode_partition_kernel<KV, D, 2><<<grid, block, 0, st>>>(p); break;
-    case 4: paged_decode_partition_kernel<KV, D, 4><<<grid, block, 0, st>>>(p); break;
-    case 8: paged_decode_partition_kernel<KV, D, 8><<<grid, block, 0, st>>>(p); break;
+    case 1: return partition_fn<KV, D, 1>();
+    case 2: return partition_fn<KV, D, 2>();
+    case 4: return partition_fn<KV, D, 4>();
+    case 8: return partition_fn<KV, D, 8>();
+    default: return nullptr;
+    }
+}
+
+template <int KV, int D, int GT>
+static hipError_t launch_tile(const DecodeParams &p, hipStream_t st, hipEvent_t after_partition) {
+    const unsigned grid = (unsigned)(p.num_waves / kWavesPerGroup);
+    const size_t lds = (size_t)(p.num_seqs + 1) * sizeof(int);
+    paged_decode_partition_kernel<KV, D, GT><<<grid, 64 * kWavesPerGroup, lds, st>>>(p);
+    if (after_partition) {
+        const hipError_t e = hipEventRecord(after_partition, st);
+        if (e != hipSuccess) return e;
+    }
+    const unsigned segs = (unsigned)(p.num_seqs * p.num_kv_heads * p.head_tiles);
+    paged_decode_merge_kernel<KV, D, GT><<<segs, 256, 0, st>>>(p);
+    return hipGetLastError();
+}
+
+template <int KV, int D>
+static hipError_t launch_for_head_size(const DecodeParams &p, int head_tile, hipStream_t st,
+                                       hipEvent_t after_partition) {
+    switch (head_tile) {
+    case 1: return launch_tile<KV, D, 1>(p, st, after_partition);
+    case 2: return launch_tile<KV, D, 2>(p, st, after_partition);
+    case 4: return launch_tile<KV, D, 4>(p, st, after_partition);
+    case 8: return launch_tile<KV, D, 8>(p, st, after_partition);
     default: return hipErrorInvalidValue;
     }
-    if (reduce) {
-        const dim3 rgrid(p.num_heads, p.num_seqs);
-        paged_decode_reduce_kernel<KV, D><<<rgrid, 64, (size_t)p.max_parts * sizeof(float), st>>>(p);
+}
+
+#define XHIP_FOR_HEAD_SIZES(X) X(32) X(64) X(80) X(96) X(112) X(128) X(192) X(256)
+
+template <int KV>
+static const void *partition_fn_dtype(int head_size, int head_tile) {
+    switch (head_size) {
+#define XHIP_CASE(d) case d: return partition_fn_for<KV, d>(head_tile);
+        XHIP_FOR_HEAD_SIZES(XHIP_CASE)
+#undef XHIP_CASE
+    default: return nullptr;
     }
-    return hipGetLastError();
+}
+
+template <int KV>
+static int occupancy_for_dtype(int head_size, int head_tile, size_t lds_bytes) {
+    const void *fn = partition_fn_dtype<KV>(head_size, head_tile);
+    if (!fn) return 0;
+    int blocks = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 64 * kWavesPerGroup,
+                                                     lds_bytes) != hipSuccess)
+        return 0;
+    return blocks;
 }
 
 template <int KV>
 static hipError_t launch_for_dtype(const DecodeParams &p, int head_size, int head_tile,
-                                   unsigned grid, bool reduce, hipStream_t st) {
+                                   hipStream_t st, hipEvent_t after_partition) {
     switch (head_size) {
-    case 32: return launch_for_head_size<KV, 32>(p, head_tile, grid, reduce, st);
-    case 64: return launch_for_head_size<KV, 64>(p, head_tile, grid, reduce, st);
-    case 80: return launch_for_head_size<KV, 80>(p, head_tile, grid, reduce, st);
-    case 96: return launch_for_head_size<KV, 96>(p, head_tile, grid, reduce, st);
-    case 112: return launch_for_head_size<KV, 112>(p, head_tile, grid, reduce, st);
-    case 128: return launch_for_head_size<KV, 128>(p, head_tile, grid, reduce, st);
-    case 192: return launch_for_head_size<KV, 192>(p, head_tile, grid, reduce, st);
-    case 256: return launch_for_head_size<KV, 256>(p, head_tile, grid, reduce, st);
+#define XHIP_CASE(d) case d: return launch_for_head_size<KV, d>(p, head_tile, st, after_partition);
+        XHIP_FOR_HEAD_SIZES(XHIP_CASE)
+#undef XHIP_CASE
     default: return hipErrorInvalidValue;
     }
 }

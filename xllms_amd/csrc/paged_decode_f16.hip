@@ -3,9 +3,13 @@
 
 namespace xhip {
 
-hipError_t launch_decode_f16(const DecodeParams &p, int head_size, int head_tile, unsigned grid,
-                             bool reduce, hipStream_t stream) {
-    return launch_for_dtype<KV_F16>(p, head_size, head_tile, grid, reduce, stream);
+int partition_occupancy_f16(int head_size, int head_tile, size_t lds_bytes) {
+    return occupancy_for_dtype<KV_F16>(head_size, head_tile, lds_bytes);
+}
+
+hipError_t launch_decode_f16(const DecodeParams &p, int head_size, int head_tile,
+                             hipStream_t stream, hipEvent_t after_partition) {
+    return launch_for_dtype<KV_F16>(p, head_size, head_tile, stream, after_partition);
 }
 
 }  // namespace xhip

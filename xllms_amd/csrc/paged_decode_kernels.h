@@ -19,11 +19,12 @@
 // lane's own output columns.  The row states are merged once, at the end of
 // the partition, with xor shuffles.
 //
-// Split-K.  A sequence's tokens are cut into partitions of part_tokens; each
-// (sequence, kv head, head tile, partition) is one wavefront work item.  A
-// sequence with one partition writes its output directly; otherwise every
-// partition writes (m, l, o) in fp32 to the workspace and
-// paged_decode_reduce_kernel merges them with the usual log-sum-exp rescale:
+// Split-K.  The work is distributed stream-K style (paged_decode_params.h):
+// each wavefront of one resident round owns an equal, contiguous range of
+// the batch's tiles, so ragged lengths cannot leave a tail of idle CUs.  A
+// segment finished inside one range is written directly; a segment cut by
+// range boundaries leaves fp32 partials (m, l, o) that
+// paged_decode_merge_kernel combines with the usual log-sum-exp rescale:
 //   M = max_p m_p,  O = sum_p 2^(m_p-M) o_p / sum_p 2^(m_p-M) l_p.
 // Scores are kept in log2 units (scale*log2(e) folded into the score) so the
 // exponentials are single v_exp_f32 instructions.
@@ -354,7 +355,65 @@ __device__ __forceinline__ void decode_partition(const DecodeParams &p, const in
     }
 }
 
-// Main kernel: one wavefront per (sequence, kv head, head tile, partition).
+// Clamped length of sequence s.
+__device__ __forceinline__ int seq_len_of(const DecodeParams &p, int s) {
+    const int L = p.seq_lens[s];
+    return L < 0 ? 0 : (L > p.max_ctx ? p.max_ctx : L);
+}
+
+__device__ __forceinline__ int tiles_per_wave(int total, int num_waves, int min_tpw) {
+    const int t = (total + num_waves - 1) / num_waves;
+    return t > min_tpw ? t : min_tpw;
+}
+
+// Exclusive prefix over sequences of the tiles of all their segments, into
+// LDS (num_seqs + 1 entries), by the whole workgroup.  Workgroup 0 also
+// stores it for the merge kernel.
+template <int TT>
+__device__ __forceinline__ void batch_prefix(const DecodeParams &p, int *pre) {
+    __shared__ int part[64 * kWavesPerGroup];
+    const int nthr = 64 * kWavesPerGroup;
+    const int tid = threadIdx.x;
+    const int B = p.num_seqs;
+    const int per = (B + nthr - 1) / nthr;
+    const int s0 = tid * per;
+    const int segs = p.num_kv_heads * p.head_tiles;
+    int local = 0;
+    for (int i = 0; i < per; i++) {
+        const int s = s0 + i;
+        if (s < B) {
+            const int t = (seq_len_of(p, s) + TT - 1) / TT * segs;
+            pre[s] = t;  // tiles of sequence s, scanned below
+            local += t;
+        }
+    }
+    part[tid] = local;
+    __syncthreads();
+    // Hillis-Steele inclusive scan of the per-thread sums.
+    for (int off = 1; off < nthr; off <<= 1) {
+        const int v = tid >= off ? part[tid - off] : 0;
+        __syncthreads();
+        part[tid] += v;
+        __syncthreads();
+    }
+    int run = part[tid] - local;  // exclusive prefix of this thread's first sequence
+    for (int i = 0; i < per; i++) {
+        const int s = s0 + i;
+        if (s < B) {
+            const int t = pre[s];
+            pre[s] = run;
+            run += t;
+        }
+    }
+    if (tid == nthr - 1) pre[B] = part[nthr - 1];
+    __syncthreads();
+    if (blockIdx.x == 0) {
+        for (int s = tid; s <= B; s += nthr) p.ws_prefix[s] = pre[s];
+    }
+}
+
+// Partition kernel: kWavesPerGroup wavefronts per workgroup, each owning one
+// stream-K range of tiles (see paged_decode_params.h).
 template <int KV, int D, int GT>
 __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_kernel(
     const DecodeParams p) {
@@ -363,146 +422,188 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
     constexpr int EB = Geo::kElemBytes;
     constexpr int NCH = Geo::kChunks;
     constexpr int RL = Geo::kRowLanes;
+    constexpr int TT = Geo::kTileTokens;
+    extern __shared__ int pre[];  // num_seqs + 1 tile prefixes
+
+    batch_prefix<TT>(p, pre);
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    unsigned item = blockIdx.x * kWavesPerGroup + wave;
-    const int ht = item % p.head_tiles;
-    item /= p.head_tiles;
-    const int part = item % p.max_parts;
-    item /= p.max_parts;
-    const int kvh = item % p.num_kv_heads;
-    const int seq = item / p.num_kv_heads;
-    if (seq >= p.num_seqs) return;
+    const int w = blockIdx.x * kWavesPerGroup + wave;
+    const int B = p.num_seqs;
+    const int total = pre[B];
+    const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);
+    const long long g_lo = (long long)w * tpw;
+    if (g_lo >= total) return;
+    int g = (int)g_lo;
+    const int g_end = min(total, g + tpw);
 
-    int L = p.seq_lens[seq];
-    L = L < 0 ? 0 : (L > p.max_ctx ? p.max_ctx : L);
-    const int nparts = (L + p.part_tokens - 1) / p.part_tokens;
-    if (part >= (nparts > 0 ? nparts : 1)) return;
+    // Sequence holding tile g: the last s with pre[s] <= g (empty sequences
+    // share their successor's prefix, so this lands on one with tiles).
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (pre[mid] <= g) lo = mid; else hi = mid - 1;
+    }
+    int s = __builtin_amdgcn_readfirstlane(lo);
 
     const int col = lane % RL;
     const int row = lane / RL;
     const bool col_ok = (NCH == RL) || (col < NCH);
-    const int g0 = ht * GT;
-    const int nh = min(GT, p.group - g0);
-    const size_t qrow0 = ((size_t)seq * p.num_heads + (size_t)kvh * p.group + g0) * D;
+    const int segs = p.num_kv_heads * p.head_tiles;
+    bool first = true;
 
-    if (L == 0) {  // empty sequence: zero rows
-        if (row == 0 && col_ok) {
+    while (g < g_end) {
+        const int L = seq_len_of(p, s);
+        const int Ts = (L + TT - 1) / TT;  // tiles per segment of sequence s
+        const int local = g - pre[s];
+        const int seg = local / Ts;
+        const int t0 = local - seg * Ts;
+        const int n = min(Ts - t0, g_end - g);
+        const int kvh = seg / p.head_tiles;
+        const int ht = seg - kvh * p.head_tiles;
+        const int g0 = ht * GT;
+        const int nh = min(GT, p.group - g0);
+        const size_t qrow0 = ((size_t)s * p.num_heads + (size_t)kvh * p.group + g0) * D;
+
+        ItemState<KV, D, GT> st;
 #pragma unroll
-            for (int g = 0; g < GT; g++)
-                if (g < nh)
-                    *(u32x4 *)((char *)p.out + (qrow0 + (size_t)g * D + col * VEC) * EB) =
-                        u32x4{0, 0, 0, 0};
+        for (int h = 0; h < GT; h++) {
+            st.q[h] = (h < nh && col_ok)
+                          ? load16((const char *)p.q + (qrow0 + (size_t)h * D + col * VEC) * EB)
+                          : u32x4{0, 0, 0, 0};
+            st.m[h] = -INFINITY;
+            st.l[h] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < VEC; e++) st.o[h][e] = 0.0f;
         }
-        return;
-    }
+        const int t_begin = t0 * TT;
+        const int t_end = min(L, (t0 + n) * TT);
+        const int *bt = p.block_tables + (size_t)s * p.max_blocks;
+        const char *kb = (const char *)p.k + (size_t)kvh * (size_t)p.kv_head_stride * EB;
+        const char *vb = (const char *)p.v + (size_t)kvh * (size_t)p.kv_head_stride * EB;
+        if (p.block_size >= Geo::kRows)
+            decode_partition<KV, D, GT, true>(p, bt, kb, vb, t_begin, t_end, row, col, col_ok, st);
+        else
+            decode_partition<KV, D, GT, false>(p, bt, kb, vb, t_begin, t_end, row, col, col_ok, st);
 
-    ItemState<KV, D, GT> st;
+        // Merge the row states (rows differ in lane bits >= log2 RL).
 #pragma unroll
-    for (int g = 0; g < GT; g++) {
-        st.q[g] = (g < nh && col_ok)
-                      ? load16((const char *)p.q + (qrow0 + (size_t)g * D + col * VEC) * EB)
-                      : u32x4{0, 0, 0, 0};
-        st.m[g] = -INFINITY;
-        st.l[g] = 0.0f;
+        for (int off = RL; off < 64; off <<= 1) {
 #pragma unroll
-        for (int e = 0; e < VEC; e++) st.o[g][e] = 0.0f;
-    }
-
-    const int t_begin = part * p.part_tokens;
-    const int t_end = min(L, t_begin + p.part_tokens);
-    const int *bt = p.block_tables + (size_t)seq * p.max_blocks;
-    const char *kb = (const char *)p.k + (size_t)kvh * (size_t)p.kv_head_stride * EB;
-    const char *vb = (const char *)p.v + (size_t)kvh * (size_t)p.kv_head_stride * EB;
-    if (p.block_size >= Geo::kRows)
-        decode_partition<KV, D, GT, true>(p, bt, kb, vb, t_begin, t_end, row, col, col_ok, st);
-    else
-        decode_partition<KV, D, GT, false>(p, bt, kb, vb, t_begin, t_end, row, col, col_ok, st);
-
-    // Merge the row states of the wavefront (rows differ in lane bits >= log2 RL).
+            for (int h = 0; h < GT; h++) {
+                const float mo = __shfl_xor(st.m[h], off);
+                const float lo2 = __shfl_xor(st.l[h], off);
+                const float M = fmaxf(st.m[h], mo);
+                const float Ms = (M == -INFINITY) ? 0.0f : M;
+                const float a = fast_exp2(st.m[h] - Ms);
+                const float b = fast_exp2(mo - Ms);
+                st.l[h] = st.l[h] * a + lo2 * b;
+                st.m[h] = M;
 #pragma unroll
-    for (int off = RL; off < 64; off <<= 1) {
-#pragma unroll
-        for (int g = 0; g < GT; g++) {
-            const float mo = __shfl_xor(st.m[g], off);
-            const float lo = __shfl_xor(st.l[g], off);
-            const float M = fmaxf(st.m[g], mo);
-            const float Ms = (M == -INFINITY) ? 0.0f : M;
-            const float a = fast_exp2(st.m[g] - Ms);
-            const float b = fast_exp2(mo - Ms);
-            st.l[g] = st.l[g] * a + lo * b;
-            st.m[g] = M;
-#pragma unroll
-            for (int e = 0; e < VEC; e++)
-                st.o[g][e] = st.o[g][e] * a + __shfl_xor(st.o[g][e], off) * b;
-        }
-    }
-
-    if (row != 0 || !col_ok) return;
-    if (nparts == 1) {
-#pragma unroll
-        for (int g = 0; g < GT; g++) {
-            if (g >= nh) continue;
-            const float inv = st.l[g] > 0.0f ? 1.0f / st.l[g] : 0.0f;
-            float f[VEC];
-#pragma unroll
-            for (int e = 0; e < VEC; e++) f[e] = st.o[g][e] * inv;
-            *(u32x4 *)((char *)p.out + (qrow0 + (size_t)g * D + col * VEC) * EB) =
-                float_to_chunk<KV, VEC>(f);
-        }
-    } else {
-#pragma unroll
-        for (int g = 0; g < GT; g++) {
-            if (g >= nh) continue;
-            const size_t pi =
-                ((size_t)seq * p.num_heads + (size_t)kvh * p.group + g0 + g) * p.max_parts + part;
-            float *dst = p.ws_o + pi * D + col * VEC;
-#pragma unroll
-            for (int e = 0; e < VEC; e += 4)
-                *(f32x4 *)(dst + e) = f32x4{st.o[g][e], st.o[g][e + 1], st.o[g][e + 2], st.o[g][e + 3]};
-            if (col == 0) {
-                p.ws_ml[2 * pi] = st.m[g];
-                p.ws_ml[2 * pi + 1] = st.l[g];
+                for (int e = 0; e < VEC; e++)
+                    st.o[h][e] = st.o[h][e] * a + __shfl_xor(st.o[h][e], off) * b;
             }
+        }
+
+        if (row == 0 && col_ok) {
+            if (t0 == 0 && n == Ts) {  // whole segment in this range: final output
+#pragma unroll
+                for (int h = 0; h < GT; h++) {
+                    if (h >= nh) continue;
+                    const float inv = st.l[h] > 0.0f ? 1.0f / st.l[h] : 0.0f;
+                    float f[VEC];
+#pragma unroll
+                    for (int e = 0; e < VEC; e++) f[e] = st.o[h][e] * inv;
+                    *(u32x4 *)((char *)p.out + (qrow0 + (size_t)h * D + col * VEC) * EB) =
+                        float_to_chunk<KV, VEC>(f);
+                }
+            } else {  // cut segment: partial into this wavefront's slot
+                const size_t slot = (size_t)w * 2 + (first ? 0 : 1);
+#pragma unroll
+                for (int h = 0; h < GT; h++) {
+                    if (h >= nh) continue;
+                    float *dst = p.ws_o + (slot * GT + h) * D + col * VEC;
+#pragma unroll
+                    for (int e = 0; e < VEC; e += 4)
+                        *(f32x4 *)(dst + e) =
+                            f32x4{st.o[h][e], st.o[h][e + 1], st.o[h][e + 2], st.o[h][e + 3]};
+                    if (col == 0) {
+                        p.ws_ml[(slot * GT + h) * 2] = st.m[h];
+                        p.ws_ml[(slot * GT + h) * 2 + 1] = st.l[h];
+                    }
+                }
+            }
+        }
+        g += n;
+        first = false;
+        if (g - pre[s] >= Ts * segs) {  // sequence done: next one with tiles
+            s++;
+            while (s < B - 1 && pre[s + 1] == pre[s]) s++;
         }
     }
 }
 
-// Merge the partitions of one (sequence, query head).  One wavefront; the
-// per-partition weights 2^(m_p - M) are staged in LDS (max_parts floats).
-template <int KV, int D>
-__global__ __launch_bounds__(64) void paged_decode_reduce_kernel(const DecodeParams p) {
-    extern __shared__ float wsh[];
-    const int h = blockIdx.x;
-    const int seq = blockIdx.y;
-    const int lane = threadIdx.x;
-    int L = p.seq_lens[seq];
-    L = L < 0 ? 0 : (L > p.max_ctx ? p.max_ctx : L);
-    const int nparts = (L + p.part_tokens - 1) / p.part_tokens;
-    if (nparts < 2) return;
+// Merge kernel: one workgroup per segment (sequence, kv head, head tile).
+// Writes zeros for an empty sequence, does nothing for a segment finished
+// inside one wavefront range, and otherwise combines the partials of every
+// wavefront that touched the segment.  Thread (h, c) owns four output
+// columns 4c..4c+3 of head h of the tile.
+template <int KV, int D, int GT>
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeParams p) {
+    using Geo = Geometry<KV, D>;
+    constexpr int TT = Geo::kTileTokens;
+    constexpr int C4 = D / 4;
+    const int segs = p.num_kv_heads * p.head_tiles;
+    const int s = blockIdx.x / segs;
+    const int seg = blockIdx.x - s * segs;
+    const int kvh = seg / p.head_tiles;
+    const int ht = seg - kvh * p.head_tiles;
+    const int g0 = ht * GT;
+    const int nh = min(GT, p.group - g0);
+    const int tid = threadIdx.x;
+    const int L = seq_len_of(p, s);
+    const size_t qrow0 = ((size_t)s * p.num_heads + (size_t)kvh * p.group + g0) * D;
 
-    const size_t base = ((size_t)seq * p.num_heads + h) * p.max_parts;
-    const float *ml = p.ws_ml + 2 * base;
-    float M = -INFINITY;
-    for (int i = lane; i < nparts; i += 64) M = fmaxf(M, ml[2 * i]);
-    M = wave_max(M);
-    const float Ms = (M == -INFINITY) ? 0.0f : M;
-    float den = 0.0f;
-    for (int i = lane; i < nparts; i += 64) {
-        const float w = fast_exp2(ml[2 * i] - Ms);
-        wsh[i] = w;
-        den += w * ml[2 * i + 1];
+    if (L == 0) {
+        for (int i = tid; i < nh * D; i += blockDim.x) store_elem<KV>(p.out, qrow0 + i, 0.0f);
+        return;
     }
-    den = wave_sum(den);
-    __syncthreads();
-    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-    const float *po = p.ws_o + base * D;
-    const size_t orow = ((size_t)seq * p.num_heads + h) * D;
-    for (int d = lane; d < D; d += 64) {
-        float acc = 0.0f;
-        for (int i = 0; i < nparts; i++) acc = fmaf(wsh[i], po[(size_t)i * D + d], acc);
-        store_elem<KV>(p.out, orow + d, acc * inv);
+    const int total = p.ws_prefix[p.num_seqs];
+    const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);
+    const int Ts = (L + TT - 1) / TT;
+    const int seg_start = p.ws_prefix[s] + seg * Ts;
+    const int w_first = seg_start / tpw;
+    const int w_last = (seg_start + Ts - 1) / tpw;
+    if (w_first == w_last) return;
+    const int np = w_last - w_first + 1;
+    const int slot0 = (seg_start == w_first * tpw) ? 0 : 1;
+
+    for (int i = tid; i < nh * C4; i += blockDim.x) {
+        const int h = i / C4;
+        const int c = i - h * C4;
+        float M = -INFINITY;
+        for (int j = 0; j < np; j++) {
+            const size_t slot = (size_t)(w_first + j) * 2 + (j == 0 ? slot0 : 0);
+            M = fmaxf(M, p.ws_ml[(slot * GT + h) * 2]);
+        }
+        const float Ms = (M == -INFINITY) ? 0.0f : M;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        float den = 0.0f;
+#pragma unroll 4
+        for (int j = 0; j < np; j++) {
+            const size_t slot = (size_t)(w_first + j) * 2 + (j == 0 ? slot0 : 0);
+            const float wgt = fast_exp2(p.ws_ml[(slot * GT + h) * 2] - Ms);
+            den += wgt * p.ws_ml[(slot * GT + h) * 2 + 1];
+            const f32x4 o = *(const f32x4 *)(p.ws_o + (slot * GT + h) * D + c * 4);
+            acc += wgt * o;
+        }
+        const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+        const size_t base = qrow0 + (size_t)h * D + c * 4;
+        store_elem<KV>(p.out, base + 0, acc[0] * inv);
+        store_elem<KV>(p.out, base + 1, acc[1] * inv);
+        store_elem<KV>(p.out, base + 2, acc[2] * inv);
+        store_elem<KV>(p.out, base + 3, acc[3] * inv);
     }
 }
 

@@ -8,15 +8,23 @@
 
 namespace xhip {
 
-// Launches the partition kernel on `grid` workgroups and, when `reduce`, the
-// partition-merge kernel over (num_heads, num_seqs).  head_tile is the query
-// heads per wavefront (1, 2, 4 or 8).  Returns hipErrorInvalidValue for a
-// head_size / head_tile with no instantiation, else the launch status.
-hipError_t launch_decode_f16(const DecodeParams &p, int head_size, int head_tile, unsigned grid,
-                             bool reduce, hipStream_t stream);
-hipError_t launch_decode_bf16(const DecodeParams &p, int head_size, int head_tile, unsigned grid,
-                              bool reduce, hipStream_t stream);
-hipError_t launch_decode_f32(const DecodeParams &p, int head_size, int head_tile, unsigned grid,
-                             bool reduce, hipStream_t stream);
+// Resident workgroups per CU of the partition kernel for this
+// (head_size, head_tile) with `lds_bytes` of dynamic LDS; 0 when there is no
+// such instantiation.
+int partition_occupancy_f16(int head_size, int head_tile, size_t lds_bytes);
+int partition_occupancy_bf16(int head_size, int head_tile, size_t lds_bytes);
+int partition_occupancy_f32(int head_size, int head_tile, size_t lds_bytes);
+
+// Launches the partition kernel on num_waves/kWavesPerGroup workgroups, then
+// the merge kernel over every (sequence, kv head, head tile).  A non-null
+// `after_partition` event is recorded on the stream between the two.
+// Returns hipErrorInvalidValue for a head_size / head_tile with no
+// instantiation, else the launch status.
+hipError_t launch_decode_f16(const DecodeParams &p, int head_size, int head_tile,
+                             hipStream_t stream, hipEvent_t after_partition);
+hipError_t launch_decode_bf16(const DecodeParams &p, int head_size, int head_tile,
+                              hipStream_t stream, hipEvent_t after_partition);
+hipError_t launch_decode_f32(const DecodeParams &p, int head_size, int head_tile,
+                             hipStream_t stream, hipEvent_t after_partition);
 
 }  // namespace xhip

@@ -8,15 +8,24 @@ namespace xhip {
 
 enum KvType : int { KV_F16 = 1, KV_BF16 = 2, KV_F32 = 3 };
 
-// Work decomposition.  One wavefront is one work item
-// (sequence, kv head, head tile, partition): it streams the partition's
-// tokens of that kv head once and serves every query head of its head tile
-// (the whole GQA group when group <= 8).  A workgroup holds kWavesPerGroup
-// items; the head tiles of one (sequence, kv head, partition) are adjacent
-// items, so they share a workgroup and hence the CU's L1 for the same pages.
+// Work decomposition (stream-K over the whole batch).
+//
+// The batch is the sequence of segments (sequence s, kv head, head tile) in
+// that order; segment (s, .) holds T_s = ceil(L_s / tile_tokens) tiles.  All
+// segments laid end to end form `total` tiles.  Wavefront w of the launch owns
+// the contiguous tile range [w*tpw, min((w+1)*tpw, total)) with
+// tpw = max(min_tiles_per_wave, ceil(total / num_waves)), so every
+// wavefront streams the same number of K/V bytes whatever the ragged lengths.
+// A segment that lies inside one wavefront's range is finished there and
+// written straight to the output; a segment cut by range boundaries leaves
+// one fp32 partial (m, l, o) per wavefront that touched it, in that
+// wavefront's slot 0 (the segment holds the wavefront's first tile) or
+// slot 1 (it holds the wavefront's last tile but not its first), and
+// paged_decode_merge_kernel combines them.
 constexpr int kWavesPerGroup = 4;
-constexpr int kMaxHeadTile = 8;   // query heads per wavefront
-constexpr int kLoadsPerTile = 4;  // 16-byte K (and V) loads per lane per tile
+constexpr int kMaxHeadTile = 8;      // query heads per wavefront
+constexpr int kLoadsPerTile = 4;     // 16-byte K (and V) loads per lane per tile
+constexpr int kMaxSeqsPerLaunch = 8192;  // the per-workgroup prefix scan lives in LDS
 
 struct DecodeParams {
     void *out;                 // [num_seqs][num_heads][head_size], element type
@@ -25,8 +34,9 @@ struct DecodeParams {
     const void *v;             // paged V cache
     const int *block_tables;   // [num_seqs][max_blocks]
     const int *seq_lens;       // [num_seqs]
-    float *ws_o;               // [num_seqs*num_heads*max_parts][head_size] fp32
-    float *ws_ml;              // [num_seqs*num_heads*max_parts][2] (max, sum)
+    float *ws_o;               // [num_waves*2][head_tile][head_size] fp32 partial outputs
+    float *ws_ml;              // [num_waves*2][head_tile][2] (running max, running sum)
+    int *ws_prefix;            // [num_seqs + 1] tiles before each sequence (written by wg 0)
     long long kv_block_stride; // elements
     long long kv_head_stride;  // elements
     int num_seqs;
@@ -37,9 +47,9 @@ struct DecodeParams {
     int max_blocks;            // block-table row length
     int block_size;
     int bs_shift;              // log2(block_size)
-    int part_tokens;           // split-K partition length (tokens)
-    int max_parts;             // ceil(max_ctx / part_tokens)
     int max_ctx;               // max_blocks * block_size
+    int num_waves;             // wavefronts of the partition kernel launch
+    int min_tiles_per_wave;    // lower bound of tpw (>= 1)
     float scale_log2;          // scale * log2(e)
 };
 

@@ -109,9 +109,10 @@ def paged_attention(out, query, key_cache, value_cache, block_tables, seq_lens, 
     return status
 
 
-def auto_partition(num_seqs: int, num_heads: int, head_size: int, num_kv_heads: int,
-                   max_num_blocks_per_seq: int, block_size: int, kv_dtype: int) -> int:
-    return _lib.backend().nxt_paged_attention_auto_partition(
+def auto_waves(num_seqs: int, num_heads: int, head_size: int, num_kv_heads: int,
+               max_num_blocks_per_seq: int, block_size: int, kv_dtype: int) -> int:
+    """Wavefronts the automatic stream-K plan launches for this shape."""
+    return _lib.backend().nxt_paged_attention_auto_waves(
         num_seqs, num_heads, head_size, num_kv_heads, max_num_blocks_per_seq, block_size, kv_dtype)
 
 

@@ -348,7 +348,7 @@ def make(config: int, **kw) -> Workload:
 
 def small_case(*, num_seqs=3, H=8, KVH=2, D=128, bs=16, kv_dtype=FP16, lens=None, seed=7,
                pool_factor=2, poison=True, max_len=200) -> Workload:
-    """Small randomized case for parity tests (seconds on the CPU oracle)."""
+    """Small randomized case for the parity tests (seconds on the CPU checker)."""
     rng = np.random.default_rng(seed)
     if lens is None:
         lens = rng.integers(1, max_len, size=num_seqs, endpoint=True)
