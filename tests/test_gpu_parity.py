@@ -80,6 +80,20 @@ def test_split_k_partition_independent(cuda, part):
     assert np.abs(got - whole).max() <= 2e-3
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("head_size", [32, 64, 80, 256])
+def test_split_k_every_tile_path(cuda, dtype, head_size):
+    """Sequences cut into many pieces (small per-wavefront ranges) on every
+    tile path and tile length: the merge must use the same range
+    arithmetic as the partition kernel."""
+    wl = W.small_case(num_seqs=5, H=8, KVH=2, D=head_size, kv_dtype=DT[dtype], seed=head_size,
+                      lens=[0, 1, 63, 700, 1500])
+    ref = oracle(wl)
+    for part in (64, 128, 1024):
+        print(f"case d={head_size} {dtype} partition={part}", flush=True)
+        assert_close(run_gpu(wl, partition_tokens=part), ref, wl.kv_dtype, f"part={part}")
+
+
 # --------------------------------------------------------- entry points
 def test_entry_points_identical(cuda):
     """nxt_paged_attention, _v2 and _flash (operator_api.h:63-115) are one

@@ -133,9 +133,16 @@ int ilog2(int x) {
 
 int elem_bytes(int kv_dtype) { return kv_dtype == NXT_KV_FP32 ? 4 : 2; }
 
-// Tokens per tile of the kernel instantiation (kLoadsPerTile loads of
-// 64/lanes-per-row rows); mirrors xhip::Geometry.
-int tile_tokens(int head_size, int kv_dtype) {
+// The MFMA tile path serves fp16/bf16 with head_size % 32 == 0 and pages of
+// at least one 16-token tile; every other shape takes the VALU tile path.
+bool use_mfma(int kv_dtype, int head_size, int block_size) {
+    return kv_dtype != NXT_KV_FP32 && head_size % 32 == 0 && block_size >= 16;
+}
+
+// Tokens per tile of the kernel instantiation: 16 on the MFMA path, else
+// kLoadsPerTile loads of 64/lanes-per-row rows (mirrors xhip::Geometry).
+int tile_tokens(int head_size, int kv_dtype, bool mfma) {
+    if (mfma) return 16;
     const int vec = 16 / elem_bytes(kv_dtype);
     const int row_lanes = pow2_ceil(head_size / vec);
     return (64 / row_lanes) * xhip::kLoadsPerTile;
@@ -146,8 +153,13 @@ struct HeadTiling {
     int head_tiles;  // wavefronts per (seq, kv head, partition)
 };
 
-bool head_tiling(int group, HeadTiling *t) {
-    if (group <= 0) return false;
+bool head_tiling(int group, bool mfma, HeadTiling *t) {
+    if (group <= 0 || group > xhip::kMaxHeadTile * xhip::kWavesPerGroup) return false;
+    if (mfma) {
+        t->head_tile = xhip::kMfmaHeads;
+        t->head_tiles = (group + xhip::kMfmaHeads - 1) / xhip::kMfmaHeads;
+        return true;
+    }
     if (group <= xhip::kMaxHeadTile) {
         t->head_tile = pow2_ceil(group);
         t->head_tiles = 1;
@@ -162,21 +174,21 @@ bool head_tiling(int group, HeadTiling *t) {
 // below this the per-range setup (prefix lookup, Q load, merge) dominates.
 constexpr int kMinTilesPerWave = 4;
 
-int partition_occupancy(int kv_dtype, int head_size, int head_tile, size_t lds) {
+int partition_occupancy(int kv_dtype, int head_size, int head_tile, bool mfma, size_t lds) {
     switch (kv_dtype) {
-    case NXT_KV_FP16: return xhip::partition_occupancy_f16(head_size, head_tile, lds);
-    case NXT_KV_BF16: return xhip::partition_occupancy_bf16(head_size, head_tile, lds);
-    default: return xhip::partition_occupancy_f32(head_size, head_tile, lds);
+    case NXT_KV_FP16: return xhip::partition_occupancy_f16(head_size, head_tile, mfma, lds);
+    case NXT_KV_BF16: return xhip::partition_occupancy_bf16(head_size, head_tile, mfma, lds);
+    default: return xhip::partition_occupancy_f32(head_size, head_tile, mfma, lds);
     }
 }
 
 // Wavefronts of the automatic plan: one resident round of the partition
 // kernel on every CU, but no more than the batch could keep busy with
 // kMinTilesPerWave tiles each.
-long long auto_waves(int kv_dtype, int head_size, int head_tile, int nseq, long long ub_tiles,
-                     int cus) {
+long long auto_waves(int kv_dtype, int head_size, int head_tile, bool mfma, int nseq,
+                     long long ub_tiles, int cus) {
     const size_t lds = (size_t)(nseq + 1) * sizeof(int);
-    const int occ = partition_occupancy(kv_dtype, head_size, head_tile, lds);
+    const int occ = partition_occupancy(kv_dtype, head_size, head_tile, mfma, lds);
     if (occ <= 0) return 0;
     long long w = (long long)cus * occ * xhip::kWavesPerGroup;
     const long long need = (ub_tiles + kMinTilesPerWave - 1) / kMinTilesPerWave;
@@ -232,8 +244,9 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
     if (max_ctx > (1LL << 28))
         return set_status(NXT_ATTN_E_UNSUPPORTED, "context bound %lld tokens too large", max_ctx);
     const int group = num_heads / num_kv_heads;
+    const bool mfma = use_mfma(kv_dtype, head_size, block_size);
     HeadTiling tiling;
-    if (!head_tiling(group, &tiling))
+    if (!head_tiling(group, mfma, &tiling))
         return set_status(NXT_ATTN_E_UNSUPPORTED, "GQA group %d > %d", group,
                           xhip::kMaxHeadTile * xhip::kWavesPerGroup);
     if (num_seqs == 0) return ok();
@@ -247,7 +260,7 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
     if ((uintptr_t)block_tables & 3 || (uintptr_t)seq_lens & 3)
         return set_status(NXT_ATTN_E_INVALID, "int32 tables must be 4-byte aligned");
 
-    const int tile = tile_tokens(head_size, kv_dtype);
+    const int tile = tile_tokens(head_size, kv_dtype, mfma);
     if (partition_tokens != 0 && (!is_pow2(partition_tokens) || partition_tokens < tile))
         return set_status(NXT_ATTN_E_UNSUPPORTED,
                           "partition_tokens %d must be a power of two >= %d for head_size %d %s",
@@ -270,7 +283,7 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         long long waves;
         int min_tpw;
         if (partition_tokens == 0) {
-            waves = auto_waves(kv_dtype, head_size, tiling.head_tile, nseq, ub_tiles, cus);
+            waves = auto_waves(kv_dtype, head_size, tiling.head_tile, mfma, nseq, ub_tiles, cus);
             if (waves <= 0)
                 return set_status(NXT_ATTN_E_HIP, "no occupancy for head_size %d %s", head_size,
                                   dtype_name(kv_dtype));
@@ -329,13 +342,16 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         }
         switch (kv_dtype) {
         case NXT_KV_FP16:
-            e = xhip::launch_decode_f16(p, head_size, tiling.head_tile, stream, t_trace_partition);
+            e = xhip::launch_decode_f16(p, head_size, tiling.head_tile, mfma, stream,
+                                        t_trace_partition);
             break;
         case NXT_KV_BF16:
-            e = xhip::launch_decode_bf16(p, head_size, tiling.head_tile, stream, t_trace_partition);
+            e = xhip::launch_decode_bf16(p, head_size, tiling.head_tile, mfma, stream,
+                                         t_trace_partition);
             break;
         default:
-            e = xhip::launch_decode_f32(p, head_size, tiling.head_tile, stream, t_trace_partition);
+            e = xhip::launch_decode_f32(p, head_size, tiling.head_tile, mfma, stream,
+                                        t_trace_partition);
             break;
         }
         if (e != hipSuccess)
@@ -417,15 +433,17 @@ __attribute__((visibility("default"))) int nxt_paged_attention_auto_waves(
         !supported_head_size(head_size) || max_num_blocks_per_seq <= 0 || block_size <= 0 ||
         (kv_dtype != NXT_KV_FP16 && kv_dtype != NXT_KV_BF16 && kv_dtype != NXT_KV_FP32))
         return NXT_ATTN_E_INVALID;
+    if (!is_pow2(block_size)) return NXT_ATTN_E_UNSUPPORTED;
+    const bool mfma = use_mfma(kv_dtype, head_size, block_size);
     HeadTiling tiling;
-    if (!head_tiling(num_heads / num_kv_heads, &tiling)) return NXT_ATTN_E_UNSUPPORTED;
+    if (!head_tiling(num_heads / num_kv_heads, mfma, &tiling)) return NXT_ATTN_E_UNSUPPORTED;
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess) return NXT_ATTN_E_HIP;
     const int nseq = num_seqs < xhip::kMaxSeqsPerLaunch ? num_seqs : xhip::kMaxSeqsPerLaunch;
-    const int tile = tile_tokens(head_size, kv_dtype);
+    const int tile = tile_tokens(head_size, kv_dtype, mfma);
     const long long ub = (long long)nseq * num_kv_heads * tiling.head_tiles *
                          (((long long)max_num_blocks_per_seq * block_size + tile - 1) / tile);
-    const long long w = auto_waves(kv_dtype, head_size, tiling.head_tile, nseq, ub,
+    const long long w = auto_waves(kv_dtype, head_size, tiling.head_tile, mfma, nseq, ub,
                                    cu_count(device));
     return w > 0 ? (int)w : NXT_ATTN_E_HIP;
 }

@@ -3,13 +3,13 @@
 
 namespace xhip {
 
-int partition_occupancy_f32(int head_size, int head_tile, size_t lds_bytes) {
-    return occupancy_for_dtype<KV_F32>(head_size, head_tile, lds_bytes);
+int partition_occupancy_f32(int head_size, int head_tile, bool mfma, size_t lds_bytes) {
+    return occupancy_for_dtype<KV_F32>(head_size, head_tile, mfma, lds_bytes);
 }
 
-hipError_t launch_decode_f32(const DecodeParams &p, int head_size, int head_tile,
+hipError_t launch_decode_f32(const DecodeParams &p, int head_size, int head_tile, bool mfma,
                              hipStream_t stream, hipEvent_t after_partition) {
-    return launch_for_dtype<KV_F32>(p, head_size, head_tile, stream, after_partition);
+    return launch_for_dtype<KV_F32>(p, head_size, head_tile, mfma, stream, after_partition);
 }
 
 }  // namespace xhip

@@ -412,22 +412,14 @@ __device__ __forceinline__ void batch_prefix(const DecodeParams &p, int *pre) {
     }
 }
 
-// Partition kernel: kWavesPerGroup wavefronts per workgroup, each owning one
-// stream-K range of tiles (see paged_decode_params.h).
-template <int KV, int D, int GT>
-__global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_kernel(
-    const DecodeParams p) {
-    using Geo = Geometry<KV, D>;
-    constexpr int VEC = Geo::kVec;
-    constexpr int EB = Geo::kElemBytes;
-    constexpr int NCH = Geo::kChunks;
-    constexpr int RL = Geo::kRowLanes;
-    constexpr int TT = Geo::kTileTokens;
-    extern __shared__ int pre[];  // num_seqs + 1 tile prefixes
-
+// Walk this wavefront's stream-K range: for every segment piece in it call
+// fn(s, L, kvh, ht, t_begin, t_end, whole, slot) where [t_begin, t_end) are
+// the piece's tokens, `whole` says the piece is the entire segment (write the
+// output) and `slot` is the partial slot otherwise.  `pre` is the LDS tile
+// prefix (num_seqs + 1 ints); every thread of the workgroup must call this.
+template <int TT, typename Fn>
+__device__ __forceinline__ void stream_k_walk(const DecodeParams &p, int *pre, Fn &&fn) {
     batch_prefix<TT>(p, pre);
-
-    const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int w = blockIdx.x * kWavesPerGroup + wave;
     const int B = p.num_seqs;
@@ -446,13 +438,8 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
         if (pre[mid] <= g) lo = mid; else hi = mid - 1;
     }
     int s = __builtin_amdgcn_readfirstlane(lo);
-
-    const int col = lane % RL;
-    const int row = lane / RL;
-    const bool col_ok = (NCH == RL) || (col < NCH);
     const int segs = p.num_kv_heads * p.head_tiles;
     bool first = true;
-
     while (g < g_end) {
         const int L = seq_len_of(p, s);
         const int Ts = (L + TT - 1) / TT;  // tiles per segment of sequence s
@@ -462,6 +449,38 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
         const int n = min(Ts - t0, g_end - g);
         const int kvh = seg / p.head_tiles;
         const int ht = seg - kvh * p.head_tiles;
+        fn(s, L, kvh, ht, t0 * TT, min(L, (t0 + n) * TT), t0 == 0 && n == Ts,
+           (size_t)w * 2 + (first ? 0 : 1));
+        g += n;
+        first = false;
+        if (g - pre[s] >= Ts * segs) {  // sequence done: next one with tiles
+            s++;
+            while (s < B - 1 && pre[s + 1] == pre[s]) s++;
+        }
+    }
+}
+
+// Partition kernel, VALU tile path: kWavesPerGroup wavefronts per workgroup,
+// each owning one stream-K range of tiles (see paged_decode_params.h).
+template <int KV, int D, int GT>
+__global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_kernel(
+    const DecodeParams p) {
+    using Geo = Geometry<KV, D>;
+    constexpr int VEC = Geo::kVec;
+    constexpr int EB = Geo::kElemBytes;
+    constexpr int NCH = Geo::kChunks;
+    constexpr int RL = Geo::kRowLanes;
+    constexpr int TT = Geo::kTileTokens;
+    extern __shared__ int pre[];  // num_seqs + 1 tile prefixes
+
+    const int lane = threadIdx.x & 63;
+    const int col = lane % RL;
+    const int row = lane / RL;
+    const bool col_ok = (NCH == RL) || (col < NCH);
+
+    stream_k_walk<TT>(p, pre, [&](int s, int L, int kvh, int ht, int t_begin, int t_end,
+                                  bool whole, size_t slot) {
+        (void)L;
         const int g0 = ht * GT;
         const int nh = min(GT, p.group - g0);
         const size_t qrow0 = ((size_t)s * p.num_heads + (size_t)kvh * p.group + g0) * D;
@@ -477,8 +496,6 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
 #pragma unroll
             for (int e = 0; e < VEC; e++) st.o[h][e] = 0.0f;
         }
-        const int t_begin = t0 * TT;
-        const int t_end = min(L, (t0 + n) * TT);
         const int *bt = p.block_tables + (size_t)s * p.max_blocks;
         const char *kb = (const char *)p.k + (size_t)kvh * (size_t)p.kv_head_stride * EB;
         const char *vb = (const char *)p.v + (size_t)kvh * (size_t)p.kv_head_stride * EB;
@@ -506,53 +523,45 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
             }
         }
 
-        if (row == 0 && col_ok) {
-            if (t0 == 0 && n == Ts) {  // whole segment in this range: final output
+        if (row != 0 || !col_ok) return;
+        if (whole) {
 #pragma unroll
-                for (int h = 0; h < GT; h++) {
-                    if (h >= nh) continue;
-                    const float inv = st.l[h] > 0.0f ? 1.0f / st.l[h] : 0.0f;
-                    float f[VEC];
+            for (int h = 0; h < GT; h++) {
+                if (h >= nh) continue;
+                const float inv = st.l[h] > 0.0f ? 1.0f / st.l[h] : 0.0f;
+                float f[VEC];
 #pragma unroll
-                    for (int e = 0; e < VEC; e++) f[e] = st.o[h][e] * inv;
-                    *(u32x4 *)((char *)p.out + (qrow0 + (size_t)h * D + col * VEC) * EB) =
-                        float_to_chunk<KV, VEC>(f);
-                }
-            } else {  // cut segment: partial into this wavefront's slot
-                const size_t slot = (size_t)w * 2 + (first ? 0 : 1);
+                for (int e = 0; e < VEC; e++) f[e] = st.o[h][e] * inv;
+                *(u32x4 *)((char *)p.out + (qrow0 + (size_t)h * D + col * VEC) * EB) =
+                    float_to_chunk<KV, VEC>(f);
+            }
+        } else {
 #pragma unroll
-                for (int h = 0; h < GT; h++) {
-                    if (h >= nh) continue;
-                    float *dst = p.ws_o + (slot * GT + h) * D + col * VEC;
+            for (int h = 0; h < GT; h++) {
+                if (h >= nh) continue;
+                float *dst = p.ws_o + (slot * GT + h) * D + col * VEC;
 #pragma unroll
-                    for (int e = 0; e < VEC; e += 4)
-                        *(f32x4 *)(dst + e) =
-                            f32x4{st.o[h][e], st.o[h][e + 1], st.o[h][e + 2], st.o[h][e + 3]};
-                    if (col == 0) {
-                        p.ws_ml[(slot * GT + h) * 2] = st.m[h];
-                        p.ws_ml[(slot * GT + h) * 2 + 1] = st.l[h];
-                    }
+                for (int e = 0; e < VEC; e += 4)
+                    *(f32x4 *)(dst + e) =
+                        f32x4{st.o[h][e], st.o[h][e + 1], st.o[h][e + 2], st.o[h][e + 3]};
+                if (col == 0) {
+                    p.ws_ml[(slot * GT + h) * 2] = st.m[h];
+                    p.ws_ml[(slot * GT + h) * 2 + 1] = st.l[h];
                 }
             }
         }
-        g += n;
-        first = false;
-        if (g - pre[s] >= Ts * segs) {  // sequence done: next one with tiles
-            s++;
-            while (s < B - 1 && pre[s + 1] == pre[s]) s++;
-        }
-    }
+    });
 }
 
 // Merge kernel: one workgroup per segment (sequence, kv head, head tile).
 // Writes zeros for an empty sequence, does nothing for a segment finished
 // inside one wavefront range, and otherwise combines the partials of every
 // wavefront that touched the segment.  Thread (h, c) owns four output
-// columns 4c..4c+3 of head h of the tile.
-template <int KV, int D, int GT>
+// columns 4c..4c+3 of head h of the tile.  TT is the tile length (tokens) of
+// the partition kernel that produced the partials: the range arithmetic must
+// match it exactly.
+template <int KV, int D, int GT, int TT>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeParams p) {
-    using Geo = Geometry<KV, D>;
-    constexpr int TT = Geo::kTileTokens;
     constexpr int C4 = D / 4;
     const int segs = p.num_kv_heads * p.head_tiles;
     const int s = blockIdx.x / segs;

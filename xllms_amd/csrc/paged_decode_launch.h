@@ -9,22 +9,23 @@
 namespace xhip {
 
 // Resident workgroups per CU of the partition kernel for this
-// (head_size, head_tile) with `lds_bytes` of dynamic LDS; 0 when there is no
-// such instantiation.
-int partition_occupancy_f16(int head_size, int head_tile, size_t lds_bytes);
-int partition_occupancy_bf16(int head_size, int head_tile, size_t lds_bytes);
-int partition_occupancy_f32(int head_size, int head_tile, size_t lds_bytes);
+// (head_size, head_tile, tile path) with `lds_bytes` of dynamic LDS; 0 when
+// there is no such instantiation.  mfma selects the MFMA tile path (16-bit
+// types, head_size % 32 == 0, head_tile 16).
+int partition_occupancy_f16(int head_size, int head_tile, bool mfma, size_t lds_bytes);
+int partition_occupancy_bf16(int head_size, int head_tile, bool mfma, size_t lds_bytes);
+int partition_occupancy_f32(int head_size, int head_tile, bool mfma, size_t lds_bytes);
 
 // Launches the partition kernel on num_waves/kWavesPerGroup workgroups, then
 // the merge kernel over every (sequence, kv head, head tile).  A non-null
 // `after_partition` event is recorded on the stream between the two.
 // Returns hipErrorInvalidValue for a head_size / head_tile with no
 // instantiation, else the launch status.
-hipError_t launch_decode_f16(const DecodeParams &p, int head_size, int head_tile,
+hipError_t launch_decode_f16(const DecodeParams &p, int head_size, int head_tile, bool mfma,
                              hipStream_t stream, hipEvent_t after_partition);
-hipError_t launch_decode_bf16(const DecodeParams &p, int head_size, int head_tile,
+hipError_t launch_decode_bf16(const DecodeParams &p, int head_size, int head_tile, bool mfma,
                               hipStream_t stream, hipEvent_t after_partition);
-hipError_t launch_decode_f32(const DecodeParams &p, int head_size, int head_tile,
+hipError_t launch_decode_f32(const DecodeParams &p, int head_size, int head_tile, bool mfma,
                              hipStream_t stream, hipEvent_t after_partition);
 
 }  // namespace xhip

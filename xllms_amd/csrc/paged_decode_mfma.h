@@ -1,0 +1,305 @@
+// MFMA tile path of the paged-decode attention (fp16 / bf16 K/V, head_size a
+// multiple of 32, block_size >= 16).  One wavefront serves up to 16 query
+// heads of one kv head; cost per 16-token tile does not depend on the group.
+//
+// Per 16-token tile (one page when block_size = 16), with g = lane/16 and
+// j = lane%16 (v_mfma_f32_16x16x{32,16} operand layouts, checked on gfx950):
+//   QK^T  S[token][head] = sum_d K[token][d] Q[head][d]
+//         D/32 x v_mfma_f32_16x16x32: A = K rows (lane: token j, dims
+//         32c+8g..+7, a 16-byte load straight from the page), B = Q of the 16
+//         heads (lane: head j, same dims).  C: lane holds S[4g+r][j].
+//   softmax per head j: the 16 scores of head j sit in lanes j, j+16, j+32,
+//         j+48 (4 each): in-lane max, two xor shuffles, exp2, running sum.
+//   PV    O^T[dim][head] += sum_t V[t][dim] P[head][t]
+//         D/16 x v_mfma_f32_16x16x16 (twice: P = P_hi + P_lo in the 16-bit
+//         type, so the product keeps ~22 bits of P): B = P, which is exactly
+//         the C layout of the QK^T step (lane: head j, tokens 4g..4g+3);
+//         A = V^T (lane: dim 16n+j, tokens 4g..4g+3), read from the V tile
+//         staged in LDS.  C: lane holds O^T[16n+4g+r][j].
+// The V tile goes global -> registers -> LDS (row stride 2*D+8 bytes so the
+// four token groups of a V^T read fall in different LDS banks).  Loads are
+// buffer loads: a token past the end of the range, or in a page with a
+// negative id, gets an out-of-range offset and reads as zero without touching
+// memory; its score is masked to -inf.  The next tile's K/V loads are issued
+// before the current tile is computed.
+#pragma once
+
+#include "paged_decode_kernels.h"
+
+namespace xhip {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr uint32_t kOobOffset = 0x80000000u;
+
+template <int D> struct MfmaGeometry {
+    static constexpr int kTile = 16;             // tokens per tile
+    static constexpr int kChunks = D / 8;        // 16-byte chunks per 16-bit row
+    static constexpr int kQkSteps = D / 32;      // QK^T MFMAs = K loads per lane
+    static constexpr int kVLoads = D / 32;       // V 16-byte loads per lane (16 rows)
+    static constexpr int kDimBlocks = D / 16;    // PV MFMAs per P half
+    static constexpr int kLdsRow = 2 * D + 8;    // bytes per staged V row
+    static constexpr int kLdsTile = 16 * kLdsRow;
+    static_assert(D % 32 == 0, "MFMA path needs head_size % 32 == 0");
+};
+
+template <int KV> __device__ __forceinline__ f32x4 mfma_qk(u32x4 a, u32x4 b, f32x4 c) {
+    if constexpr (KV == KV_F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+template <int KV> __device__ __forceinline__ f32x4 mfma_pv(u32x2 a, u32x2 b, f32x4 c) {
+    if constexpr (KV == KV_F16)
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                     __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a),
+                                                         __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+}
+
+// Round fp32 to the 16-bit type (RNE); returns the bits and the rounded value.
+template <int KV> __device__ __forceinline__ uint32_t round16(float x, float &rounded) {
+    if constexpr (KV == KV_F16) {
+        const _Float16 h = (_Float16)x;
+        rounded = (float)h;
+        return (uint32_t)__builtin_bit_cast(uint16_t, h);
+    } else {
+        const uint32_t b = f32_to_bf16_bits(x);
+        rounded = __builtin_bit_cast(float, b << 16);
+        return b;
+    }
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const char *base) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7FFFFFFF, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+}
+
+template <int D> struct MfmaTileRegs {
+    u32x4 k[MfmaGeometry<D>::kQkSteps];
+    u32x4 v[MfmaGeometry<D>::kVLoads];
+};
+
+// Issue the K and V loads of the tile starting at token t0 (block id blk):
+// rows past t_end or in a negative page read as zero.
+template <int D>
+__device__ __forceinline__ void mfma_load_tile(const DecodeParams &p, const char *kb,
+                                               const char *vb, int t0, int t_end, int blk,
+                                               int lane, MfmaTileRegs<D> &r) {
+    using G = MfmaGeometry<D>;
+    const int bmask = p.block_size - 1;
+    const bool page_ok = blk >= 0;
+    const long long page = (long long)blk * p.kv_block_stride + (long long)(t0 & bmask) * D;
+    const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kb + page * 2);
+    const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vb + page * 2);
+    const int j = lane & 15, g = lane >> 4;
+    const bool krow_ok = page_ok && (t0 + j < t_end);
+#pragma unroll
+    for (int c = 0; c < G::kQkSteps; c++)
+        r.k[c] = buf_load16(rk, krow_ok ? (uint32_t)(j * 2 * D + 64 * c + 16 * g) : kOobOffset);
+#pragma unroll
+    for (int c = 0; c < G::kVLoads; c++) {
+        const int q = 64 * c + lane;
+        const int row = q / G::kChunks;
+        const int chunk = q - row * G::kChunks;
+        const bool ok = page_ok && (t0 + row < t_end);
+        r.v[c] = buf_load16(rv, ok ? (uint32_t)(row * 2 * D + 16 * chunk) : kOobOffset);
+    }
+}
+
+// Running state of one wavefront over one segment: lane (g, j) owns head j.
+template <int D> struct MfmaState {
+    f32x4 o[MfmaGeometry<D>::kDimBlocks];  // O^T[16n + 4g + r][j]
+    float m;                               // running max of head j (log2 units)
+    float l;                               // this lane's part of the running sum
+};
+
+template <int KV, int D>
+__device__ __forceinline__ void mfma_tile(const DecodeParams &p, const u32x4 *q, int t0,
+                                          int t_end, bool page_ok, int lane, char *lds,
+                                          const MfmaTileRegs<D> &r, MfmaState<D> &st) {
+    using G = MfmaGeometry<D>;
+    const int j = lane & 15, g = lane >> 4;
+
+    // V tile -> LDS (row-major, padded rows), two 8-byte writes per chunk.
+#pragma unroll
+    for (int c = 0; c < G::kVLoads; c++) {
+        const int qi = 64 * c + lane;
+        const int row = qi / G::kChunks;
+        const int chunk = qi - row * G::kChunks;
+        u32x2 *dst = (u32x2 *)(lds + row * G::kLdsRow + 16 * chunk);
+        dst[0] = u32x2{r.v[c][0], r.v[c][1]};
+        dst[1] = u32x2{r.v[c][2], r.v[c][3]};
+    }
+
+    // S = K Q^T for 16 tokens x 16 heads.
+    f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < G::kQkSteps; c++) s = mfma_qk<KV>(r.k[c], q[c], s);
+
+    // Online softmax of head j over tokens 4g..4g+3 of this lane.
+    float sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const bool ok = page_ok && (t0 + 4 * g + i < t_end);
+        sc[i] = ok ? s[i] * p.scale_log2 : -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(st.m, mx);
+    const float ms = (m_new == -INFINITY) ? 0.0f : m_new;
+    const float alpha = fast_exp2(st.m - ms);
+    float pe[4];
+    float psum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        pe[i] = fast_exp2(sc[i] - ms);
+        psum += pe[i];
+    }
+    st.l = st.l * alpha + psum;
+    st.m = m_new;
+
+    // P in the 16-bit type as hi + lo parts (B operand of the PV MFMA).
+    uint32_t hb[4], lb[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float hv, lv;
+        hb[i] = round16<KV>(pe[i], hv);
+        lb[i] = round16<KV>(pe[i] - hv, lv);
+    }
+    const u32x2 p_hi = {hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
+    const u32x2 p_lo = {lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
+
+#pragma unroll
+    for (int n = 0; n < G::kDimBlocks; n++) st.o[n] *= alpha;
+
+    // O^T += V^T P for every 16-dim block.
+    const char *vrow = lds + (4 * g) * G::kLdsRow + 2 * j;
+#pragma unroll
+    for (int n = 0; n < G::kDimBlocks; n++) {
+        const char *src = vrow + 32 * n;
+        const uint32_t v0 = *(const uint16_t *)(src);
+        const uint32_t v1 = *(const uint16_t *)(src + G::kLdsRow);
+        const uint32_t v2 = *(const uint16_t *)(src + 2 * G::kLdsRow);
+        const uint32_t v3 = *(const uint16_t *)(src + 3 * G::kLdsRow);
+        const u32x2 a = {v0 | (v1 << 16), v2 | (v3 << 16)};
+        st.o[n] = mfma_pv<KV>(a, p_hi, st.o[n]);
+        st.o[n] = mfma_pv<KV>(a, p_lo, st.o[n]);
+    }
+}
+
+// Stream tokens [t_begin, t_end) of one segment through the MFMA tiles.
+template <int KV, int D>
+__device__ __forceinline__ void mfma_segment(const DecodeParams &p, const int *bt, const char *kb,
+                                             const char *vb, int t_begin, int t_end, int lane,
+                                             char *lds, const u32x4 *q, MfmaState<D> &st) {
+    const int ntiles = (t_end - t_begin + 15) >> 4;
+    // Block ids of up to 64 tiles at a time, one per lane (vector loads, so
+    // the tile loop issues no scalar memory traffic).
+    int ids = 0;
+    MfmaTileRegs<D> ra, rb;
+    int blk_a = 0;
+    for (int i = 0; i < ntiles; i++) {
+        if ((i & 63) == 0) {
+            const int ti = t_begin + 16 * (i + lane);
+            ids = bt[(ti < t_end ? ti : t_end - 1) >> p.bs_shift];
+            if (i == 0) {
+                blk_a = __builtin_amdgcn_readlane(ids, 0);
+                mfma_load_tile<D>(p, kb, vb, t_begin, t_end, blk_a, lane, ra);
+            }
+        }
+        const int t0 = t_begin + 16 * i;
+        // Prefetch tile i+1 (all rows out of range past the segment end).
+        const int nl = (i + 1) & 63;
+        int blk_b = (i + 1 < ntiles && nl != 0) ? __builtin_amdgcn_readlane(ids, nl) : -1;
+        if (i + 1 < ntiles && nl == 0) {
+            const int ti = t0 + 16;
+            blk_b = bt[ti >> p.bs_shift];
+        }
+        mfma_load_tile<D>(p, kb, vb, t0 + 16, t_end, blk_b, lane, rb);
+        mfma_tile<KV, D>(p, q, t0, t_end, blk_a >= 0, lane, lds, ra, st);
+        ra = rb;
+        blk_a = blk_b;
+    }
+}
+
+}  // namespace xhip
+
+namespace xhip {
+
+// Partition kernel, MFMA tile path (head tile of 16 query heads).
+template <int KV, int D>
+__global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_mfma_kernel(
+    const DecodeParams p) {
+    using G = MfmaGeometry<D>;
+    constexpr int GT = kMfmaHeads;
+    extern __shared__ int pre[];  // num_seqs + 1 tile prefixes
+    __shared__ __attribute__((aligned(16))) char vtile[kWavesPerGroup][G::kLdsTile];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    char *lds = vtile[wave];
+    const int j = lane & 15, gq = lane >> 4;
+
+    stream_k_walk<16>(p, pre, [&](int s, int L, int kvh, int ht, int t_begin, int t_end,
+                                  bool whole, size_t slot) {
+        (void)L;
+        const int g0 = ht * GT;
+        const int nh = min(GT, p.group - g0);
+        const size_t qrow0 = ((size_t)s * p.num_heads + (size_t)kvh * p.group + g0) * D;
+        u32x4 q[G::kQkSteps];
+#pragma unroll
+        for (int c = 0; c < G::kQkSteps; c++)
+            q[c] = (j < nh) ? load16((const char *)p.q + (qrow0 + (size_t)j * D + 32 * c + 8 * gq) * 2)
+                            : u32x4{0, 0, 0, 0};
+        MfmaState<D> st;
+#pragma unroll
+        for (int n = 0; n < G::kDimBlocks; n++) st.o[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        st.m = -INFINITY;
+        st.l = 0.0f;
+        const int *bt = p.block_tables + (size_t)s * p.max_blocks;
+        const char *kb = (const char *)p.k + (size_t)kvh * (size_t)p.kv_head_stride * 2;
+        const char *vb = (const char *)p.v + (size_t)kvh * (size_t)p.kv_head_stride * 2;
+        mfma_segment<KV, D>(p, bt, kb, vb, t_begin, t_end, lane, lds, q, st);
+
+        float l = st.l;
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+        if (j >= nh) return;
+        if (whole) {
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            char *dst = (char *)p.out + (qrow0 + (size_t)j * D + 4 * gq) * 2;
+#pragma unroll
+            for (int n = 0; n < G::kDimBlocks; n++) {
+                float f0, f1, f2, f3;
+                const uint32_t b0 = round16<KV>(st.o[n][0] * inv, f0);
+                const uint32_t b1 = round16<KV>(st.o[n][1] * inv, f1);
+                const uint32_t b2 = round16<KV>(st.o[n][2] * inv, f2);
+                const uint32_t b3 = round16<KV>(st.o[n][3] * inv, f3);
+                *(u32x2 *)(dst + 32 * n) = u32x2{b0 | (b1 << 16), b2 | (b3 << 16)};
+            }
+        } else {
+            float *dst = p.ws_o + (slot * GT + j) * D + 4 * gq;
+#pragma unroll
+            for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st.o[n];
+            if (gq == 0) {
+                p.ws_ml[(slot * GT + j) * 2] = st.m;
+                p.ws_ml[(slot * GT + j) * 2 + 1] = l;
+            }
+        }
+    });
+}
+
+}  // namespace xhip
