@@ -94,6 +94,23 @@ def test_split_k_every_tile_path(cuda, dtype, head_size):
         assert_close(run_gpu(wl, partition_tokens=part), ref, wl.kv_dtype, f"part={part}")
 
 
+def test_back_to_back_launches_reuse_counters(cuda):
+    """The in-kernel merge counters are left at zero by every launch: many
+    launches of different shapes on one stream (one shared workspace), each
+    checked, with repeats of the same shape in between."""
+    cases = [W.small_case(num_seqs=6, H=32, KVH=8, D=128, kv_dtype=W.FP16, seed=90 + i,
+                          max_len=2500) for i in range(3)]
+    cases.append(W.small_case(num_seqs=3, H=16, KVH=1, D=64, kv_dtype=W.BF16, seed=99,
+                              max_len=3000))
+    refs = [oracle(wl) for wl in cases]
+    for rep in range(3):
+        for i, (wl, ref) in enumerate(zip(cases, refs)):
+            for part in (0, 64):
+                print(f"case rep={rep} shape={i} partition={part}", flush=True)
+                assert_close(run_gpu(wl, partition_tokens=part), ref, wl.kv_dtype,
+                             f"rep {rep} case {i} part {part}")
+
+
 # --------------------------------------------------------- entry points
 def test_entry_points_identical(cuda):
     """nxt_paged_attention, _v2 and _flash (operator_api.h:63-115) are one

@@ -43,7 +43,10 @@ static hipError_t launch_merge(const DecodeParams &p, hipStream_t st, hipEvent_t
         if (e != hipSuccess) return e;
     }
     const unsigned segs = (unsigned)(p.num_seqs * p.num_kv_heads * p.head_tiles);
-    paged_decode_merge_kernel<KV, D, GT, TT><<<segs, 256, 0, st>>>(p);
+    const int heads = p.group < GT ? p.group : GT;
+    const unsigned chunks = (unsigned)((heads * (D / 4) + kMergeCols - 1) / kMergeCols);
+    paged_decode_merge_kernel<KV, D, GT, TT>
+        <<<dim3(segs, chunks), kMergeCols * kMergeSplit, 0, st>>>(p);
     return hipGetLastError();
 }
 

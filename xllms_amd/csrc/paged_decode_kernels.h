@@ -553,16 +553,26 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
     });
 }
 
-// Merge kernel: one workgroup per segment (sequence, kv head, head tile).
-// Writes zeros for an empty sequence, does nothing for a segment finished
-// inside one wavefront range, and otherwise combines the partials of every
-// wavefront that touched the segment.  Thread (h, c) owns four output
-// columns 4c..4c+3 of head h of the tile.  TT is the tile length (tokens) of
-// the partition kernel that produced the partials: the range arithmetic must
-// match it exactly.
+// Merge kernel: one workgroup per (segment, chunk of kMergeCols output
+// float4 columns), where a segment is (sequence, kv head, head tile) and the
+// columns run over (head h < nh, dims 4c..4c+3).  It writes zeros for an
+// empty sequence, does nothing for a segment finished inside one wavefront
+// range, and otherwise combines the partials of every wavefront that touched
+// the segment in one pass: each of the kMergeSplit threads of a column runs
+// an online log-sum-exp merge over every kMergeSplit-th partial (running max,
+// rescaled denominator and float4 numerator), and the splits are combined in
+// LDS the same way.  TT is the tile length (tokens) of the partition kernel
+// that produced the partials: the range arithmetic must match it exactly.
+constexpr int kMergeCols = 32;
+constexpr int kMergeSplit = 8;
+
 template <int KV, int D, int GT, int TT>
-__global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeParams p) {
+__global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_kernel(
+    const DecodeParams p) {
     constexpr int C4 = D / 4;
+    __shared__ f32x4 s_acc[kMergeSplit][kMergeCols];
+    __shared__ float s_m[kMergeSplit][kMergeCols];
+    __shared__ float s_l[kMergeSplit][kMergeCols];
     const int segs = p.num_kv_heads * p.head_tiles;
     const int s = blockIdx.x / segs;
     const int seg = blockIdx.x - s * segs;
@@ -570,12 +580,19 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodePar
     const int ht = seg - kvh * p.head_tiles;
     const int g0 = ht * GT;
     const int nh = min(GT, p.group - g0);
+    const int ncols = nh * C4;
+    const int col0 = blockIdx.y * kMergeCols;
+    if (col0 >= ncols) return;
     const int tid = threadIdx.x;
     const int L = seq_len_of(p, s);
     const size_t qrow0 = ((size_t)s * p.num_heads + (size_t)kvh * p.group + g0) * D;
 
     if (L == 0) {
-        for (int i = tid; i < nh * D; i += blockDim.x) store_elem<KV>(p.out, qrow0 + i, 0.0f);
+        if (tid < kMergeCols && col0 + tid < ncols) {
+            const size_t base = qrow0 + (size_t)(col0 + tid) * 4;  // head-major columns
+#pragma unroll
+            for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, 0.0f);
+        }
         return;
     }
     const int total = p.ws_prefix[p.num_seqs];
@@ -587,33 +604,51 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodePar
     if (w_first == w_last) return;
     const int np = w_last - w_first + 1;
     const int slot0 = (seg_start == w_first * tpw) ? 0 : 1;
+    // partial j of the segment lives in slot (w_first + j)*2 + (j == 0 ? slot0 : 0)
+    const size_t sbase = (size_t)w_first * 2;
 
-    for (int i = tid; i < nh * C4; i += blockDim.x) {
-        const int h = i / C4;
-        const int c = i - h * C4;
-        float M = -INFINITY;
-        for (int j = 0; j < np; j++) {
-            const size_t slot = (size_t)(w_first + j) * 2 + (j == 0 ? slot0 : 0);
-            M = fmaxf(M, p.ws_ml[(slot * GT + h) * 2]);
-        }
-        const float Ms = (M == -INFINITY) ? 0.0f : M;
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        float den = 0.0f;
+    const int cl = tid % kMergeCols;
+    const int ps = tid / kMergeCols;
+    const int col = col0 + cl;
+    const bool active = col < ncols;
+    const int h = active ? col / C4 : 0;
+    const int c = col - h * C4;
+    float m = -INFINITY, l = 0.0f;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (active) {
 #pragma unroll 4
-        for (int j = 0; j < np; j++) {
-            const size_t slot = (size_t)(w_first + j) * 2 + (j == 0 ? slot0 : 0);
-            const float wgt = fast_exp2(p.ws_ml[(slot * GT + h) * 2] - Ms);
-            den += wgt * p.ws_ml[(slot * GT + h) * 2 + 1];
+        for (int jj = ps; jj < np; jj += kMergeSplit) {
+            const size_t slot = sbase + 2 * jj + (jj == 0 ? slot0 : 0);
+            const float mj = p.ws_ml[(slot * GT + h) * 2];
+            const float lj = p.ws_ml[(slot * GT + h) * 2 + 1];
             const f32x4 o = *(const f32x4 *)(p.ws_o + (slot * GT + h) * D + c * 4);
-            acc += wgt * o;
+            const float M = fmaxf(m, mj);
+            const float Ms = (M == -INFINITY) ? 0.0f : M;
+            const float a = fast_exp2(m - Ms), b = fast_exp2(mj - Ms);
+            l = l * a + lj * b;
+            acc = acc * a + o * b;
+            m = M;
         }
-        const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-        const size_t base = qrow0 + (size_t)h * D + c * 4;
-        store_elem<KV>(p.out, base + 0, acc[0] * inv);
-        store_elem<KV>(p.out, base + 1, acc[1] * inv);
-        store_elem<KV>(p.out, base + 2, acc[2] * inv);
-        store_elem<KV>(p.out, base + 3, acc[3] * inv);
     }
+    s_acc[ps][cl] = acc;
+    s_m[ps][cl] = m;
+    s_l[ps][cl] = l;
+    __syncthreads();
+    if (ps != 0 || !active) return;
+#pragma unroll
+    for (int k = 1; k < kMergeSplit; k++) {
+        const float mk = s_m[k][cl];
+        const float M = fmaxf(m, mk);
+        const float Ms = (M == -INFINITY) ? 0.0f : M;
+        const float a = fast_exp2(m - Ms), b = fast_exp2(mk - Ms);
+        l = l * a + s_l[k][cl] * b;
+        acc = acc * a + s_acc[k][cl] * b;
+        m = M;
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const size_t base = qrow0 + (size_t)h * D + c * 4;
+#pragma unroll
+    for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, acc[e] * inv);
 }
 
 }  // namespace xhip
