@@ -88,6 +88,15 @@ def load_traffic(workload_name: str):
     return d.get("hbm_bytes_per_launch")
 
 
+def partition_kernel_name(wl) -> str:
+    """Kernel that streams K/V for this workload: the MFMA tile kernel serves
+    fp16/bf16 pages with head_size % 32 == 0 and block_size >= 16, the VALU
+    tile kernel everything else (same rule as use_mfma in paged_decode_api.cpp)."""
+    from xllms_amd import workloads as W
+    mfma = wl.kv_dtype != W.FP32 and wl.head_size % 32 == 0 and wl.block_size >= 16
+    return "paged_decode_partition_mfma_kernel" if mfma else "paged_decode_partition_kernel"
+
+
 def cpu_baseline(wl, budget_s: float) -> dict:
     """Time the oracle on the host: all threads, then one thread, each on as
     many whole copies of the batch (or leading sequences) as fit the budget."""
@@ -284,7 +293,7 @@ def main() -> int:
         "logical_bytes": logical_bytes,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": "paged_decode_partition_kernel",
+                     "traffic": traffic, "kernel": partition_kernel_name(wl),
                      "kernel_avg_us": round(kernel_avg_ms * 1e3, 2)},
         "cpu_baseline": cpu,
         "check": check,
