@@ -94,6 +94,35 @@ def test_split_k_every_tile_path(cuda, dtype, head_size):
         assert_close(run_gpu(wl, partition_tokens=part), ref, wl.kv_dtype, f"part={part}")
 
 
+@pytest.mark.parametrize("shape", [
+    # (H, KVH, D, dtype, num_seqs): >= 512 segments, so the merge runs one
+    # workgroup per segment; float4 columns per segment 128 (two threads per
+    # column split the partials), 512 and 1024 (threads own 2 / 4 columns),
+    # and the VALU head tiles of 8 query heads (one and four per kv head).
+    (32, 8, 128, "fp16", 64),
+    (64, 4, 128, "bf16", 128),
+    (32, 2, 256, "fp16", 256),
+    (64, 8, 64, "fp32", 64),
+    (64, 2, 64, "fp32", 64),
+])
+def test_merge_per_segment_paths(cuda, shape):
+    """Batches with enough segments merge with one workgroup per segment:
+    every column layout of that merge, with empty sequences and segments cut
+    into many partials."""
+    H, KVH, D, dtype, nseq = shape
+    rng = np.random.default_rng(H * D + KVH)
+    lens = rng.integers(1, 700, size=nseq)
+    lens[::17] = 0
+    lens[5] = 1
+    wl = W.small_case(num_seqs=nseq, H=H, KVH=KVH, D=D, kv_dtype=DT[dtype], seed=H + D,
+                      lens=lens.tolist())
+    ref = oracle(wl)
+    for part in (0, 64):
+        print(f"case H={H} KVH={KVH} d={D} {dtype} seqs={nseq} partition={part}", flush=True)
+        assert_close(run_gpu(wl, partition_tokens=part), ref, wl.kv_dtype,
+                     f"H={H} KVH={KVH} d={D} part={part}")
+
+
 def test_back_to_back_launches_reuse_counters(cuda):
     """The in-kernel merge counters are left at zero by every launch: many
     launches of different shapes on one stream (one shared workspace), each

@@ -334,6 +334,10 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         p.num_waves = (int)waves;
         p.min_tiles_per_wave = min_tpw;
         p.scale_log2 = scale * 1.4426950408889634f;
+        // One merge workgroup per segment once the segments alone fill two
+        // workgroups per CU; fewer, longer segments (few sequences, long
+        // contexts) take the (segment, column chunk) merge grid.
+        p.merge_per_segment = (long long)nseq * segs >= 2LL * cus ? 1 : 0;
 
         if (t_trace_start) {
             e = hipEventRecord(t_trace_start, stream);

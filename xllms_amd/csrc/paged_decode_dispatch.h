@@ -43,6 +43,10 @@ static hipError_t launch_merge(const DecodeParams &p, hipStream_t st, hipEvent_t
         if (e != hipSuccess) return e;
     }
     const unsigned segs = (unsigned)(p.num_seqs * p.num_kv_heads * p.head_tiles);
+    if (p.merge_per_segment) {
+        paged_decode_merge_segment_kernel<KV, D, GT, TT><<<segs, kMergeSegThreads, 0, st>>>(p);
+        return hipGetLastError();
+    }
     const int heads = p.group < GT ? p.group : GT;
     const unsigned chunks = (unsigned)((heads * (D / 4) + kMergeCols - 1) / kMergeCols);
     paged_decode_merge_kernel<KV, D, GT, TT>

@@ -657,4 +657,112 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
     for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, acc[e] * inv);
 }
 
+
+// Merge kernel, one workgroup per segment: for batches with enough segments
+// to fill the GPU (where the (segment, chunk) grid above would launch several
+// thousand short workgroups, each costing ~2 ns of dispatch).  The 256
+// threads cover the segment's ncols float4 columns: with ncols >= 256 each
+// thread owns columns t, t + 256, ...; with fewer, the S = 256 / pow2(ncols)
+// threads of a column split its partials (every S-th one) and combine in LDS.
+// Each thread runs the online log-sum-exp merge with four partials' loads in
+// flight.
+constexpr int kMergeSegThreads = 256;
+
+template <int KV, int D, int GT, int TT>
+__global__ __launch_bounds__(kMergeSegThreads) void paged_decode_merge_segment_kernel(
+    const DecodeParams p) {
+    constexpr int C4 = D / 4;
+    constexpr int KC = (GT * C4 + kMergeSegThreads - 1) / kMergeSegThreads;
+    __shared__ f32x4 s_acc[kMergeSegThreads];
+    __shared__ float s_m[kMergeSegThreads];
+    __shared__ float s_l[kMergeSegThreads];
+    const int segs = p.num_kv_heads * p.head_tiles;
+    const int s = blockIdx.x / segs;
+    const int seg = blockIdx.x - s * segs;
+    const int kvh = seg / p.head_tiles;
+    const int g0 = (seg - kvh * p.head_tiles) * GT;
+    const int nh = min(GT, p.group - g0);
+    const int ncols = nh * C4;
+    const int tid = threadIdx.x;
+    const int L = seq_len_of(p, s);
+    const size_t qrow0 = ((size_t)s * p.num_heads + (size_t)kvh * p.group + g0) * D;
+
+    if (L == 0) {
+        for (int col = tid; col < ncols; col += kMergeSegThreads) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) store_elem<KV>(p.out, qrow0 + (size_t)col * 4 + e, 0.0f);
+        }
+        return;
+    }
+    const int total = p.ws_prefix[p.num_seqs];
+    const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);
+    const int Ts = (L + TT - 1) / TT;
+    const int seg_start = p.ws_prefix[s] + seg * Ts;
+    const int w_first = seg_start / tpw;
+    const int w_last = (seg_start + Ts - 1) / tpw;
+    if (w_first == w_last) return;
+    const int np = w_last - w_first + 1;
+    const int slot0 = (seg_start == w_first * tpw) ? 0 : 1;
+    const size_t sbase = (size_t)w_first * 2;
+
+    // Column span per split: all 256 threads when ncols >= 256, else pow2(ncols).
+    int span = kMergeSegThreads;
+    while ((span >> 1) >= ncols) span >>= 1;
+    const int split = tid / span;             // 0 .. S-1
+    const int nsplit = kMergeSegThreads / span;
+    const int cl = tid - split * span;
+
+    float m[KC], l[KC];
+    f32x4 acc[KC];
+#pragma unroll
+    for (int k = 0; k < KC; k++) {
+        m[k] = -INFINITY;
+        l[k] = 0.0f;
+        acc[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        const int col = cl + k * kMergeSegThreads;
+        if (col >= ncols) continue;
+        const int h = col / C4;
+        const int c = col - h * C4;
+#pragma unroll 4
+        for (int j = split; j < np; j += nsplit) {
+            const size_t slot = sbase + 2 * j + (j == 0 ? slot0 : 0);
+            const float mj = p.ws_ml[(slot * GT + h) * 2];
+            const float lj = p.ws_ml[(slot * GT + h) * 2 + 1];
+            const f32x4 o = *(const f32x4 *)(p.ws_o + (slot * GT + h) * D + c * 4);
+            const float M = fmaxf(m[k], mj);
+            const float Ms = (M == -INFINITY) ? 0.0f : M;
+            const float a = fast_exp2(m[k] - Ms), b = fast_exp2(mj - Ms);
+            l[k] = l[k] * a + lj * b;
+            acc[k] = acc[k] * a + o * b;
+            m[k] = M;
+        }
+    }
+    if (nsplit > 1) {  // KC == 1 here: ncols < 256
+        s_acc[tid] = acc[0];
+        s_m[tid] = m[0];
+        s_l[tid] = l[0];
+        __syncthreads();
+        if (split != 0) return;
+        for (int k = 1; k < nsplit; k++) {
+            const int o = k * span + cl;
+            const float mk = s_m[o];
+            const float M = fmaxf(m[0], mk);
+            const float Ms = (M == -INFINITY) ? 0.0f : M;
+            const float a = fast_exp2(m[0] - Ms), b = fast_exp2(mk - Ms);
+            l[0] = l[0] * a + s_l[o] * b;
+            acc[0] = acc[0] * a + s_acc[o] * b;
+            m[0] = M;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < KC; k++) {
+        const int col = cl + k * kMergeSegThreads;
+        if (col >= ncols) continue;
+        const float inv = l[k] > 0.0f ? 1.0f / l[k] : 0.0f;
+        const size_t base = qrow0 + (size_t)col * 4;  // head-major columns
+#pragma unroll
+        for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, acc[k][e] * inv);
+    }
+}
+
 }  // namespace xhip

@@ -52,6 +52,7 @@ struct DecodeParams {
     int num_waves;             // wavefronts of the partition kernel launch
     int min_tiles_per_wave;    // lower bound of tpw (>= 1)
     float scale_log2;          // scale * log2(e)
+    int merge_per_segment;     // 1: merge with one workgroup per segment
 };
 
 }  // namespace xhip
