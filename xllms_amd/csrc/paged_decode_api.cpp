@@ -182,14 +182,21 @@ int partition_occupancy(int kv_dtype, int head_size, int head_tile, bool mfma, s
     }
 }
 
+// Workgroups per CU of the MFMA partition kernel's plan: two (8 wavefronts
+// per CU, 2 per SIMD).  Measured on MI355X against the three that fit: 4-10%
+// less time on configs 2, 3 and 4 (fewer concurrent page streams per HBM
+// channel, and an even finish across wavefronts).
+constexpr int kMfmaGroupsPerCu = 2;
+
 // Wavefronts of the automatic plan: one resident round of the partition
 // kernel on every CU, but no more than the batch could keep busy with
 // kMinTilesPerWave tiles each.
 long long auto_waves(int kv_dtype, int head_size, int head_tile, bool mfma, int nseq,
                      long long ub_tiles, int cus) {
     const size_t lds = (size_t)(nseq + 1) * sizeof(int);
-    const int occ = partition_occupancy(kv_dtype, head_size, head_tile, mfma, lds);
+    int occ = partition_occupancy(kv_dtype, head_size, head_tile, mfma, lds);
     if (occ <= 0) return 0;
+    if (mfma && occ > kMfmaGroupsPerCu) occ = kMfmaGroupsPerCu;
     long long w = (long long)cus * occ * xhip::kWavesPerGroup;
     const long long need = (ub_tiles + kMinTilesPerWave - 1) / kMinTilesPerWave;
     if (need < w) w = need;
