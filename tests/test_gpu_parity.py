@@ -260,6 +260,23 @@ def test_padded_strides(cuda):
     del torch
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
+def test_context_bound_splits_launches(cuda, dtype):
+    """A block table bounding 2^28 tokens per sequence (32 kv heads x 2^24
+    tiles = 2^29 tiles per sequence) exceeds the 2^30 tiles one launch may
+    index: the batch goes in launches of two sequences each, with the same
+    results."""
+    import dataclasses
+    wl = W.small_case(num_seqs=5, H=32, KVH=32, D=64, kv_dtype=DT[dtype], seed=77,
+                      lens=[0, 1, 50, 200, 700])
+    max_blocks = 1 << 24
+    bt = np.full((wl.num_seqs, max_blocks), -1, dtype=np.int32)
+    bt[:, :wl.max_num_blocks_per_seq] = wl.block_tables
+    wl = dataclasses.replace(wl, block_tables=bt)
+    print(f"case {dtype} max_blocks={max_blocks}", flush=True)
+    assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"context bound {dtype}")
+
+
 # ---------------------------------------------------- benchmark configs
 def test_config1_full(cuda):
     wl = W.config1()

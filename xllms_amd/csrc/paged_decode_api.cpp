@@ -204,7 +204,8 @@ long long auto_waves(int kv_dtype, int head_size, int head_tile, bool mfma, int 
     return w > 0 ? w : xhip::kWavesPerGroup;
 }
 
-constexpr long long kMaxWaves = 1LL << 22;  // bounds the partial workspace of explicit plans
+constexpr long long kMaxWaves = 1LL << 22;
+constexpr long long kMaxLaunchTiles = 1LL << 30;  // bounds the partial workspace of explicit plans
 
 const char *dtype_name(int kv_dtype) {
     switch (kv_dtype) {
@@ -281,12 +282,20 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
     const int segs = num_kv_heads * tiling.head_tiles;
     const long long tiles_per_seg = (max_ctx + tile - 1) / tile;
 
-    // Batches beyond kMaxSeqsPerLaunch go in consecutive launches (the
-    // per-workgroup prefix scan of the partition kernel lives in LDS).
-    for (int s0 = 0; s0 < num_seqs; s0 += xhip::kMaxSeqsPerLaunch) {
-        const int nseq = num_seqs - s0 < xhip::kMaxSeqsPerLaunch ? num_seqs - s0
-                                                                 : xhip::kMaxSeqsPerLaunch;
-        const long long ub_tiles = (long long)nseq * segs * tiles_per_seg;
+    // Batches go in consecutive launches of at most kMaxSeqsPerLaunch
+    // sequences (the per-workgroup prefix scan of the partition kernel lives
+    // in LDS) and at most kMaxLaunchTiles tiles by the context bound (tile
+    // indices are 32-bit on the device).
+    const long long seq_tiles = (long long)segs * tiles_per_seg;
+    if (seq_tiles >= kMaxLaunchTiles)
+        return set_status(NXT_ATTN_E_UNSUPPORTED,
+                          "one sequence bounds %lld tiles (kv heads x context); limit %lld",
+                          seq_tiles, kMaxLaunchTiles);
+    const long long fit = kMaxLaunchTiles / seq_tiles;
+    const int per_launch = fit < xhip::kMaxSeqsPerLaunch ? (int)fit : xhip::kMaxSeqsPerLaunch;
+    for (int s0 = 0; s0 < num_seqs; s0 += per_launch) {
+        const int nseq = num_seqs - s0 < per_launch ? num_seqs - s0 : per_launch;
+        const long long ub_tiles = (long long)nseq * seq_tiles;
         long long waves;
         int min_tpw;
         if (partition_tokens == 0) {
