@@ -121,6 +121,94 @@ def cpu_baseline(wl, budget_s: float) -> dict:
     return res
 
 
+def bench_kv_append(args) -> int:
+    """KV append on the workload's shape.  Prefill form: all tokens of the
+    batch (their K/V rows gathered from the pool, so writing them back must
+    leave the pool unchanged: the check) written to their slots; decode form:
+    one new token per sequence.  Algorithmic bytes = rows read + rows written
+    + 4 B per slot."""
+    import numpy as np
+    import torch
+    from xllms_amd import paged_attention as PA
+    from xllms_amd import workloads as W
+
+    wl = W.make(args.config)
+    dw = W.upload(wl)
+    bs, kvh, d = wl.block_size, wl.num_kv_heads, wl.head_size
+    slots = []
+    for s_, L in enumerate(wl.seq_lens):
+        for t in range(int(L)):
+            slots.append(int(wl.block_tables[s_, t // bs]) * bs + t % bs)
+    slots = np.asarray(slots, dtype=np.int32)
+    n = len(slots)
+    sl = torch.from_numpy(slots).cuda()
+    blk = sl.long() // bs
+    off = sl.long() % bs
+    key = dw.key_cache[blk, :, off, :].contiguous()        # [n, kvh, d]
+    value = dw.value_cache[blk, :, off, :].contiguous()
+    k_before = dw.key_cache.clone()
+    v_before = dw.value_cache.clone()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream().cuda_stream
+    lib = PA._lib.backend()
+    a = (dw.key_cache.data_ptr(), dw.value_cache.data_ptr(), key.data_ptr(), value.data_ptr(),
+         sl.data_ptr(), n, kvh, d, bs, wl.kv_block_stride, wl.kv_head_stride, wl.kv_dtype, stream)
+    for _ in range(args.warmup):
+        lib.nxt_paged_kv_write_slots(*a)
+    ev = HipEvents()
+    e0, e1 = ev.create(), ev.create()
+    torch.cuda.synchronize()
+    ev.record(e0, stream)
+    for _ in range(args.steps):
+        lib.nxt_paged_kv_write_slots(*a)
+    ev.record(e1, stream)
+    torch.cuda.synchronize()
+    st, msg = PA.last_status()
+    if st != 0:
+        raise RuntimeError(f"kv append failed: {msg}")
+    ms = ev.elapsed_ms(e0, e1) / args.steps
+    ibits = torch.int32 if wl.kv_dtype == W.FP32 else torch.int16   # the pool holds NaN sentinels
+    unchanged = bool(torch.equal(dw.key_cache.view(ibits), k_before.view(ibits)) and
+                     torch.equal(dw.value_cache.view(ibits), v_before.view(ibits)))
+    row_bytes = kvh * d * wl.elem_bytes
+    alg = 2 * n * row_bytes * 2 + 4 * n
+    gbs = alg / (ms / 1e3) / 1e9
+    # decode step: one token per sequence, at its last position
+    pos = torch.from_numpy((wl.seq_lens - 1).astype(np.int32)).cuda()
+    kd = key[:wl.num_seqs].contiguous()
+    vd = value[:wl.num_seqs].contiguous()
+    ad = (dw.key_cache.data_ptr(), dw.value_cache.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+          dw.block_tables.data_ptr(), pos.data_ptr(), wl.num_seqs, kvh, d,
+          wl.max_num_blocks_per_seq, bs, wl.kv_block_stride, wl.kv_head_stride, wl.kv_dtype, stream)
+    for _ in range(args.warmup):
+        lib.nxt_paged_kv_append(*ad)
+    torch.cuda.synchronize()
+    ev.record(e0, stream)
+    for _ in range(args.steps):
+        lib.nxt_paged_kv_append(*ad)
+    ev.record(e1, stream)
+    torch.cuda.synchronize()
+    dms = ev.elapsed_ms(e0, e1) / args.steps
+    ev.destroy_all()
+    log(f"[bench] kv append: {n} tokens in {ms * 1e3:.1f} us = {gbs:.0f} GB/s "
+        f"({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s); decode step ({wl.num_seqs} tokens) "
+        f"{dms * 1e3:.2f} us; pool unchanged after write-back: {unchanged}")
+    print(json.dumps({
+        "metric": "paged KV append GB/s (prefill form) + decode-step latency",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "higher_is_better": True,
+        "dtype": {W.FP16: "fp16", W.BF16: "bf16", W.FP32: "fp32"}[wl.kv_dtype],
+        "data": "synthetic (rows gathered from the seeded pool)",
+        "config": {"workload": wl.name, "tokens": n, "num_kv_heads": kvh, "head_size": d,
+                   "block_size": bs},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "paged_kv_append_kernel", "kernel_avg_us": round(ms * 1e3, 2)},
+        "decode_step_us": round(dms * 1e3, 2), "decode_tokens": wl.num_seqs,
+        "check": {"pool_unchanged_after_write_back": unchanged}}), flush=True)
+    return 0 if unchanged else 1
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -133,6 +221,10 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-check", action="store_true", help="skip the post-run oracle check")
+    ap.add_argument("--kv-append", action="store_true",
+                    help="instead of the attention, time the KV append on the workload's shape: "
+                         "every token of the batch written through nxt_paged_kv_write_slots "
+                         "(HBM-bound) and one decode step through nxt_paged_kv_append")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run 5 plain device copies of MIB MiB "
                          "(the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -162,6 +254,9 @@ def main() -> int:
 
     from xllms_amd import paged_attention as PA
     from xllms_amd import workloads as W
+
+    if args.kv_append:
+        return bench_kv_append(args)
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)

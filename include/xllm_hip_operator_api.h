@@ -141,6 +141,37 @@ int nxt_attn_release_workspaces(void);
 /* Library version string, e.g. "xllm-hip-attn 0.1.0 gfx950". */
 const char *nxt_attn_version(void);
 
+/* ---------------------------------------------------------- KV append
+ * The step before the decode attention: store the new token's K and V rows
+ * in the paged cache.  The reference has no GPU counterpart; its CPU decode
+ * loop copies the rows into a contiguous cache at position cur_len and then
+ * attends over cur_len + 1 tokens (examples/text_gen.c:1274-1281).  Here
+ * the cache is the operator-API page layout [num_blocks][num_kv_heads]
+ * [block_size][head_size] with the same strides (elements) as
+ * nxt_paged_attention, and the new rows are key / value
+ * [num_tokens][num_kv_heads][head_size] in the cache dtype.  The caller owns
+ * every buffer and guarantees that page ids and slots lie inside the cache.
+ * Asynchronous on `stream`; bytes are copied exactly.  Returns NXT_ATTN_OK
+ * or a negative status (also recorded for nxt_attn_last_status). */
+
+/* Decode: token s (row s of key / value) of sequence s goes to page
+ * block_tables[s][positions[s] / block_size], slot positions[s] %
+ * block_size.  A negative position, a position at or past
+ * max_num_blocks_per_seq * block_size, or a negative page id skips it. */
+int nxt_paged_kv_append(void *key_cache, void *value_cache, const void *key,
+                        const void *value, const int *block_tables, const int *positions,
+                        int num_seqs, int num_kv_heads, int head_size,
+                        int max_num_blocks_per_seq, int block_size, int kv_block_stride,
+                        int kv_head_stride, int kv_dtype, nxt_stream_t stream);
+
+/* Prefill / general: token i goes to flat slot slot_mapping[i] (page =
+ * slot / block_size, offset = slot % block_size); a negative slot skips it. */
+int nxt_paged_kv_write_slots(void *key_cache, void *value_cache, const void *key,
+                             const void *value, const int *slot_mapping, int num_tokens,
+                             int num_kv_heads, int head_size, int block_size,
+                             int kv_block_stride, int kv_head_stride, int kv_dtype,
+                             nxt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

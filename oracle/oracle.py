@@ -50,6 +50,9 @@ def lib() -> ctypes.CDLL:
         L.oracle_half_to_float.restype = cf
         L.oracle_bf16_to_float.argtypes = [ctypes.c_uint16]
         L.oracle_bf16_to_float.restype = cf
+        L.oracle_paged_kv_append.argtypes = [vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ll,
+                                             ll, ci]
+        L.oracle_paged_kv_append.restype = ci
         _lib = L
     return _lib
 
@@ -153,3 +156,34 @@ def widen(bits: np.ndarray, dtype: int) -> np.ndarray:
     if dtype == FP16:
         return bits.view(np.float16).astype(np.float32)
     return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+def paged_kv_append(key_cache: np.ndarray, value_cache: np.ndarray, key: np.ndarray,
+                    value: np.ndarray, *, block_size: int, kv_block_stride: int,
+                    kv_head_stride: int, slots=None, block_tables=None, positions=None):
+    """KV-cache write of text_gen.c:1274-1278 over the paged layout (see
+    oracle_paged_kv_append): returns updated copies of the two caches.
+    key / value: [num_tokens, num_kv_heads, head_size] in the cache dtype
+    (any 2- or 4-byte numpy dtype; bytes are copied unchanged)."""
+    kc = np.array(key_cache, copy=True, order="C")
+    vc = np.array(value_cache, copy=True, order="C")
+    k = _c(key)
+    v = _c(value)
+    n, kvh, d = k.shape
+    if slots is not None:
+        sl = _c(np.asarray(slots, dtype=np.int32))
+        bt = pos = None
+        max_blocks = 0
+    else:
+        sl = None
+        bt = _c(np.asarray(block_tables, dtype=np.int32))
+        pos = _c(np.asarray(positions, dtype=np.int32))
+        max_blocks = bt.shape[1]
+    ptr = lambda a: None if a is None else a.ctypes.data
+    rc = lib().oracle_paged_kv_append(kc.ctypes.data, vc.ctypes.data, k.ctypes.data,
+                                      v.ctypes.data, ptr(sl), ptr(bt), ptr(pos), n, kvh, d,
+                                      max_blocks, block_size, kv_block_stride, kv_head_stride,
+                                      k.dtype.itemsize)
+    if rc != 0:
+        raise ValueError("oracle_paged_kv_append rejected its arguments")
+    return kc, vc

@@ -50,6 +50,20 @@
  *      bit-for-bit against the reference's own compiled function
  *      (oracle/_ref), which pins the fp32 arithmetic order used above.
  *
+ *  oracle_paged_kv_append
+ *      The reference's KV-cache write of one decode step,
+ *      examples/text_gen.c:1274-1278: the new token's K row and V row
+ *      (kv_dim = num_kv_heads * head_dim elements, head-major) are copied
+ *      into the cache at position cur_len.  Restated over the operator-API
+ *      pages: head h of token i goes to block slot/block_size, offset
+ *      slot%block_size, element offset blk*kv_block_stride +
+ *      h*kv_head_stride + off*head_size, bytes copied unchanged.  The slot is
+ *      slots[i] when slots is given (prefill), else
+ *      block_tables[i][positions[i]/block_size]*block_size +
+ *      positions[i]%block_size (decode, token i = sequence i); a negative
+ *      slot / position / page id, or a position at or past
+ *      max_blocks*block_size, skips the token.
+ *
  * Pinning (tests/test_oracle_*.py): the gpt2 restatement is bit-exact against
  * the compiled reference; the paged f32 routine agrees with it on MHA inputs
  * converted between the two layouts, with the f64 closed form, with
@@ -339,4 +353,37 @@ void oracle_gpt2_paged_attention(const float *query, const float *key_cache,
         }
     }
     free(w);
+}
+
+int oracle_paged_kv_append(void *key_cache, void *value_cache, const void *key, const void *value,
+                           const int *slots, const int *block_tables, const int *positions,
+                           int num_tokens, int num_kv_heads, int head_size, int max_blocks,
+                           int block_size, long long kv_block_stride, long long kv_head_stride,
+                           int elem_bytes) {
+    if (num_tokens < 0 || num_kv_heads <= 0 || head_size <= 0 || block_size <= 0 ||
+        (elem_bytes != 2 && elem_bytes != 4))
+        return -1;
+    const size_t row = (size_t)head_size * (size_t)elem_bytes;
+    for (int i = 0; i < num_tokens; i++) {
+        long long slot;
+        if (slots) {
+            slot = slots[i];
+        } else {
+            const int pos = positions[i];
+            if (pos < 0 || (long long)pos >= (long long)max_blocks * block_size) continue;
+            const int blk = block_tables[(size_t)i * (size_t)max_blocks + (size_t)(pos / block_size)];
+            if (blk < 0) continue;
+            slot = (long long)blk * block_size + pos % block_size;
+        }
+        if (slot < 0) continue;
+        const long long blk = slot / block_size, off = slot % block_size;
+        for (int h = 0; h < num_kv_heads; h++) {
+            const size_t dst = (size_t)(blk * kv_block_stride + h * kv_head_stride +
+                                        off * (long long)head_size) * (size_t)elem_bytes;
+            const size_t src = ((size_t)i * (size_t)num_kv_heads + (size_t)h) * row;
+            memcpy((char *)key_cache + dst, (const char *)key + src, row);
+            memcpy((char *)value_cache + dst, (const char *)value + src, row);
+        }
+    }
+    return 0;
 }

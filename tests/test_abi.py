@@ -169,6 +169,36 @@ def test_void_entry_points_record_status():
     assert lib.nxt_attn_last_status() == PA.NXT_ATTN_OK
 
 
+def test_kv_append_validation_without_launch():
+    """The KV-append entry points check their arguments before any device
+    call (these return without touching a GPU)."""
+    lib = _lib.backend()
+    p = 256
+    # decode form: kv_dtype, block_size, head_size, sizes
+    assert lib.nxt_paged_kv_append(p, p, p, p, p, p, 4, 2, 128, 8, 16, 4096, 2048, 9, None) == \
+        PA.NXT_ATTN_E_INVALID
+    assert lib.nxt_paged_kv_append(p, p, p, p, p, p, 4, 2, 128, 8, 12, 4096, 2048, 1, None) == \
+        PA.NXT_ATTN_E_UNSUPPORTED
+    assert lib.nxt_paged_kv_append(p, p, p, p, p, p, 4, 2, 100, 8, 16, 4096, 2048, 1, None) == \
+        PA.NXT_ATTN_E_UNSUPPORTED
+    assert lib.nxt_paged_kv_append(p, p, p, p, p, p, -1, 2, 128, 8, 16, 4096, 2048, 1, None) == \
+        PA.NXT_ATTN_E_INVALID
+    assert lib.nxt_paged_kv_append(p, p, p, p, None, p, 4, 2, 128, 8, 16, 4096, 2048, 1,
+                                   None) == PA.NXT_ATTN_E_INVALID
+    # misaligned cache pointer
+    assert lib.nxt_paged_kv_append(p + 2, p, p, p, p, p, 4, 2, 128, 8, 16, 4096, 2048, 1,
+                                   None) == PA.NXT_ATTN_E_UNSUPPORTED
+    # nothing to do: OK without a device
+    assert lib.nxt_paged_kv_append(None, None, None, None, None, None, 0, 2, 128, 8, 16, 4096,
+                                   2048, 1, None) == PA.NXT_ATTN_OK
+    # slot form
+    assert lib.nxt_paged_kv_write_slots(p, p, p, p, None, 4, 2, 128, 16, 4096, 2048, 1,
+                                        None) == PA.NXT_ATTN_E_INVALID
+    assert lib.nxt_paged_kv_write_slots(p, p, p, p, p, 4, 2, 128, 24, 4096, 2048, 1,
+                                        None) == PA.NXT_ATTN_E_UNSUPPORTED
+    assert PA.last_status()[0] == PA.NXT_ATTN_E_UNSUPPORTED
+
+
 def test_product_never_imports_the_oracle():
     """The product path (package + native sources) has no route to oracle/."""
     pkg = os.path.join(ROOT, "xllms_amd")

@@ -1,0 +1,125 @@
+"""Pins the CPU restatement of the KV-cache write (oracle_paged_kv_append) --
+CPU only.
+
+The reference's decode loop stores the new token's K/V at position cur_len
+and then attends over cur_len + 1 tokens (examples/text_gen.c:1274-1281).
+Pins:
+  1. an independent numpy scatter (fancy indexing through the page table)
+     gives the same bytes, for both the decode (block table + position) and
+     the slot-mapping form, including the skip rules;
+  2. building a paged cache one decode step at a time with the oracle append
+     and attending over cur_len + 1 tokens reproduces attention over the
+     contiguous K/V history (a float64 brute force), i.e. the append puts
+     every token where the paged attention reads it.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from xllms_amd import workloads as W
+
+
+def numpy_scatter(kc, vc, key, value, slots, block_size):
+    kc, vc = kc.copy(), vc.copy()
+    for i, slot in enumerate(slots):
+        if slot < 0:
+            continue
+        blk, off = divmod(int(slot), block_size)
+        kc[blk, :, off, :] = key[i]
+        vc[blk, :, off, :] = value[i]
+    return kc, vc
+
+
+def decode_slots(block_tables, positions, block_size):
+    max_blocks = block_tables.shape[1]
+    out = []
+    for s, pos in enumerate(positions):
+        if pos < 0 or pos >= max_blocks * block_size:
+            out.append(-1)
+            continue
+        blk = block_tables[s, pos // block_size]
+        out.append(-1 if blk < 0 else int(blk) * block_size + pos % block_size)
+    return out
+
+
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+@pytest.mark.parametrize("block_size", [1, 4, 16, 64])
+def test_decode_append_matches_numpy_scatter(dtype, block_size):
+    rng = np.random.default_rng(block_size)
+    nb, kvh, d, B = 64, 3, 32, 9
+    kc = rng.standard_normal((nb, kvh, block_size, d)).astype(dtype)
+    vc = rng.standard_normal((nb, kvh, block_size, d)).astype(dtype)
+    key = rng.standard_normal((B, kvh, d)).astype(dtype)
+    value = rng.standard_normal((B, kvh, d)).astype(dtype)
+    max_blocks = 5
+    bt = rng.permutation(nb)[:B * max_blocks].reshape(B, max_blocks).astype(np.int32)
+    bt[2, 1] = -1
+    positions = rng.integers(0, max_blocks * block_size, size=B).astype(np.int32)
+    positions[0] = -1                             # skipped
+    positions[1] = max_blocks * block_size        # past the table: skipped
+    positions[2] = block_size + 0                 # negative page id: skipped
+    got = O.paged_kv_append(kc, vc, key, value, block_size=block_size,
+                            kv_block_stride=kvh * block_size * d, kv_head_stride=block_size * d,
+                            block_tables=bt, positions=positions)
+    want = numpy_scatter(kc, vc, key, value, decode_slots(bt, positions, block_size), block_size)
+    assert np.array_equal(got[0].view(np.uint8), want[0].view(np.uint8))
+    assert np.array_equal(got[1].view(np.uint8), want[1].view(np.uint8))
+    # the skipped tokens left their would-be slots alone
+    assert np.array_equal(got[0][bt[0]], kc[bt[0]])
+
+
+def test_slot_mapping_matches_numpy_scatter():
+    rng = np.random.default_rng(5)
+    nb, kvh, bs, d, n = 12, 2, 16, 64, 50
+    kc = rng.standard_normal((nb, kvh, bs, d)).astype(np.float16)
+    vc = rng.standard_normal((nb, kvh, bs, d)).astype(np.float16)
+    key = rng.standard_normal((n, kvh, d)).astype(np.float16)
+    value = rng.standard_normal((n, kvh, d)).astype(np.float16)
+    slots = rng.permutation(nb * bs)[:n].astype(np.int32)
+    slots[::7] = -1
+    got = O.paged_kv_append(kc, vc, key, value, block_size=bs, kv_block_stride=kvh * bs * d,
+                            kv_head_stride=bs * d, slots=slots)
+    want = numpy_scatter(kc, vc, key, value, slots, bs)
+    assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+
+
+def test_decode_loop_reproduces_contiguous_attention():
+    """text_gen.c's loop: append at cur_len, attend over cur_len + 1 tokens."""
+    rng = np.random.default_rng(11)
+    H, KVH, d, bs, steps = 4, 2, 32, 4, 23
+    G = H // KVH
+    pages = rng.permutation(16).astype(np.int32)        # one sequence, shuffled pages
+    bt = pages[None, :8]
+    kc = np.full((16, KVH, bs, d), np.nan, dtype=np.float32)   # unwritten slots are NaN
+    vc = kc.copy()
+    hist_k, hist_v = [], []
+    scale = 1.0 / np.sqrt(d)
+    for cur_len in range(steps):
+        k_tok = rng.standard_normal((1, KVH, d)).astype(np.float32)
+        v_tok = rng.standard_normal((1, KVH, d)).astype(np.float32)
+        q = rng.standard_normal((1, H, d)).astype(np.float32)
+        kc, vc = O.paged_kv_append(kc, vc, k_tok, v_tok, block_size=bs,
+                                   kv_block_stride=KVH * bs * d, kv_head_stride=bs * d,
+                                   block_tables=bt, positions=np.array([cur_len], np.int32))
+        hist_k.append(k_tok[0])
+        hist_v.append(v_tok[0])
+        got = O.paged_attention(q, kc, vc, bt, np.array([cur_len + 1], np.int32),
+                                num_kv_heads=KVH, scale=scale, block_size=bs, dtype=W.FP32,
+                                kv_block_stride=KVH * bs * d, kv_head_stride=bs * d)
+        K = np.stack(hist_k).astype(np.float64)          # [L, KVH, d]
+        V = np.stack(hist_v).astype(np.float64)
+        for h in range(H):
+            sc = K[:, h // G] @ q[0, h].astype(np.float64) * scale
+            w = np.exp(sc - sc.max())
+            ref = (w / w.sum()) @ V[:, h // G]
+            np.testing.assert_allclose(got[0, h], ref, rtol=1e-5, atol=1e-6)
+
+
+def test_rejects_bad_arguments():
+    k = np.zeros((1, 1, 8), np.float16)
+    with pytest.raises(ValueError):
+        O.paged_kv_append(np.zeros((1, 1, 4, 8), np.int8), np.zeros((1, 1, 4, 8), np.int8),
+                          k.astype(np.int8), k.astype(np.int8), block_size=4,
+                          kv_block_stride=32, kv_head_stride=32, slots=[0])

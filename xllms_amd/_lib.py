@@ -54,6 +54,8 @@ OPERATOR_SYMBOLS = (
     "nxt_attn_set_trace_events",
     "nxt_attn_release_workspaces",
     "nxt_attn_version",
+    "nxt_paged_kv_append",
+    "nxt_paged_kv_write_slots",
 )
 PLUGIN_SYMBOLS = ("nxt_backend_init", "nxt_backend_run", "nxt_backend_fini", "nxt_backend_run_ex")
 
@@ -82,6 +84,10 @@ def backend() -> ctypes.CDLL:
         lib.nxt_attn_set_trace_events.restype = None
         lib.nxt_attn_version.argtypes = []
         lib.nxt_attn_version.restype = ctypes.c_char_p
+        lib.nxt_paged_kv_append.argtypes = [c_void_p] * 6 + [c_int] * 8 + [c_void_p]
+        lib.nxt_paged_kv_append.restype = c_int
+        lib.nxt_paged_kv_write_slots.argtypes = [c_void_p] * 5 + [c_int] * 7 + [c_void_p]
+        lib.nxt_paged_kv_write_slots.restype = c_int
         lib._xllm_typed = True
     return lib
 

@@ -16,6 +16,7 @@
 
 #include "paged_decode_launch.h"
 #include "paged_decode_params.h"
+#include "paged_kv_append.h"
 #include "xllm_hip_operator_api.h"
 
 namespace {
@@ -380,6 +381,58 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
     return ok();
 }
 
+// KV append (decode: block_tables + positions; prefill: slots).
+int kv_append_run(void *key_cache, void *value_cache, const void *key, const void *value,
+                  const int *slots, const int *block_tables, const int *positions, int num_tokens,
+                  int num_kv_heads, int head_size, int max_num_blocks_per_seq, int block_size,
+                  int kv_block_stride, int kv_head_stride, int kv_dtype, nxt_stream_t stream_handle) {
+    if (kv_dtype != NXT_KV_FP16 && kv_dtype != NXT_KV_BF16 && kv_dtype != NXT_KV_FP32)
+        return set_status(NXT_ATTN_E_INVALID, "kv_dtype %d is not FP16/BF16/FP32", kv_dtype);
+    if (num_tokens < 0 || num_kv_heads <= 0 || block_size <= 0 || kv_block_stride < 0 ||
+        kv_head_stride < 0 || (!slots && max_num_blocks_per_seq <= 0))
+        return set_status(NXT_ATTN_E_INVALID, "bad sizes (tokens %d, kv heads %d, block_size %d)",
+                          num_tokens, num_kv_heads, block_size);
+    if (!supported_head_size(head_size))
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "head_size %d not supported", head_size);
+    if (!is_pow2(block_size) || block_size > 1024)
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "block_size %d is not a power of two <= 1024",
+                          block_size);
+    const long long max_ctx = slots ? 0 : (long long)max_num_blocks_per_seq * block_size;
+    if (max_ctx > (1LL << 28))
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "context bound %lld tokens too large", max_ctx);
+    if (num_tokens == 0) return ok();
+    if (!key_cache || !value_cache || !key || !value || (!slots && (!block_tables || !positions)))
+        return set_status(NXT_ATTN_E_INVALID, "NULL pointer");
+    const int eb = elem_bytes(kv_dtype);
+    const long long bstride = (long long)kv_block_stride * eb, hstride = (long long)kv_head_stride * eb;
+    if (((uintptr_t)key_cache | (uintptr_t)value_cache | (uintptr_t)key | (uintptr_t)value) & 15 ||
+        (bstride & 15) || (hstride & 15))
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "tensors and kv strides must be 16-byte aligned");
+    xhip::KvAppendParams p;
+    memset(&p, 0, sizeof(p));
+    p.key_cache = key_cache;
+    p.value_cache = value_cache;
+    p.key = key;
+    p.value = value;
+    p.slots = slots;
+    p.block_tables = block_tables;
+    p.positions = positions;
+    p.kv_block_stride_bytes = bstride;
+    p.kv_head_stride_bytes = hstride;
+    p.num_tokens = num_tokens;
+    p.num_kv_heads = num_kv_heads;
+    p.row_bytes = head_size * eb;
+    p.row_chunks = p.row_bytes / 16;
+    p.block_size = block_size;
+    p.bs_shift = ilog2(block_size);
+    p.max_blocks = max_num_blocks_per_seq;
+    p.max_ctx = (int)max_ctx;
+    const hipError_t e = xhip::launch_kv_append(p, (hipStream_t)stream_handle);
+    if (e != hipSuccess)
+        return set_status(NXT_ATTN_E_HIP, "kv append launch: %s", hipGetErrorString(e));
+    return ok();
+}
+
 int dtype_from_size(int dtype_size) {
     if (dtype_size == 2) return NXT_KV_FP16;
     if (dtype_size == 4) return NXT_KV_FP32;
@@ -466,6 +519,26 @@ __attribute__((visibility("default"))) int nxt_paged_attention_auto_waves(
     const long long w = auto_waves(kv_dtype, head_size, tiling.head_tile, mfma, nseq, ub,
                                    cu_count(device));
     return w > 0 ? (int)w : NXT_ATTN_E_HIP;
+}
+
+__attribute__((visibility("default"))) int nxt_paged_kv_append(
+    void *key_cache, void *value_cache, const void *key, const void *value,
+    const int *block_tables, const int *positions, int num_seqs, int num_kv_heads, int head_size,
+    int max_num_blocks_per_seq, int block_size, int kv_block_stride, int kv_head_stride,
+    int kv_dtype, nxt_stream_t stream) {
+    return kv_append_run(key_cache, value_cache, key, value, nullptr, block_tables, positions,
+                         num_seqs, num_kv_heads, head_size, max_num_blocks_per_seq, block_size,
+                         kv_block_stride, kv_head_stride, kv_dtype, stream);
+}
+
+__attribute__((visibility("default"))) int nxt_paged_kv_write_slots(
+    void *key_cache, void *value_cache, const void *key, const void *value,
+    const int *slot_mapping, int num_tokens, int num_kv_heads, int head_size, int block_size,
+    int kv_block_stride, int kv_head_stride, int kv_dtype, nxt_stream_t stream) {
+    if (!slot_mapping && num_tokens > 0) return set_status(NXT_ATTN_E_INVALID, "NULL slot_mapping");
+    return kv_append_run(key_cache, value_cache, key, value, slot_mapping, nullptr, nullptr,
+                         num_tokens, num_kv_heads, head_size, 0, block_size, kv_block_stride,
+                         kv_head_stride, kv_dtype, stream);
 }
 
 __attribute__((visibility("default"))) int nxt_attn_last_status(void) { return t_status; }

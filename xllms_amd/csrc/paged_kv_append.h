@@ -1,0 +1,31 @@
+// Launch parameters of the paged KV-append kernel (paged_kv_append.hip).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+namespace xhip {
+
+struct KvAppendParams {
+    void *key_cache;
+    void *value_cache;
+    const void *key;           // [num_tokens][num_kv_heads][row_bytes]
+    const void *value;
+    const int *slots;          // [num_tokens] flat slots, or null: use block_tables + positions
+    const int *block_tables;   // [num_tokens][max_blocks] (decode: token s = sequence s)
+    const int *positions;      // [num_tokens]
+    long long kv_block_stride_bytes;
+    long long kv_head_stride_bytes;
+    int num_tokens;
+    int num_kv_heads;
+    int row_bytes;             // head_size * element bytes, a multiple of 16
+    int row_chunks;            // row_bytes / 16
+    int block_size;            // power of two
+    int bs_shift;
+    int max_blocks;
+    int max_ctx;               // max_blocks * block_size
+};
+
+hipError_t launch_kv_append(const KvAppendParams &p, hipStream_t stream);
+
+}  // namespace xhip

@@ -118,3 +118,42 @@ def auto_waves(num_seqs: int, num_heads: int, head_size: int, num_kv_heads: int,
 
 def release_workspaces() -> int:
     return _lib.backend().nxt_attn_release_workspaces()
+
+
+def paged_kv_append(key_cache, value_cache, key, value, *, block_tables=None, positions=None,
+                    slot_mapping=None, num_kv_heads: int | None = None,
+                    block_size: int | None = None, kv_block_stride: int | None = None,
+                    kv_head_stride: int | None = None, kv_dtype: int | None = None, stream=None,
+                    check: bool = True) -> int:
+    """Store new K/V rows (key / value [num_tokens, num_kv_heads, head_size])
+    in the paged caches: with block_tables + positions (decode: row s is
+    sequence s's token at positions[s]) through nxt_paged_kv_append, or with
+    slot_mapping (flat slot per row) through nxt_paged_kv_write_slots."""
+    lib = _lib.backend()
+    num_tokens, kvh, head_size = key.shape
+    if num_kv_heads is None:
+        num_kv_heads = kvh
+    if block_size is None:
+        block_size = key_cache.shape[2]
+    if kv_block_stride is None:
+        kv_block_stride = key_cache.stride(0)
+    if kv_head_stride is None:
+        kv_head_stride = key_cache.stride(1)
+    if kv_dtype is None:
+        kv_dtype = kv_dtype_of(key_cache)
+    st = _stream_handle(stream)
+    if slot_mapping is not None:
+        status = lib.nxt_paged_kv_write_slots(
+            _ptr(key_cache), _ptr(value_cache), _ptr(key), _ptr(value), _ptr(slot_mapping),
+            num_tokens, num_kv_heads, head_size, block_size, kv_block_stride, kv_head_stride,
+            kv_dtype, st)
+    else:
+        if block_tables is None or positions is None:
+            raise ValueError("need block_tables and positions, or slot_mapping")
+        status = lib.nxt_paged_kv_append(
+            _ptr(key_cache), _ptr(value_cache), _ptr(key), _ptr(value), _ptr(block_tables),
+            _ptr(positions), num_tokens, num_kv_heads, head_size, block_tables.shape[1],
+            block_size, kv_block_stride, kv_head_stride, kv_dtype, st)
+    if check and status != NXT_ATTN_OK:
+        raise PagedAttentionError(status, lib.nxt_attn_last_error().decode())
+    return status
