@@ -221,6 +221,10 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-check", action="store_true", help="skip the post-run oracle check")
+    ap.add_argument("--cascade", action="store_true",
+                    help="prefix-aware decode (nxt_paged_attention_cascade): shared prefixes found "
+                         "once from the block tables (nxt_paged_prefix_groups, outside the timed "
+                         "steps), each step one cascade call")
     ap.add_argument("--kv-append", action="store_true",
                     help="instead of the attention, time the KV append on the workload's shape: "
                          "every token of the batch written through nxt_paged_kv_write_slots "
@@ -292,6 +296,23 @@ def main() -> int:
              wl.head_size, wl.num_kv_heads, ctypes.c_float(wl.scale), wl.max_num_blocks_per_seq,
              wl.block_size, wl.elem_bytes, wl.kv_block_stride, wl.kv_head_stride, stream)
         return a if entry else a + (wl.kv_dtype, args.partition)
+    n_groups = None
+    if args.cascade:
+        # once per batch composition, as a server would: find the shared prefixes
+        pgroup, pblocks, pcount = PA.prefix_groups(dw.block_tables, dw.seq_lens,
+                                                   block_size=wl.block_size)
+        torch.cuda.synchronize()
+        n_groups = int(pcount.cpu()[0])
+        entry = "nxt_paged_attention_cascade"
+        fn = lib.nxt_paged_attention_cascade
+        def args_for(kc, vc):  # noqa: F811
+            return (dw.out.data_ptr(), dw.query.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                    dw.block_tables.data_ptr(), dw.seq_lens.data_ptr(), pgroup.data_ptr(),
+                    pblocks.data_ptr(), max(n_groups, 0), wl.num_seqs, wl.num_heads,
+                    wl.head_size, wl.num_kv_heads, ctypes.c_float(wl.scale),
+                    wl.max_num_blocks_per_seq, wl.block_size, wl.kv_block_stride,
+                    wl.kv_head_stride, wl.kv_dtype, stream)
+        log(f"[bench] cascade: {n_groups} shared-prefix groups found")
     call_args = [args_for(k, v) for k, v in zip(kpools, vpools)]
 
     def step(i: int) -> None:
@@ -312,7 +333,8 @@ def main() -> int:
     wall0 = time.perf_counter()
     ev.record(begin, stream)
     for i in range(args.steps):
-        lib.nxt_attn_set_trace_events(k_start[i], k_done[i])
+        if not args.cascade:
+            lib.nxt_attn_set_trace_events(k_start[i], k_done[i])
         step(args.warmup + i)
     lib.nxt_attn_set_trace_events(None, None)
     ev.record(end, stream)
@@ -322,15 +344,19 @@ def main() -> int:
     if st != 0:
         raise RuntimeError(f"launch failed: {msg}")
     total_ms = ev.elapsed_ms(begin, end)
-    kern_ms = np.array([ev.elapsed_ms(a, b) for a, b in zip(k_start, k_done)])
+    kern_ms = (np.array([total_ms / args.steps]) if args.cascade else
+               np.array([ev.elapsed_ms(a, b) for a, b in zip(k_start, k_done)]))
     ev.destroy_all()
 
     ms_per_step = total_ms / args.steps
-    kernel_avg_ms = float(kern_ms.mean())
+    # A cascade step is several kernels (plan, two partition + merge passes,
+    # combine): its roofline figure uses the whole step.
+    kernel_avg_ms = ms_per_step if args.cascade else float(kern_ms.mean())
     value = wl.num_seqs / (ms_per_step / 1e3)
     achieved = alg_bytes / (kernel_avg_ms / 1e3) / 1e9
     log(f"[bench] {args.steps} steps: {ms_per_step * 1e3:.1f} us/step (wall {wall / args.steps * 1e6:.1f}"
-        f" us), partition kernel {kernel_avg_ms * 1e3:.1f} us avg "
+        f" us), {'cascade step' if args.cascade else 'partition kernel'} "
+        f"{kernel_avg_ms * 1e3:.1f} us avg "
         f"(min {kern_ms.min() * 1e3:.1f}, max {kern_ms.max() * 1e3:.1f}), "
         f"{achieved:.0f} GB/s = {achieved / HBM_PEAK_GBS:.1%} of 8 TB/s, "
         f"step {alg_bytes / (ms_per_step / 1e3) / 1e9:.0f} GB/s")
@@ -382,13 +408,16 @@ def main() -> int:
                    "context_range": [int(wl.seq_lens.min()), int(wl.seq_lens.max())],
                    "split_k": ("stream-K, %d wavefronts" % waves) if args.partition == 0
                    else f"{args.partition} tokens per wavefront", "kv_pools_rotated": pools,
-                   "entry_point": entry or "nxt_paged_attention_ex", "seed": wl.seed},
+                   "entry_point": entry or "nxt_paged_attention_ex", "seed": wl.seed,
+                   **({"prefix_groups": n_groups} if args.cascade else {})},
         "achieved_gbs_step": round(alg_bytes / (ms_per_step / 1e3) / 1e9, 1),
         "algorithmic_bytes": alg_bytes,
         "logical_bytes": logical_bytes,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": partition_kernel_name(wl),
+                     "traffic": None if args.cascade else traffic,
+                     "kernel": ("cascade decode step (plan, prefix and suffix partition + merge, "
+                                "combine)") if args.cascade else partition_kernel_name(wl),
                      "kernel_avg_us": round(kernel_avg_ms * 1e3, 2)},
         "cpu_baseline": cpu,
         "check": check,

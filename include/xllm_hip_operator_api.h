@@ -141,6 +141,42 @@ int nxt_attn_release_workspaces(void);
 /* Library version string, e.g. "xllm-hip-attn 0.1.0 gfx950". */
 const char *nxt_attn_version(void);
 
+/* ------------------------------------------------ prefix-aware (cascade) decode
+ * No counterpart in the reference: its decode reads every sequence's pages
+ * even where sequences share them (radix-shared prefixes,
+ * src/core/prefix_sharing.c).  Same result as nxt_paged_attention_ex (same
+ * arguments and layouts, within the dtype's rounding), but the pages of a
+ * shared prefix are read once per 16 (sequence, query head) rows of the
+ * sequences that share them instead of once per sequence.
+ *   prefix_group[num_seqs]  device int32: group of each sequence, -1 = none
+ *   prefix_blocks[max_groups] device int32: the number of leading pages (full
+ *                           pages, block_size tokens each) that every member
+ *                           of the group has in common, same physical ids.
+ * A sequence whose entry does not fit (group id out of range, a prefix
+ * longer than its table or its length) is decoded without sharing.
+ * max_groups = 0 is the ordinary decode.  num_seqs <= 8192, max_groups <=
+ * num_seqs.  Allocates (once, per stream) a workspace for its plan and the
+ * fp32 pass outputs; asynchronous on `stream`. */
+int nxt_paged_attention_cascade(void *out, const void *query, const void *key_cache,
+                                const void *value_cache, const int *block_tables,
+                                const int *seq_lens, const int *prefix_group,
+                                const int *prefix_blocks, int max_groups, int num_seqs,
+                                int num_heads, int head_size, int num_kv_heads, float scale,
+                                int max_num_blocks_per_seq, int block_size, int kv_block_stride,
+                                int kv_head_stride, int kv_dtype, nxt_stream_t stream);
+
+/* Finds the shared prefixes of a batch from its block tables, for callers
+ * without a radix tree: sequences whose first page is the same physical
+ * page form a group (two or more members); the group's prefix_blocks is the
+ * longest run of leading pages all members share with its lowest-numbered
+ * member, counting pages full in both.  Writes prefix_group[num_seqs],
+ * prefix_blocks[] and *num_groups (device memory; ids < num_seqs / 2 + 1,
+ * numbered by lowest member).  num_seqs <= 4096.  Meant to run once per
+ * batch composition, not per decode step. */
+int nxt_paged_prefix_groups(const int *block_tables, const int *seq_lens, int num_seqs,
+                            int max_num_blocks_per_seq, int block_size, int *prefix_group,
+                            int *prefix_blocks, int *num_groups, nxt_stream_t stream);
+
 /* ---------------------------------------------------------- KV append
  * The step before the decode attention: store the new token's K and V rows
  * in the paged cache.  The reference has no GPU counterpart; its CPU decode

@@ -56,6 +56,8 @@ OPERATOR_SYMBOLS = (
     "nxt_attn_version",
     "nxt_paged_kv_append",
     "nxt_paged_kv_write_slots",
+    "nxt_paged_attention_cascade",
+    "nxt_paged_prefix_groups",
 )
 PLUGIN_SYMBOLS = ("nxt_backend_init", "nxt_backend_run", "nxt_backend_fini", "nxt_backend_run_ex")
 
@@ -88,6 +90,12 @@ def backend() -> ctypes.CDLL:
         lib.nxt_paged_kv_append.restype = c_int
         lib.nxt_paged_kv_write_slots.argtypes = [c_void_p] * 5 + [c_int] * 7 + [c_void_p]
         lib.nxt_paged_kv_write_slots.restype = c_int
+        lib.nxt_paged_attention_cascade.argtypes = ([c_void_p] * 8 + [c_int] * 5 + [c_float] +
+                                                    [c_int] * 5 + [c_void_p])
+        lib.nxt_paged_attention_cascade.restype = c_int
+        lib.nxt_paged_prefix_groups.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p,
+                                                c_void_p, c_void_p, c_void_p]
+        lib.nxt_paged_prefix_groups.restype = c_int
         lib._xllm_typed = True
     return lib
 

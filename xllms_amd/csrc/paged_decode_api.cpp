@@ -14,6 +14,7 @@
 #include <mutex>
 #include <vector>
 
+#include "paged_decode_cascade.h"
 #include "paged_decode_launch.h"
 #include "paged_decode_params.h"
 #include "paged_kv_append.h"
@@ -47,9 +48,13 @@ int ok() {
 struct Workspace {
     int device;
     hipStream_t stream;
+    int kind;  // kWsSplitK: split-K partials; kWsCascade: cascade plan and pass outputs
     void *ptr;
     size_t bytes;
 };
+
+constexpr int kWsSplitK = 0;
+constexpr int kWsCascade = 1;
 
 std::mutex g_ws_mu;
 std::vector<Workspace> g_ws;
@@ -57,10 +62,10 @@ std::vector<Workspace> g_ws;
 // Returns a workspace of at least `bytes` for (device, stream).  Growing one
 // waits for the stream first, so no kernel still in flight on it can touch
 // the old buffer.
-int get_workspace(int device, hipStream_t stream, size_t bytes, void **out) {
+int get_workspace(int device, hipStream_t stream, size_t bytes, void **out, int kind = kWsSplitK) {
     std::lock_guard<std::mutex> lock(g_ws_mu);
     for (Workspace &w : g_ws) {
-        if (w.device != device || w.stream != stream) continue;
+        if (w.device != device || w.stream != stream || w.kind != kind) continue;
         if (w.bytes >= bytes) {
             *out = w.ptr;
             return NXT_ATTN_OK;
@@ -81,7 +86,7 @@ int get_workspace(int device, hipStream_t stream, size_t bytes, void **out) {
         *out = w.ptr;
         return NXT_ATTN_OK;
     }
-    Workspace w{device, stream, nullptr, 0};
+    Workspace w{device, stream, kind, nullptr, 0};
     hipError_t e = hipMalloc(&w.ptr, bytes);
     if (e != hipSuccess)
         return set_status(NXT_ATTN_E_NOMEM, "split-K workspace of %zu bytes: %s", bytes,
@@ -217,11 +222,19 @@ const char *dtype_name(int kv_dtype) {
     }
 }
 
+// Partial-output mode of a pass (cascade decode): fp32 rows + log-sum-exp
+// instead of `out`, and the K/V load policy.
+struct PartialOut {
+    float *out_f32;
+    float *out_lse;
+    int cached_seqs;  // leading sequences whose K/V loads are cacheable
+};
+
 int run(void *out, const void *query, const void *key_cache, const void *value_cache,
         const int *block_tables, const int *seq_lens, int num_seqs, int num_heads, int head_size,
         int num_kv_heads, float scale, int max_num_blocks_per_seq, int block_size, int dtype_size,
         int kv_block_stride, int kv_head_stride, nxt_stream_t stream_handle, int kv_dtype,
-        int partition_tokens) {
+        int partition_tokens, const PartialOut *po = nullptr) {
     // ---- argument checks (host only; nothing is read from the device)
     if (kv_dtype != NXT_KV_FP16 && kv_dtype != NXT_KV_BF16 && kv_dtype != NXT_KV_FP32)
         return set_status(NXT_ATTN_E_UNSUPPORTED, "kv_dtype %d is not FP16/BF16/FP32", kv_dtype);
@@ -259,10 +272,13 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         return set_status(NXT_ATTN_E_UNSUPPORTED, "GQA group %d > %d", group,
                           xhip::kMaxHeadTile * xhip::kWavesPerGroup);
     if (num_seqs == 0) return ok();
-    if (!out || !query || !key_cache || !value_cache || !block_tables || !seq_lens)
+    const void *out_any = po ? (const void *)po->out_f32 : out;
+    if (!out_any || !query || !key_cache || !value_cache || !block_tables || !seq_lens ||
+        (po && !po->out_lse))
         return set_status(NXT_ATTN_E_INVALID, "NULL tensor pointer");
     const int eb = elem_bytes(kv_dtype);
-    if (((uintptr_t)out | (uintptr_t)query | (uintptr_t)key_cache | (uintptr_t)value_cache) & 15)
+    if (((uintptr_t)out_any | (uintptr_t)query | (uintptr_t)key_cache | (uintptr_t)value_cache) &
+        15)
         return set_status(NXT_ATTN_E_UNSUPPORTED, "tensors must be 16-byte aligned");
     if ((((long long)kv_block_stride * eb) & 15) || (((long long)kv_head_stride * eb) & 15))
         return set_status(NXT_ATTN_E_UNSUPPORTED, "kv strides must be multiples of 16 bytes");
@@ -328,7 +344,12 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         const size_t row0 = (size_t)s0 * num_heads * head_size * eb_total;
         DecodeParams p;
         memset(&p, 0, sizeof(p));
-        p.out = (char *)out + row0;
+        p.out = out ? (char *)out + row0 : nullptr;
+        if (po) {
+            p.out_f32 = po->out_f32 + (size_t)s0 * num_heads * head_size;
+            p.out_lse = po->out_lse + (size_t)s0 * num_heads;
+            p.cached_seqs = po->cached_seqs > s0 ? po->cached_seqs - s0 : 0;
+        }
         p.q = (const char *)query + row0;
         p.k = key_cache;
         p.v = value_cache;
@@ -378,6 +399,123 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         if (e != hipSuccess)
             return set_status(NXT_ATTN_E_HIP, "kernel launch: %s", hipGetErrorString(e));
     }
+    return ok();
+}
+
+// ------------------------------------------------------------ cascade decode
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int cascade_run(void *out, const void *query, const void *key_cache, const void *value_cache,
+                const int *block_tables, const int *seq_lens, const int *prefix_group,
+                const int *prefix_blocks, int max_groups, int num_seqs, int num_heads,
+                int head_size, int num_kv_heads, float scale, int max_num_blocks_per_seq,
+                int block_size, int kv_block_stride, int kv_head_stride, int kv_dtype,
+                nxt_stream_t stream_handle) {
+    if (max_groups < 0) return set_status(NXT_ATTN_E_INVALID, "max_groups %d < 0", max_groups);
+    const int eb = (kv_dtype == NXT_KV_FP16 || kv_dtype == NXT_KV_BF16) ? 2 : 4;
+    if (max_groups == 0 || num_seqs <= 0)  // nothing shared: the ordinary decode
+        return run(out, query, key_cache, value_cache, block_tables, seq_lens, num_seqs, num_heads,
+                   head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size, eb,
+                   kv_block_stride, kv_head_stride, stream_handle, kv_dtype, 0);
+    if (!prefix_group || !prefix_blocks)
+        return set_status(NXT_ATTN_E_INVALID, "NULL prefix_group / prefix_blocks");
+    if (num_seqs > xhip::kMaxSeqsPerLaunch || max_groups > num_seqs)
+        return set_status(NXT_ATTN_E_UNSUPPORTED,
+                          "cascade batch of %d sequences / %d groups (limits %d, num_seqs)",
+                          num_seqs, max_groups, xhip::kMaxSeqsPerLaunch);
+    if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads || !out ||
+        max_num_blocks_per_seq <= 0 || !is_pow2(block_size))
+        return set_status(NXT_ATTN_E_INVALID, "bad cascade arguments");
+    const int group = num_heads / num_kv_heads;
+    const int rows = (group + xhip::kCascadeRows - 1) / xhip::kCascadeRows * xhip::kCascadeRows;
+    const long long v_max = ((long long)num_seqs * group + rows - 1) / rows + max_groups;
+    const size_t mb = (size_t)max_num_blocks_per_seq;
+    const size_t KR = (size_t)num_kv_heads * rows;
+    if (v_max > xhip::kMaxSeqsPerLaunch)
+        return set_status(NXT_ATTN_E_UNSUPPORTED,
+                          "cascade prefix batch of %lld sequences (limit %d): fewer sequences "
+                          "or groups per call",
+                          v_max, xhip::kMaxSeqsPerLaunch);
+    // workspace layout (each piece 256-byte aligned)
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += align256(bytes);
+        return o;
+    };
+    const size_t o_gc = take(4 * (size_t)max_groups), o_gf = take(4 * (size_t)max_groups),
+                 o_gv = take(4 * (size_t)max_groups), o_gm = take(4 * (size_t)max_groups),
+                 o_ms = take(4 * (size_t)num_seqs), o_rk = take(4 * (size_t)num_seqs),
+                 o_vg = take(4 * (size_t)v_max), o_vl = take(4 * (size_t)v_max),
+                 o_vb = take(4 * (size_t)v_max * mb),
+                 o_vq = take((size_t)v_max * KR * head_size * eb),
+                 o_sl = take(4 * (size_t)num_seqs), o_sb = take(4 * (size_t)num_seqs * mb),
+                 o_po = take(4 * (size_t)v_max * KR * head_size), o_pl = take(4 * (size_t)v_max * KR),
+                 o_so = take(4 * (size_t)num_seqs * num_heads * head_size),
+                 o_sls = take(4 * (size_t)num_seqs * num_heads);
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return set_status(NXT_ATTN_E_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    hipStream_t stream = (hipStream_t)stream_handle;
+    void *ws = nullptr;
+    int st = get_workspace(device, stream, off, &ws, kWsCascade);
+    if (st != NXT_ATTN_OK) return st;
+    char *w = (char *)ws;
+    xhip::CascadeParams c;
+    memset(&c, 0, sizeof(c));
+    c.block_tables = block_tables;
+    c.seq_lens = seq_lens;
+    c.q = query;
+    c.out = out;
+    c.prefix_group = prefix_group;
+    c.prefix_blocks = prefix_blocks;
+    c.num_seqs = num_seqs;
+    c.num_heads = num_heads;
+    c.num_kv_heads = num_kv_heads;
+    c.group = group;
+    c.head_size = head_size;
+    c.elem_bytes = eb;
+    c.kv_dtype = kv_dtype;
+    c.max_blocks = max_num_blocks_per_seq;
+    c.block_size = block_size;
+    c.max_ctx = (int)((long long)max_num_blocks_per_seq * block_size);
+    c.max_groups = max_groups;
+    c.rows = rows;
+    c.v_max = (int)v_max;
+    c.g_count = (int *)(w + o_gc);
+    c.g_first = (int *)(w + o_gf);
+    c.g_vbase = (int *)(w + o_gv);
+    c.g_moff = (int *)(w + o_gm);
+    c.member_seq = (int *)(w + o_ms);
+    c.rank = (int *)(w + o_rk);
+    c.v_group = (int *)(w + o_vg);
+    c.v_lens = (int *)(w + o_vl);
+    c.v_bt = (int *)(w + o_vb);
+    c.v_q = w + o_vq;
+    c.s_lens = (int *)(w + o_sl);
+    c.s_bt = (int *)(w + o_sb);
+    c.p_out = (const float *)(w + o_po);
+    c.p_lse = (const float *)(w + o_pl);
+    c.s_out = (const float *)(w + o_so);
+    c.s_lse = (const float *)(w + o_sls);
+    // plan -> prefix pass (R gathered query rows per kv head, cacheable K/V:
+    // the rows of a group read the same pages) -> suffix pass -> combine
+    e = xhip::launch_cascade_plan(c, stream);
+    if (e != hipSuccess)
+        return set_status(NXT_ATTN_E_HIP, "cascade plan launch: %s", hipGetErrorString(e));
+    const PartialOut pre{(float *)(w + o_po), (float *)(w + o_pl), (int)v_max};
+    st = run(nullptr, c.v_q, key_cache, value_cache, c.v_bt, c.v_lens, (int)v_max,
+             num_kv_heads * rows, head_size, num_kv_heads, scale, max_num_blocks_per_seq,
+             block_size, eb, kv_block_stride, kv_head_stride, stream_handle, kv_dtype, 0, &pre);
+    if (st != NXT_ATTN_OK) return st;
+    const PartialOut suf{(float *)(w + o_so), (float *)(w + o_sls), 0};
+    st = run(nullptr, query, key_cache, value_cache, c.s_bt, c.s_lens, num_seqs, num_heads,
+             head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size, eb,
+             kv_block_stride, kv_head_stride, stream_handle, kv_dtype, 0, &suf);
+    if (st != NXT_ATTN_OK) return st;
+    e = xhip::launch_cascade_combine(c, stream);
+    if (e != hipSuccess)
+        return set_status(NXT_ATTN_E_HIP, "cascade combine launch: %s", hipGetErrorString(e));
     return ok();
 }
 
@@ -539,6 +677,49 @@ __attribute__((visibility("default"))) int nxt_paged_kv_write_slots(
     return kv_append_run(key_cache, value_cache, key, value, slot_mapping, nullptr, nullptr,
                          num_tokens, num_kv_heads, head_size, 0, block_size, kv_block_stride,
                          kv_head_stride, kv_dtype, stream);
+}
+
+__attribute__((visibility("default"))) int nxt_paged_attention_cascade(
+    void *out, const void *query, const void *key_cache, const void *value_cache,
+    const int *block_tables, const int *seq_lens, const int *prefix_group,
+    const int *prefix_blocks, int max_groups, int num_seqs, int num_heads, int head_size,
+    int num_kv_heads, float scale, int max_num_blocks_per_seq, int block_size,
+    int kv_block_stride, int kv_head_stride, int kv_dtype, nxt_stream_t stream) {
+    // the ordinary path's argument checks, without launching anything
+    const int eb = (kv_dtype == NXT_KV_FP16 || kv_dtype == NXT_KV_BF16) ? 2 : 4;
+    int st = run(out, query, key_cache, value_cache, block_tables, seq_lens, 0, num_heads,
+                 head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size, eb,
+                 kv_block_stride, kv_head_stride, stream, kv_dtype, 0);
+    if (st != NXT_ATTN_OK) return st;
+    if (num_seqs < 0) return set_status(NXT_ATTN_E_INVALID, "num_seqs %d < 0", num_seqs);
+    if (num_seqs == 0) return ok();
+    if (((uintptr_t)out | (uintptr_t)query) & 15)
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "tensors must be 16-byte aligned");
+    return cascade_run(out, query, key_cache, value_cache, block_tables, seq_lens, prefix_group,
+                       prefix_blocks, max_groups, num_seqs, num_heads, head_size, num_kv_heads,
+                       scale, max_num_blocks_per_seq, block_size, kv_block_stride,
+                       kv_head_stride, kv_dtype, stream);
+}
+
+__attribute__((visibility("default"))) int nxt_paged_prefix_groups(
+    const int *block_tables, const int *seq_lens, int num_seqs, int max_num_blocks_per_seq,
+    int block_size, int *prefix_group, int *prefix_blocks, int *num_groups, nxt_stream_t stream) {
+    if (num_seqs < 0 || num_seqs > xhip::kCascadeMaxSeqs)
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "prefix detection handles 0..%d sequences",
+                          xhip::kCascadeMaxSeqs);
+    if (max_num_blocks_per_seq <= 0 || !is_pow2(block_size) || block_size > 1024 ||
+        (long long)max_num_blocks_per_seq * block_size > (1LL << 28))
+        return set_status(NXT_ATTN_E_INVALID, "bad table shape (%d blocks of %d)",
+                          max_num_blocks_per_seq, block_size);
+    if (!block_tables || !seq_lens || !prefix_group || !prefix_blocks || !num_groups)
+        return set_status(NXT_ATTN_E_INVALID, "NULL pointer");
+    const hipError_t e = xhip::launch_prefix_detect(block_tables, seq_lens, num_seqs,
+                                                    max_num_blocks_per_seq, block_size,
+                                                    prefix_group, prefix_blocks, num_groups,
+                                                    (hipStream_t)stream);
+    if (e != hipSuccess)
+        return set_status(NXT_ATTN_E_HIP, "prefix detection launch: %s", hipGetErrorString(e));
+    return ok();
 }
 
 __attribute__((visibility("default"))) int nxt_attn_last_status(void) { return t_status; }

@@ -1,0 +1,69 @@
+// Prefix-aware (cascade) decode: launch parameters and launchers of the plan,
+// detection and combine kernels (paged_decode_cascade.hip).  The attention
+// itself runs twice through the ordinary partition + merge kernels: once on
+// a prefix batch and once on a suffix batch that these kernels build.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+namespace xhip {
+
+// Query rows per kv head of a prefix-batch sequence are a multiple of the
+// MFMA head tile: one wavefront serves 16 (member, head) rows of a group per
+// page.
+constexpr int kCascadeRows = 16;
+// Sequences one detection workgroup handles (LDS hash table).
+constexpr int kCascadeMaxSeqs = 4096;
+
+struct CascadeParams {
+    // caller's batch
+    const int *block_tables;   // [num_seqs][max_blocks]
+    const int *seq_lens;       // [num_seqs]
+    const void *q;             // [num_seqs][num_heads][head_size]
+    void *out;                 // [num_seqs][num_heads][head_size], element type
+    const int *prefix_group;   // [num_seqs] group id < max_groups, or -1
+    const int *prefix_blocks;  // [max_groups] shared full pages of each group
+    int num_seqs, num_heads, num_kv_heads, group, head_size, elem_bytes, kv_dtype;
+    int max_blocks, block_size, max_ctx;
+    int max_groups;
+    int rows;                  // R: query rows per kv head of a prefix-batch sequence
+                               // (16 * ceil(G / 16))
+    int v_max;                 // prefix-batch sequences reserved (an upper bound)
+    // plan (workspace)
+    int *g_count;              // [max_groups] members
+    int *g_first;              // [max_groups] lowest member
+    int *g_vbase;              // [max_groups] first prefix-batch sequence
+    int *g_moff;               // [max_groups] offset of the group in member_seq
+    int *member_seq;           // [num_seqs] members of every group, by group
+    int *rank;                 // [num_seqs] member rank inside its group (-1: none)
+    int *v_group;              // [v_max] group of a prefix-batch sequence (-1: unused)
+    int *v_lens;               // [v_max]
+    int *v_bt;                 // [v_max][max_blocks]
+    void *v_q;                 // [v_max][num_kv_heads * rows][head_size]
+    int *s_lens;               // [num_seqs] suffix lengths
+    int *s_bt;                 // [num_seqs][max_blocks] suffix block tables
+    // pass outputs (fp32 + log-sum-exp in log2 units)
+    const float *p_out;        // [v_max][num_kv_heads * rows][head_size]
+    const float *p_lse;        // [v_max][num_kv_heads * rows]
+    const float *s_out;        // [num_seqs][num_heads][head_size]
+    const float *s_lse;        // [num_seqs][num_heads]
+};
+
+// Plan: group membership and the prefix / suffix batches.
+hipError_t launch_cascade_plan(const CascadeParams &c, hipStream_t stream);
+// out = log-sum-exp merge of the prefix-batch and suffix-batch rows.
+hipError_t launch_cascade_combine(const CascadeParams &c, hipStream_t stream);
+
+// Detection of shared prefixes from the block tables (one workgroup,
+// num_seqs <= kCascadeMaxSeqs): sequences whose first page is the same
+// physical page form a group (at least two members); the group's prefix is
+// the longest run of leading pages every member shares with the group's
+// lowest-numbered member, counting only pages full in both.  Writes
+// prefix_group[num_seqs] (-1: none), prefix_blocks[num_groups] and
+// *num_groups (all device memory).
+hipError_t launch_prefix_detect(const int *block_tables, const int *seq_lens, int num_seqs,
+                                int max_blocks, int block_size, int *prefix_group,
+                                int *prefix_blocks, int *num_groups, hipStream_t stream);
+
+}  // namespace xhip

@@ -1,0 +1,341 @@
+// Prefix-aware (cascade) decode on gfx950: plan, combine and detection
+// kernels.  No counterpart in the reference (its decode reads every
+// sequence's pages, shared or not); see paged_decode_cascade.h.
+//
+// A group is a set of sequences whose first P pages are the same physical
+// pages.  Attention over a group's shared prefix is computed once per page
+// for all of its members: the plan gathers the members' query rows, R per kv
+// head, into the sequences of a prefix batch whose block table is the shared
+// prefix, and shifts every member's own block table past the prefix into a
+// suffix batch.  The ordinary partition + merge kernels run on both batches
+// in partial-output mode (fp32 rows plus their log-sum-exp; prefix pages
+// loaded cacheable, since the rows of a group read them close in time), and
+// the combine kernel merges the two rows of every (sequence, head):
+//   M = max(lse_p, lse_s), O = (2^(lse_p-M) O_p + 2^(lse_s-M) O_s) /
+//                              (2^(lse_p-M) + 2^(lse_s-M)).
+// (One run over both batches together was measured slower: every wavefront
+// then streams prefix and suffix tiles back to back at the slower per-tile
+// rate of the two.)  A row of the prefix batch depends only on its own query
+// (the MFMA tile computes every (token, row) score and every (dim, row)
+// output from that row alone), so where a member lands among the rows does
+// not change its result, and rows no member uses are never read.
+#include <hip/hip_runtime.h>
+#include <limits.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "paged_decode_cascade.h"
+#include "paged_decode_kernels.h"
+
+namespace xhip {
+
+namespace {
+
+constexpr int kPlanThreads = 1024;
+
+__device__ __forceinline__ int clamp_len(int L, int max_ctx) {
+    return L < 0 ? 0 : (L > max_ctx ? max_ctx : L);
+}
+
+// Shared prefix pages of sequence s under the caller's grouping, or 0 when
+// the entry is out of range (then the sequence is decoded without cascade).
+__device__ __forceinline__ int member_prefix(const CascadeParams &c, int s, int *group) {
+    const int g = c.prefix_group[s];
+    *group = -1;
+    if (g < 0 || g >= c.max_groups) return 0;
+    const int P = c.prefix_blocks[g];
+    if (P < 1 || P > c.max_blocks) return 0;
+    if ((long long)P * c.block_size > clamp_len(c.seq_lens[s], c.max_ctx)) return 0;
+    *group = g;
+    return P;
+}
+
+// Exclusive scan, in place, of n ints of global memory by one workgroup of
+// kPlanThreads threads; returns the total to every thread.
+__device__ int block_exclusive_scan(int *a, int n, int *part) {
+    const int tid = threadIdx.x;
+    const int per = (n + kPlanThreads - 1) / kPlanThreads;
+    const int i0 = tid * per;
+    int local = 0;
+    for (int i = i0; i < i0 + per && i < n; i++) local += a[i];
+    part[tid] = local;
+    __syncthreads();
+    for (int off = 1; off < kPlanThreads; off <<= 1) {
+        const int v = tid >= off ? part[tid - off] : 0;
+        __syncthreads();
+        part[tid] += v;
+        __syncthreads();
+    }
+    int run = part[tid] - local;
+    for (int i = i0; i < i0 + per && i < n; i++) {
+        const int v = a[i];
+        a[i] = run;
+        run += v;
+    }
+    const int total = part[kPlanThreads - 1];
+    __syncthreads();
+    return total;
+}
+
+// Plan, part 1 (one workgroup): members, ranks, and where every group's rows
+// go in the prefix batch.
+__global__ __launch_bounds__(kPlanThreads) void cascade_plan_meta_kernel(const CascadeParams c) {
+    __shared__ int part[kPlanThreads];
+    const int tid = threadIdx.x;
+    const int B = c.num_seqs, NG = c.max_groups;
+    for (int g = tid; g < NG; g += kPlanThreads) {
+        c.g_count[g] = 0;
+        c.g_first[g] = INT_MAX;
+    }
+    __syncthreads();
+    for (int s = tid; s < B; s += kPlanThreads) {
+        int g;
+        member_prefix(c, s, &g);
+        int r = -1;
+        if (g >= 0) {
+            r = atomicAdd(&c.g_count[g], 1);
+            atomicMin(&c.g_first[g], s);
+        }
+        c.rank[s] = r;
+    }
+    __syncthreads();
+    // prefix sequences of every group: ceil(members * group / rows)
+    for (int g = tid; g < NG; g += kPlanThreads) {
+        c.g_vbase[g] = (c.g_count[g] * c.group + c.rows - 1) / c.rows;
+        c.g_moff[g] = c.g_count[g];
+    }
+    __syncthreads();
+    const int vt = block_exclusive_scan(c.g_vbase, NG, part);
+    block_exclusive_scan(c.g_moff, NG, part);
+    for (int s = tid; s < B; s += kPlanThreads) {
+        const int r = c.rank[s];
+        if (r >= 0) c.member_seq[c.g_moff[c.prefix_group[s]] + r] = s;
+    }
+    for (int g = tid; g < NG; g += kPlanThreads) {
+        const int n = (c.g_count[g] * c.group + c.rows - 1) / c.rows;
+        for (int k = 0; k < n; k++) c.v_group[c.g_vbase[g] + k] = g;
+    }
+    for (int v = vt + tid; v < c.v_max; v += kPlanThreads) c.v_group[v] = -1;
+}
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// Plan, part 2 (grid-stride): the prefix batch (gathered query rows, block
+// tables = the shared prefix, lengths) and the suffix batch (block tables
+// shifted past the prefix, lengths).
+__global__ __launch_bounds__(256) void cascade_plan_gather_kernel(const CascadeParams c) {
+    const int R = c.rows;
+    const int KR = c.num_kv_heads * R;
+    const int CH = c.head_size * c.elem_bytes / 16;
+    const size_t row_bytes = (size_t)c.head_size * c.elem_bytes;
+    const long long n1 = (long long)c.v_max * KR * CH;
+    const long long n2 = (long long)c.v_max * c.max_blocks;
+    const long long n3 = (long long)c.num_seqs * c.max_blocks;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n1 + n2 + n3;
+         i += stride) {
+        if (i < n1) {
+            const int ch = (int)(i % CH);
+            const long long row = i / CH;
+            const int v = (int)(row / KR);
+            const int hj = (int)(row - (long long)v * KR);
+            const int g = c.v_group[v];
+            if (g < 0) continue;  // unused: its length is 0, its rows are never read
+            const int h = hj / R, j = hj - h * R;
+            const int rig = (v - c.g_vbase[g]) * R + j;
+            const int r = rig / c.group, gq = rig - r * c.group;
+            if (r >= c.g_count[g]) continue;  // no member: never read
+            const int s = c.member_seq[c.g_moff[g] + r];
+            const size_t src = ((size_t)s * c.num_heads + (size_t)h * c.group + gq) * row_bytes +
+                               (size_t)ch * 16;
+            const size_t dst = ((size_t)v * KR + hj) * row_bytes + (size_t)ch * 16;
+            *(u32x4_t *)((char *)c.v_q + dst) = *(const u32x4_t *)((const char *)c.q + src);
+        } else if (i < n1 + n2) {
+            const long long k = i - n1;
+            const int v = (int)(k / c.max_blocks), b = (int)(k - (long long)v * c.max_blocks);
+            const int g = c.v_group[v];
+            const int P = g >= 0 ? c.prefix_blocks[g] : 0;
+            if (b == 0) c.v_lens[v] = P * c.block_size;
+            if (b < P)
+                c.v_bt[k] = c.block_tables[(size_t)c.g_first[g] * c.max_blocks + b];
+        } else {
+            const long long k = i - n1 - n2;
+            const int s = (int)(k / c.max_blocks), b = (int)(k - (long long)s * c.max_blocks);
+            int g;
+            const int P = c.rank[s] >= 0 ? member_prefix(c, s, &g) : 0;
+            if (b == 0)
+                c.s_lens[s] = P > 0 ? clamp_len(c.seq_lens[s], c.max_ctx) - P * c.block_size
+                                    : c.seq_lens[s];
+            c.s_bt[k] = b + P < c.max_blocks ? c.block_tables[(size_t)s * c.max_blocks + b + P]
+                                              : -1;
+        }
+    }
+}
+
+template <int KV>
+__global__ __launch_bounds__(256) void cascade_combine_kernel(const CascadeParams c) {
+    const int C4 = c.head_size / 4;
+    const long long n = (long long)c.num_seqs * c.num_heads * C4;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    const int R = c.rows;
+    const int KR = c.num_kv_heads * R;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const int c4 = (int)(i % C4);
+        const long long row = i / C4;  // s * num_heads + head
+        const int s = (int)(row / c.num_heads);
+        const int head = (int)(row - (long long)s * c.num_heads);
+        const float ls = c.s_lse[row];
+        const f32x4 os = *(const f32x4 *)(c.s_out + row * c.head_size + 4 * c4);
+        float lp = -INFINITY;
+        f32x4 op = {0.0f, 0.0f, 0.0f, 0.0f};
+        const int r = c.rank[s];
+        if (r >= 0) {
+            const int g = c.prefix_group[s];
+            const int kvh = head / c.group, gq = head - kvh * c.group;
+            const int rig = r * c.group + gq;
+            const int v = c.g_vbase[g] + rig / R, j = rig % R;
+            const long long prow = (long long)v * KR + kvh * R + j;
+            lp = c.p_lse[prow];
+            op = *(const f32x4 *)(c.p_out + prow * c.head_size + 4 * c4);
+        }
+        const float M = fmaxf(ls, lp);
+        f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (M != -INFINITY) {
+            const float ws = ls == -INFINITY ? 0.0f : exp2f(ls - M);
+            const float wp = lp == -INFINITY ? 0.0f : exp2f(lp - M);
+            o = (os * ws + op * wp) * (1.0f / (ws + wp));
+        }
+        const size_t base = (size_t)row * c.head_size + 4 * c4;
+#pragma unroll
+        for (int e = 0; e < 4; e++) store_elem<KV>(c.out, base + e, o[e]);
+    }
+}
+
+// Detection (one workgroup): open-addressing hash table in LDS from a first
+// page id to its group, then the shared run of every member against the
+// group's lowest member.
+constexpr int kDetectTable = 2 * kCascadeMaxSeqs;
+
+__global__ __launch_bounds__(kPlanThreads) void prefix_detect_kernel(
+    const int *block_tables, const int *seq_lens, int num_seqs, int max_blocks, int block_size,
+    int *prefix_group, int *prefix_blocks, int *num_groups) {
+    __shared__ int tkey[kDetectTable];   // first page id; later the group id of the slot
+    __shared__ int tmin[kDetectTable];   // lowest member
+    __shared__ int tcnt[kDetectTable];   // members
+    __shared__ int tpre[kDetectTable];   // shared leading pages
+    __shared__ int part[kPlanThreads];
+    const int tid = threadIdx.x;
+    const long long max_ctx = (long long)max_blocks * block_size;
+    for (int h = tid; h < kDetectTable; h += kPlanThreads) {
+        tkey[h] = -1;
+        tmin[h] = INT_MAX;
+        tcnt[h] = 0;
+        tpre[h] = INT_MAX;
+    }
+    __syncthreads();
+    auto len_of = [&](int s) {
+        const int L = seq_lens[s];
+        return L < 0 ? 0 : (L > max_ctx ? (int)max_ctx : L);
+    };
+    for (int s = tid; s < num_seqs; s += kPlanThreads) {
+        const int key = len_of(s) >= block_size ? block_tables[(size_t)s * max_blocks] : -1;
+        int slot = -1;
+        if (key >= 0) {
+            int h = (int)(((uint32_t)key * 2654435761u) >> 19) & (kDetectTable - 1);
+            for (;;) {  // the table holds at most num_seqs <= kDetectTable / 2 keys
+                const int old = atomicCAS(&tkey[h], -1, key);
+                if (old == -1 || old == key) break;
+                h = (h + 1) & (kDetectTable - 1);
+            }
+            atomicMin(&tmin[h], s);
+            atomicAdd(&tcnt[h], 1);
+            slot = h;
+        }
+        prefix_group[s] = slot;  // scratch until the last phase
+    }
+    __syncthreads();
+    for (int s = tid; s < num_seqs; s += kPlanThreads) {
+        const int slot = prefix_group[s];
+        if (slot < 0 || tcnt[slot] < 2) continue;
+        const int lead = tmin[slot];
+        const int n = min(len_of(s), len_of(lead)) / block_size;
+        const int *a = block_tables + (size_t)s * max_blocks;
+        const int *b = block_tables + (size_t)lead * max_blocks;
+        int P = 0;
+        while (P < n && a[P] == b[P]) P++;
+        atomicMin(&tpre[slot], P);
+    }
+    __syncthreads();
+    // group ids: leaders of groups with >= 2 members and >= 1 shared page,
+    // numbered in sequence order
+    const int per = (num_seqs + kPlanThreads - 1) / kPlanThreads;
+    const int s0 = tid * per;
+    int local = 0;
+    for (int s = s0; s < s0 + per && s < num_seqs; s++) {
+        const int slot = prefix_group[s];
+        local += slot >= 0 && tmin[slot] == s && tcnt[slot] >= 2 && tpre[slot] >= 1;
+    }
+    part[tid] = local;
+    __syncthreads();
+    for (int off = 1; off < kPlanThreads; off <<= 1) {
+        const int v = tid >= off ? part[tid - off] : 0;
+        __syncthreads();
+        part[tid] += v;
+        __syncthreads();
+    }
+    int id = part[tid] - local;
+    for (int s = s0; s < s0 + per && s < num_seqs; s++) {
+        const int slot = prefix_group[s];
+        if (slot >= 0 && tmin[slot] == s && tcnt[slot] >= 2 && tpre[slot] >= 1) {
+            tkey[slot] = id;
+            prefix_blocks[id] = tpre[slot];
+            id++;
+        }
+    }
+    if (tid == kPlanThreads - 1) *num_groups = part[kPlanThreads - 1];
+    __syncthreads();
+    for (int s = tid; s < num_seqs; s += kPlanThreads) {
+        const int slot = prefix_group[s];
+        prefix_group[s] = (slot >= 0 && tcnt[slot] >= 2 && tpre[slot] >= 1) ? tkey[slot] : -1;
+    }
+}
+
+unsigned grid_for(long long n) {
+    long long b = (n + 255) / 256;
+    if (b > 65536) b = 65536;
+    return (unsigned)(b > 0 ? b : 1);
+}
+
+}  // namespace
+
+hipError_t launch_cascade_plan(const CascadeParams &c, hipStream_t stream) {
+    cascade_plan_meta_kernel<<<1, kPlanThreads, 0, stream>>>(c);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const long long n = (long long)c.v_max * c.num_kv_heads * c.rows *
+                            (c.head_size * c.elem_bytes / 16) +
+                        (long long)(c.v_max + c.num_seqs) * c.max_blocks;
+    cascade_plan_gather_kernel<<<grid_for(n), 256, 0, stream>>>(c);
+    return hipGetLastError();
+}
+
+hipError_t launch_cascade_combine(const CascadeParams &c, hipStream_t stream) {
+    const unsigned grid = grid_for((long long)c.num_seqs * c.num_heads * (c.head_size / 4));
+    switch (c.kv_dtype) {
+    case KV_F16: cascade_combine_kernel<KV_F16><<<grid, 256, 0, stream>>>(c); break;
+    case KV_BF16: cascade_combine_kernel<KV_BF16><<<grid, 256, 0, stream>>>(c); break;
+    default: cascade_combine_kernel<KV_F32><<<grid, 256, 0, stream>>>(c); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_prefix_detect(const int *block_tables, const int *seq_lens, int num_seqs,
+                                int max_blocks, int block_size, int *prefix_group,
+                                int *prefix_blocks, int *num_groups, hipStream_t stream) {
+    prefix_detect_kernel<<<1, kPlanThreads, 0, stream>>>(block_tables, seq_lens, num_seqs,
+                                                          max_blocks, block_size, prefix_group,
+                                                          prefix_blocks, num_groups);
+    return hipGetLastError();
+}
+
+}  // namespace xhip

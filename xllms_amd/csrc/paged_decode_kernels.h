@@ -530,7 +530,21 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
         }
 
         if (row != 0 || !col_ok) return;
-        if (whole) {
+        if (whole && p.out_f32) {
+#pragma unroll
+            for (int h = 0; h < GT; h++) {
+                if (h >= nh) continue;
+                const float inv = st.l[h] > 0.0f ? 1.0f / st.l[h] : 0.0f;
+                float *dst = p.out_f32 + qrow0 + (size_t)h * D + col * VEC;
+#pragma unroll
+                for (int e = 0; e < VEC; e += 4)
+                    *(f32x4 *)(dst + e) = f32x4{st.o[h][e], st.o[h][e + 1], st.o[h][e + 2],
+                                                st.o[h][e + 3]} * inv;
+                if (col == 0)
+                    p.out_lse[qrow0 / D + h] =
+                        st.l[h] > 0.0f ? st.m[h] + log2f(st.l[h]) : -INFINITY;
+            }
+        } else if (whole) {
 #pragma unroll
             for (int h = 0; h < GT; h++) {
                 if (h >= nh) continue;
@@ -596,8 +610,13 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
     if (L == 0) {
         if (tid < kMergeCols && col0 + tid < ncols) {
             const size_t base = qrow0 + (size_t)(col0 + tid) * 4;  // head-major columns
+            if (p.out_f32) {
+                *(f32x4 *)(p.out_f32 + base) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                if ((col0 + tid) % C4 == 0) p.out_lse[qrow0 / D + (col0 + tid) / C4] = -INFINITY;
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, 0.0f);
+                for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, 0.0f);
+            }
         }
         return;
     }
@@ -653,6 +672,11 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
     }
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     const size_t base = qrow0 + (size_t)h * D + c * 4;
+    if (p.out_f32) {
+        *(f32x4 *)(p.out_f32 + base) = acc * inv;
+        if (c == 0) p.out_lse[qrow0 / D + h] = l > 0.0f ? m + log2f(l) : -INFINITY;
+        return;
+    }
 #pragma unroll
     for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, acc[e] * inv);
 }
@@ -689,8 +713,14 @@ __global__ __launch_bounds__(kMergeSegThreads) void paged_decode_merge_segment_k
 
     if (L == 0) {
         for (int col = tid; col < ncols; col += kMergeSegThreads) {
+            if (p.out_f32) {
+                *(f32x4 *)(p.out_f32 + qrow0 + (size_t)col * 4) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                if (col % C4 == 0) p.out_lse[qrow0 / D + col / C4] = -INFINITY;
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; e++) store_elem<KV>(p.out, qrow0 + (size_t)col * 4 + e, 0.0f);
+                for (int e = 0; e < 4; e++)
+                    store_elem<KV>(p.out, qrow0 + (size_t)col * 4 + e, 0.0f);
+            }
         }
         return;
     }
@@ -760,6 +790,12 @@ __global__ __launch_bounds__(kMergeSegThreads) void paged_decode_merge_segment_k
         if (col >= ncols) continue;
         const float inv = l[k] > 0.0f ? 1.0f / l[k] : 0.0f;
         const size_t base = qrow0 + (size_t)col * 4;  // head-major columns
+        if (p.out_f32) {
+            *(f32x4 *)(p.out_f32 + base) = acc[k] * inv;
+            if (col % C4 == 0)
+                p.out_lse[qrow0 / D + col / C4] = l[k] > 0.0f ? m[k] + log2f(l[k]) : -INFINITY;
+            continue;
+        }
 #pragma unroll
         for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, acc[k][e] * inv);
     }

@@ -91,6 +91,10 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
     return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kStreamPolicy);
 }
 
+__device__ __forceinline__ u32x4 buf_load16_cached(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+}
+
 template <int D> struct MfmaTileRegs {
     u32x4 k[MfmaGeometry<D>::kQkSteps];
     u32x4 v[MfmaGeometry<D>::kVLoads];
@@ -101,7 +105,7 @@ template <int D> struct MfmaTileRegs {
 template <int D>
 __device__ __forceinline__ void mfma_load_tile(const DecodeParams &p, const char *kb,
                                                const char *vb, int t0, int t_end, int blk,
-                                               int lane, MfmaTileRegs<D> &r) {
+                                               int lane, bool cached, MfmaTileRegs<D> &r) {
     using G = MfmaGeometry<D>;
     const int bmask = p.block_size - 1;
     const bool page_ok = blk >= 0;
@@ -110,16 +114,28 @@ __device__ __forceinline__ void mfma_load_tile(const DecodeParams &p, const char
     const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vb + page * 2);
     const int j = lane & 15, g = lane >> 4;
     const bool krow_ok = page_ok && (t0 + j < t_end);
+    uint32_t koff[G::kQkSteps], voff[G::kVLoads];
 #pragma unroll
     for (int c = 0; c < G::kQkSteps; c++)
-        r.k[c] = buf_load16(rk, krow_ok ? (uint32_t)(j * 2 * D + 64 * c + 16 * g) : kOobOffset);
+        koff[c] = krow_ok ? (uint32_t)(j * 2 * D + 64 * c + 16 * g) : kOobOffset;
 #pragma unroll
     for (int c = 0; c < G::kVLoads; c++) {
         const int q = 64 * c + lane;
         const int row = q / G::kChunks;
         const int chunk = q - row * G::kChunks;
         const bool ok = page_ok && (t0 + row < t_end);
-        r.v[c] = buf_load16(rv, ok ? (uint32_t)(row * 2 * D + 16 * chunk) : kOobOffset);
+        voff[c] = ok ? (uint32_t)(row * 2 * D + 16 * chunk) : kOobOffset;
+    }
+    if (cached) {
+#pragma unroll
+        for (int c = 0; c < G::kQkSteps; c++) r.k[c] = buf_load16_cached(rk, koff[c]);
+#pragma unroll
+        for (int c = 0; c < G::kVLoads; c++) r.v[c] = buf_load16_cached(rv, voff[c]);
+    } else {
+#pragma unroll
+        for (int c = 0; c < G::kQkSteps; c++) r.k[c] = buf_load16(rk, koff[c]);
+#pragma unroll
+        for (int c = 0; c < G::kVLoads; c++) r.v[c] = buf_load16(rv, voff[c]);
     }
 }
 
@@ -209,7 +225,8 @@ __device__ __forceinline__ void mfma_tile(const DecodeParams &p, const u32x4 *q,
 template <int KV, int D>
 __device__ __forceinline__ void mfma_segment(const DecodeParams &p, const int *bt, const char *kb,
                                              const char *vb, int t_begin, int t_end, int lane,
-                                             char *lds, const u32x4 *q, MfmaState<D> &st) {
+                                             bool cached, char *lds, const u32x4 *q,
+                                             MfmaState<D> &st) {
     const int ntiles = (t_end - t_begin + 15) >> 4;
     // Block ids of up to 64 tiles at a time, one per lane (vector loads, so
     // the tile loop issues no scalar memory traffic).
@@ -222,7 +239,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeParams &p, const int *b
             ids = bt[(ti < t_end ? ti : t_end - 1) >> p.bs_shift];
             if (i == 0) {
                 blk_a = __builtin_amdgcn_readlane(ids, 0);
-                mfma_load_tile<D>(p, kb, vb, t_begin, t_end, blk_a, lane, ra);
+                mfma_load_tile<D>(p, kb, vb, t_begin, t_end, blk_a, lane, cached, ra);
             }
         }
         const int t0 = t_begin + 16 * i;
@@ -233,7 +250,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeParams &p, const int *b
             const int ti = t0 + 16;
             blk_b = bt[ti >> p.bs_shift];
         }
-        mfma_load_tile<D>(p, kb, vb, t0 + 16, t_end, blk_b, lane, rb);
+        mfma_load_tile<D>(p, kb, vb, t0 + 16, t_end, blk_b, lane, cached, rb);
         mfma_tile<KV, D>(p, q, t0, t_end, blk_a >= 0, lane, lds, ra, st);
         ra = rb;
         blk_a = blk_b;
@@ -277,13 +294,19 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_mf
         const int *bt = p.block_tables + (size_t)s * p.max_blocks;
         const char *kb = (const char *)p.k + (size_t)kvh * (size_t)p.kv_head_stride * 2;
         const char *vb = (const char *)p.v + (size_t)kvh * (size_t)p.kv_head_stride * 2;
-        mfma_segment<KV, D>(p, bt, kb, vb, t_begin, t_end, lane, lds, q, st);
+        mfma_segment<KV, D>(p, bt, kb, vb, t_begin, t_end, lane, s < p.cached_seqs, lds, q, st);
 
         float l = st.l;
         l += __shfl_xor(l, 16);
         l += __shfl_xor(l, 32);
         if (j >= nh) return;
-        if (whole) {
+        if (whole && p.out_f32) {
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            float *dst = p.out_f32 + qrow0 + (size_t)j * D + 4 * gq;
+#pragma unroll
+            for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st.o[n] * inv;
+            if (gq == 0) p.out_lse[qrow0 / D + j] = l > 0.0f ? st.m + log2f(l) : -INFINITY;
+        } else if (whole) {
             const float inv = l > 0.0f ? 1.0f / l : 0.0f;
             char *dst = (char *)p.out + (qrow0 + (size_t)j * D + 4 * gq) * 2;
 #pragma unroll

@@ -53,6 +53,14 @@ struct DecodeParams {
     int min_tiles_per_wave;    // lower bound of tpw (>= 1)
     float scale_log2;          // scale * log2(e)
     int merge_per_segment;     // 1: merge with one workgroup per segment
+    // Partial-output mode (cascade passes): when out_f32 is set, every
+    // (sequence, head) row is written in fp32 to out_f32 (indexed like out)
+    // together with its log-sum-exp in log2 units, m + log2(l), to
+    // out_lse[seq * num_heads + head] (-inf for an empty row); out is unused.
+    float *out_f32;
+    float *out_lse;
+    int cached_seqs;           // sequences [0, cached_seqs) load K/V cacheable (pages read
+                               // by several wavefronts close in time); the rest nontemporal
 };
 
 }  // namespace xhip

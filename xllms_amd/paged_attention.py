@@ -157,3 +157,53 @@ def paged_kv_append(key_cache, value_cache, key, value, *, block_tables=None, po
     if check and status != NXT_ATTN_OK:
         raise PagedAttentionError(status, lib.nxt_attn_last_error().decode())
     return status
+
+
+def paged_attention_cascade(out, query, key_cache, value_cache, block_tables, seq_lens,
+                            prefix_group, prefix_blocks, *, num_kv_heads: int, scale: float,
+                            max_groups: int | None = None, block_size: int | None = None,
+                            kv_block_stride: int | None = None, kv_head_stride: int | None = None,
+                            kv_dtype: int | None = None, stream=None, check: bool = True) -> int:
+    """Prefix-aware decode (nxt_paged_attention_cascade): same result as
+    paged_attention, reading each shared prefix page once per 16 rows of the
+    sequences that share it.  prefix_group: int32 [num_seqs] (-1 = none),
+    prefix_blocks: int32 [max_groups] shared leading pages per group."""
+    lib = _lib.backend()
+    num_seqs, num_heads, head_size = query.shape
+    if max_groups is None:
+        max_groups = prefix_blocks.shape[0]
+    if block_size is None:
+        block_size = key_cache.shape[2]
+    if kv_head_stride is None:
+        kv_head_stride = key_cache.stride(1)
+    if kv_block_stride is None:
+        kv_block_stride = key_cache.stride(0)
+    if kv_dtype is None:
+        kv_dtype = kv_dtype_of(key_cache)
+    status = lib.nxt_paged_attention_cascade(
+        _ptr(out), _ptr(query), _ptr(key_cache), _ptr(value_cache), _ptr(block_tables),
+        _ptr(seq_lens), _ptr(prefix_group), _ptr(prefix_blocks), max_groups, num_seqs, num_heads,
+        head_size, num_kv_heads, ctypes.c_float(scale), block_tables.shape[1], block_size,
+        kv_block_stride, kv_head_stride, kv_dtype, _stream_handle(stream))
+    if check and status != NXT_ATTN_OK:
+        raise PagedAttentionError(status, lib.nxt_attn_last_error().decode())
+    return status
+
+
+def prefix_groups(block_tables, seq_lens, *, block_size: int, stream=None):
+    """Shared-prefix groups of a batch found from its block tables
+    (nxt_paged_prefix_groups).  Returns device tensors (prefix_group [B],
+    prefix_blocks [B // 2 + 1]) and the device int32 count [1]."""
+    import torch
+    lib = _lib.backend()
+    B = seq_lens.shape[0]
+    dev = seq_lens.device
+    group = torch.empty(B, dtype=torch.int32, device=dev)
+    blocks = torch.zeros(B // 2 + 1, dtype=torch.int32, device=dev)
+    count = torch.zeros(1, dtype=torch.int32, device=dev)
+    status = lib.nxt_paged_prefix_groups(_ptr(block_tables), _ptr(seq_lens), B,
+                                         block_tables.shape[1], block_size, _ptr(group),
+                                         _ptr(blocks), _ptr(count), _stream_handle(stream))
+    if status != NXT_ATTN_OK:
+        raise PagedAttentionError(status, lib.nxt_attn_last_error().decode())
+    return group, blocks, count
