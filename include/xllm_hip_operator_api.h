@@ -208,6 +208,17 @@ int nxt_paged_kv_write_slots(void *key_cache, void *value_cache, const void *key
                              int kv_block_stride, int kv_head_stride, int kv_dtype,
                              nxt_stream_t stream);
 
+/* Copy-on-write of a partly shared page: the K and V rows (every kv head) of
+ * slot src_slots[i] are copied to slot dst_slots[i] of the same caches; a
+ * negative source or destination skips the pair.  No destination may be the
+ * source of another pair in the same call.  The reference has no counterpart
+ * (its radix tree hands out shared pages only, prefix_sharing.c:211-265);
+ * nxt_kv_seq_admit (xllm_hip_kv_index.h) produces the lists. */
+int nxt_paged_kv_copy_slots(void *key_cache, void *value_cache, const int *src_slots,
+                            const int *dst_slots, int num_tokens, int num_kv_heads, int head_size,
+                            int block_size, int kv_block_stride, int kv_head_stride, int kv_dtype,
+                            nxt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -187,3 +187,25 @@ def paged_kv_append(key_cache: np.ndarray, value_cache: np.ndarray, key: np.ndar
     if rc != 0:
         raise ValueError("oracle_paged_kv_append rejected its arguments")
     return kc, vc
+
+
+def paged_kv_copy_slots(key_cache: np.ndarray, value_cache: np.ndarray, src, dst, *,
+                        num_kv_heads: int, head_size: int, block_size: int,
+                        kv_block_stride: int, kv_head_stride: int):
+    """Copy-on-write of page slots (nxt_paged_kv_copy_slots): the rows of
+    slot src[i] (every kv head) are gathered from the caches and stored at
+    slot dst[i] through oracle_paged_kv_append; a negative source or
+    destination skips the pair.  Returns updated copies of the two caches."""
+    src = np.asarray(src, dtype=np.int64)
+    dst = np.asarray(dst, dtype=np.int32).copy()
+    keep = src >= 0
+    dst[~keep] = -1
+    s = np.where(keep, src, 0)
+    base = ((s // block_size) * kv_block_stride + (s % block_size) * head_size)[:, None, None]
+    idx = base + (np.arange(num_kv_heads) * kv_head_stride)[None, :, None] + \
+        np.arange(head_size)[None, None, :]
+    k = key_cache.reshape(-1)[idx]
+    v = value_cache.reshape(-1)[idx]
+    return paged_kv_append(key_cache, value_cache, k, v, block_size=block_size,
+                           kv_block_stride=kv_block_stride, kv_head_stride=kv_head_stride,
+                           slots=dst)

@@ -55,7 +55,8 @@ def test_library_exports_exactly_the_declared_symbols():
     exported = exported_functions(_lib.BACKEND_SO)
     declared = declared_functions()
     assert exported == declared, (sorted(exported - declared), sorted(declared - exported))
-    assert set(_lib.OPERATOR_SYMBOLS) | set(_lib.PLUGIN_SYMBOLS) == declared
+    assert (set(_lib.OPERATOR_SYMBOLS) | set(_lib.PLUGIN_SYMBOLS) |
+            set(_lib.KV_INDEX_SYMBOLS)) == declared
 
 
 def test_library_loads_and_resolves_every_symbol():

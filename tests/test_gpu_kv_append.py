@@ -99,6 +99,33 @@ def test_slot_mapping_bit_exact(cuda, dtype):
     assert np.array_equal(host_bits(dw.value_cache, kv_dtype), bits(want_v))
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("head_size", [64, 128])
+def test_copy_slots_bit_exact(cuda, dtype, head_size):
+    """nxt_paged_kv_copy_slots: rows move slot to slot inside the caches,
+    skipped pairs and every other byte unchanged."""
+    kv_dtype = DT[dtype]
+    wl = W.small_case(num_seqs=4, H=8, KVH=4, D=head_size, bs=16, kv_dtype=kv_dtype,
+                      seed=41 + head_size, lens=[300, 40, 1, 77])
+    rng = np.random.default_rng(42)
+    slots = rng.permutation(wl.num_blocks * 16).astype(np.int32)
+    n = 90
+    src, dst = slots[:n].copy(), slots[n:2 * n].copy()
+    src[::11] = -1
+    dst[5::13] = -1
+    want_k, want_v = O.paged_kv_copy_slots(wl.key_cache, wl.value_cache, src, dst,
+                                           num_kv_heads=4, head_size=head_size, block_size=16,
+                                           kv_block_stride=wl.kv_block_stride,
+                                           kv_head_stride=wl.kv_head_stride)
+    dw = W.upload(wl)
+    print(f"case {dtype} d={head_size}", flush=True)
+    PA.paged_kv_copy_slots(dw.key_cache, dw.value_cache, device_int(src), device_int(dst))
+    import torch
+    torch.cuda.synchronize()
+    assert np.array_equal(host_bits(dw.key_cache, kv_dtype), bits(want_k))
+    assert np.array_equal(host_bits(dw.value_cache, kv_dtype), bits(want_v))
+
+
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 def test_decode_step_append_then_attend(cuda, dtype):
     """One decode step as text_gen.c:1274-1281 does it: store the new token at

@@ -85,6 +85,28 @@ def test_slot_mapping_matches_numpy_scatter():
     assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
 
 
+@pytest.mark.parametrize("d", [64, 128])
+def test_copy_slots_matches_numpy_page_copy(d):
+    """The copy-on-write helper: an independent numpy copy through the 4-D
+    page view, skip rules included."""
+    rng = np.random.default_rng(6 + d)
+    nb, kvh, bs, n = 10, 3, 16, 40
+    kc = rng.standard_normal((nb, kvh, bs, d)).astype(np.float32)
+    vc = rng.standard_normal((nb, kvh, bs, d)).astype(np.float32)
+    slots = rng.permutation(nb * bs).astype(np.int32)
+    src, dst = slots[:n].copy(), slots[n:2 * n].copy()
+    src[::9] = -1
+    dst[4::7] = -1
+    got = O.paged_kv_copy_slots(kc, vc, src, dst, num_kv_heads=kvh, head_size=d, block_size=bs,
+                                kv_block_stride=kvh * bs * d, kv_head_stride=bs * d)
+    wk, wv = kc.copy(), vc.copy()
+    for s, t in zip(src, dst):
+        if s >= 0 and t >= 0:
+            wk[t // bs, :, t % bs] = kc[s // bs, :, s % bs]
+            wv[t // bs, :, t % bs] = vc[s // bs, :, s % bs]
+    assert np.array_equal(got[0], wk) and np.array_equal(got[1], wv)
+
+
 def test_decode_loop_reproduces_contiguous_attention():
     """text_gen.c's loop: append at cur_len, attend over cur_len + 1 tokens."""
     rng = np.random.default_rng(11)

@@ -58,6 +58,17 @@ OPERATOR_SYMBOLS = (
     "nxt_paged_kv_write_slots",
     "nxt_paged_attention_cascade",
     "nxt_paged_prefix_groups",
+    "nxt_paged_kv_copy_slots",
+)
+# include/xllm_hip_kv_index.h (host code in the same library)
+KV_INDEX_SYMBOLS = (
+    "nxt_kv_index_create", "nxt_kv_index_destroy",
+    "nxt_kv_block_alloc", "nxt_kv_block_ref_inc", "nxt_kv_block_ref_dec", "nxt_kv_block_refs",
+    "nxt_kv_blocks_free",
+    "nxt_kv_prefix_match", "nxt_kv_prefix_insert", "nxt_kv_prefix_evict", "nxt_kv_prefix_lock",
+    "nxt_kv_prefix_unlock", "nxt_kv_prefix_stats",
+    "nxt_kv_seq_admit", "nxt_kv_seq_append", "nxt_kv_batch_append", "nxt_kv_seq_cache",
+    "nxt_kv_seq_release", "nxt_kv_seq_len", "nxt_kv_batch_tables", "nxt_kv_batch_prefix_groups",
 )
 PLUGIN_SYMBOLS = ("nxt_backend_init", "nxt_backend_run", "nxt_backend_fini", "nxt_backend_run_ex")
 
@@ -96,8 +107,42 @@ def backend() -> ctypes.CDLL:
         lib.nxt_paged_prefix_groups.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p,
                                                 c_void_p, c_void_p, c_void_p]
         lib.nxt_paged_prefix_groups.restype = c_int
+        lib.nxt_paged_kv_copy_slots.argtypes = [c_void_p] * 4 + [c_int] * 7 + [c_void_p]
+        lib.nxt_paged_kv_copy_slots.restype = c_int
+        _type_kv_index(lib)
         lib._xllm_typed = True
     return lib
+
+
+def _type_kv_index(lib: ctypes.CDLL) -> None:
+    vp, i32, u64 = c_void_p, ctypes.c_int32, ctypes.c_uint64
+    sig = {
+        "nxt_kv_index_create": ([c_int, c_int, c_int], vp),
+        "nxt_kv_index_destroy": ([vp], None),
+        "nxt_kv_block_alloc": ([vp], c_int),
+        "nxt_kv_block_ref_inc": ([vp, c_int], c_int),
+        "nxt_kv_block_ref_dec": ([vp, c_int], c_int),
+        "nxt_kv_block_refs": ([vp, c_int], c_int),
+        "nxt_kv_blocks_free": ([vp], c_int),
+        "nxt_kv_prefix_match": ([vp, vp, i32, vp, vp], c_int),
+        "nxt_kv_prefix_insert": ([vp, vp, i32, vp, i32], i32),
+        "nxt_kv_prefix_evict": ([vp, i32], i32),
+        "nxt_kv_prefix_lock": ([vp, u64], c_int),
+        "nxt_kv_prefix_unlock": ([vp, u64], c_int),
+        "nxt_kv_prefix_stats": ([vp, vp], c_int),
+        "nxt_kv_seq_admit": ([vp, vp, i32, vp, vp, vp, vp], c_int),
+        "nxt_kv_seq_append": ([vp, i32, vp, i32, vp], c_int),
+        "nxt_kv_batch_append": ([vp, vp, i32, vp, vp], c_int),
+        "nxt_kv_seq_cache": ([vp, i32], i32),
+        "nxt_kv_seq_release": ([vp, i32, c_int], c_int),
+        "nxt_kv_seq_len": ([vp, i32], i32),
+        "nxt_kv_batch_tables": ([vp, vp, i32, i32, vp, vp], c_int),
+        "nxt_kv_batch_prefix_groups": ([vp, vp, i32, vp, vp, vp], c_int),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
 
 
 def workload() -> ctypes.CDLL:

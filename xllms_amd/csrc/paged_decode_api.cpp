@@ -523,7 +523,8 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
 int kv_append_run(void *key_cache, void *value_cache, const void *key, const void *value,
                   const int *slots, const int *block_tables, const int *positions, int num_tokens,
                   int num_kv_heads, int head_size, int max_num_blocks_per_seq, int block_size,
-                  int kv_block_stride, int kv_head_stride, int kv_dtype, nxt_stream_t stream_handle) {
+                  int kv_block_stride, int kv_head_stride, int kv_dtype, nxt_stream_t stream_handle,
+                  const int *src_slots = nullptr) {
     if (kv_dtype != NXT_KV_FP16 && kv_dtype != NXT_KV_BF16 && kv_dtype != NXT_KV_FP32)
         return set_status(NXT_ATTN_E_INVALID, "kv_dtype %d is not FP16/BF16/FP32", kv_dtype);
     if (num_tokens < 0 || num_kv_heads <= 0 || block_size <= 0 || kv_block_stride < 0 ||
@@ -553,6 +554,7 @@ int kv_append_run(void *key_cache, void *value_cache, const void *key, const voi
     p.key = key;
     p.value = value;
     p.slots = slots;
+    p.src_slots = src_slots;
     p.block_tables = block_tables;
     p.positions = positions;
     p.kv_block_stride_bytes = bstride;
@@ -677,6 +679,17 @@ __attribute__((visibility("default"))) int nxt_paged_kv_write_slots(
     return kv_append_run(key_cache, value_cache, key, value, slot_mapping, nullptr, nullptr,
                          num_tokens, num_kv_heads, head_size, 0, block_size, kv_block_stride,
                          kv_head_stride, kv_dtype, stream);
+}
+
+__attribute__((visibility("default"))) int nxt_paged_kv_copy_slots(
+    void *key_cache, void *value_cache, const int *src_slots, const int *dst_slots, int num_tokens,
+    int num_kv_heads, int head_size, int block_size, int kv_block_stride, int kv_head_stride,
+    int kv_dtype, nxt_stream_t stream) {
+    if ((!src_slots || !dst_slots) && num_tokens > 0)
+        return set_status(NXT_ATTN_E_INVALID, "NULL slot list");
+    return kv_append_run(key_cache, value_cache, key_cache, value_cache, dst_slots, nullptr,
+                         nullptr, num_tokens, num_kv_heads, head_size, 0, block_size,
+                         kv_block_stride, kv_head_stride, kv_dtype, stream, src_slots);
 }
 
 __attribute__((visibility("default"))) int nxt_paged_attention_cascade(

@@ -9,8 +9,10 @@ namespace xhip {
 struct KvAppendParams {
     void *key_cache;
     void *value_cache;
-    const void *key;           // [num_tokens][num_kv_heads][row_bytes]
-    const void *value;
+    const void *key;           // [num_tokens][num_kv_heads][row_bytes], or the caches
+    const void *value;         // themselves when src_slots is set
+    const int *src_slots;      // [num_tokens] copy mode: token i's rows are read from
+                               // this cache slot (null: from key / value)
     const int *slots;          // [num_tokens] flat slots, or null: use block_tables + positions
     const int *block_tables;   // [num_tokens][max_blocks] (decode: token s = sequence s)
     const int *positions;      // [num_tokens]

@@ -11,7 +11,8 @@
 // block_size, where slot_of comes either from `slots` (prefill: one flat
 // slot per token) or from `block_tables` + `positions` (decode: token s of
 // sequence s at position positions[s]).  A negative slot, position or page
-// id skips the token.  HBM-bound byte copy: each lane moves 16 bytes of K
+// id skips the token.  In copy mode (`src_slots`) the rows come from another
+// slot of the same caches: the copy-on-write of a partly shared page.  HBM-bound byte copy: each lane moves 16 bytes of K
 // and 16 of V with one load and one store each; a wavefront covers four
 // 256-byte rows.
 #include <hip/hip_runtime.h>
@@ -45,7 +46,16 @@ __global__ __launch_bounds__(256) void paged_kv_append_kernel(const KvAppendPara
         const long long off = slot & (p.block_size - 1);
         const size_t dst = (size_t)(blk * p.kv_block_stride_bytes + h * p.kv_head_stride_bytes +
                                     off * p.row_bytes) + (size_t)c * 16;
-        const size_t src = (size_t)row * p.row_bytes + (size_t)c * 16;
+        size_t src;
+        if (p.src_slots) {  // copy inside the cache, page slot to page slot
+            const long long from = p.src_slots[tok];
+            if (from < 0) continue;
+            src = (size_t)((from >> p.bs_shift) * p.kv_block_stride_bytes +
+                           h * p.kv_head_stride_bytes +
+                           (from & (p.block_size - 1)) * p.row_bytes) + (size_t)c * 16;
+        } else {
+            src = (size_t)row * p.row_bytes + (size_t)c * 16;
+        }
         const u32x4 k = *(const u32x4 *)((const char *)p.key + src);
         const u32x4 v = *(const u32x4 *)((const char *)p.value + src);
         *(u32x4 *)((char *)p.key_cache + dst) = k;

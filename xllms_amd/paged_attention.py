@@ -159,6 +159,29 @@ def paged_kv_append(key_cache, value_cache, key, value, *, block_tables=None, po
     return status
 
 
+def paged_kv_copy_slots(key_cache, value_cache, src_slots, dst_slots, *,
+                        num_kv_heads: int | None = None, block_size: int | None = None,
+                        kv_block_stride: int | None = None, kv_head_stride: int | None = None,
+                        kv_dtype: int | None = None, stream=None, check: bool = True) -> int:
+    """Copy the K/V rows of page slots src_slots[i] to dst_slots[i] (int32
+    device tensors) inside the caches (nxt_paged_kv_copy_slots): the
+    copy-on-write of a partly shared page at admission."""
+    lib = _lib.backend()
+    _, kvh, bs, head_size = key_cache.shape
+    num_kv_heads = kvh if num_kv_heads is None else num_kv_heads
+    block_size = bs if block_size is None else block_size
+    kv_block_stride = key_cache.stride(0) if kv_block_stride is None else kv_block_stride
+    kv_head_stride = key_cache.stride(1) if kv_head_stride is None else kv_head_stride
+    kv_dtype = kv_dtype_of(key_cache) if kv_dtype is None else kv_dtype
+    status = lib.nxt_paged_kv_copy_slots(
+        _ptr(key_cache), _ptr(value_cache), _ptr(src_slots), _ptr(dst_slots),
+        src_slots.shape[0], num_kv_heads, head_size, block_size, kv_block_stride,
+        kv_head_stride, kv_dtype, _stream_handle(stream))
+    if check and status != NXT_ATTN_OK:
+        raise PagedAttentionError(status, lib.nxt_attn_last_error().decode())
+    return status
+
+
 def paged_attention_cascade(out, query, key_cache, value_cache, block_tables, seq_lens,
                             prefix_group, prefix_blocks, *, num_kv_heads: int, scale: float,
                             max_groups: int | None = None, block_size: int | None = None,
