@@ -29,6 +29,7 @@
 #ifndef XLLM_HIP_BACKEND_H_
 #define XLLM_HIP_BACKEND_H_
 
+#include <stdbool.h>
 #include <stdint.h>
 
 #include "xllm_hip_operator_api.h"
@@ -48,6 +49,86 @@ typedef enum {
 } NxtBackendState;
 
 typedef struct NxtBackend NxtBackend;
+typedef struct NxtModel NxtModel;
+typedef struct NxtModelInstance NxtModelInstance;
+typedef struct NxtInferRequest NxtInferRequest;
+
+/* Mirrors of include/backend.h:13-33, 54-62, 66-113 and 155-189 (layouts as
+ * the reference compiler lays them out on LP64: NxtTensor 48 bytes,
+ * NxtModelConfig 120, NxtModel 168, NxtModelInstance 48, NxtInferRequest 56;
+ * asserted in tests/c/layout_check.c). */
+typedef enum {
+    NXT_TYPE_BOOL = 1,
+    NXT_TYPE_UINT8 = 2,
+    NXT_TYPE_UINT16 = 3,
+    NXT_TYPE_UINT32 = 4,
+    NXT_TYPE_UINT64 = 5,
+    NXT_TYPE_INT8 = 6,
+    NXT_TYPE_INT16 = 7,
+    NXT_TYPE_INT32 = 8,
+    NXT_TYPE_INT64 = 9,
+    NXT_TYPE_FP16 = 10,
+    NXT_TYPE_FP32 = 11,
+    NXT_TYPE_FP64 = 12,
+    NXT_TYPE_BYTES = 13,
+} NxtDataType;
+
+typedef enum {
+    NXT_MEM_CPU = 0,
+    NXT_MEM_GPU = 1,
+    NXT_MEM_CPU_PINNED = 2,
+} NxtMemoryType;
+
+typedef struct {
+    const char *name;
+    NxtDataType dtype;
+    int64_t *shape;
+    uint32_t dims_count;
+    uint64_t byte_size;
+    NxtMemoryType memory_type;
+    int32_t memory_type_id;
+} NxtTensor;
+
+typedef enum {
+    NXT_INSTANCE_KIND_GPU = 0,
+    NXT_INSTANCE_KIND_CPU = 1,
+} NxtInstanceKind;
+
+typedef struct {
+    uint32_t count;
+    NxtInstanceKind kind;
+    int32_t *gpus;
+    uint32_t gpus_count;
+} NxtInstanceGroup;
+
+typedef struct {
+    int policy; /* NxtVersionPolicy */
+    uint32_t num_versions;
+    int32_t *versions;
+    uint32_t versions_count;
+} NxtModelVersionConfig;
+
+typedef struct {
+    float preferred_batch_size_ratio;
+    double max_queue_delay_ms;
+    bool preserve_ordering;
+    int32_t priority_levels;
+} NxtDynamicBatchingConfig;
+
+typedef struct {
+    char *name;
+    char *backend_name;
+    char *model_path;
+    int32_t max_batch_size;
+    uint32_t input_count;
+    NxtTensor **inputs;
+    uint32_t output_count;
+    NxtTensor **outputs;
+    uint32_t instance_group_count;
+    NxtInstanceGroup *instance_groups;
+    NxtModelVersionConfig version_config;
+    NxtDynamicBatchingConfig dynamic_batching;
+} NxtModelConfig;
 
 /* Mirror of include/backend.h:128-137: eight function pointers (64 bytes on
  * LP64).  Only the first three are resolved from this plugin. */
@@ -74,8 +155,40 @@ struct NxtBackend {
     NxtBackendState state;
     int32_t priority;
     uint32_t model_count;
-    void *models;
+    NxtModel *models;
     void *backend_state;
+};
+
+struct NxtModel {
+    char *name;
+    int32_t version;
+    NxtModelConfig config;
+    NxtBackend *backend;
+    NxtModelInstance *instances;
+    uint32_t instance_count;
+    NxtBackendState state;
+    void *backend_state;
+};
+
+struct NxtModelInstance {
+    NxtModel *model;
+    char *name;
+    NxtInstanceKind kind;
+    int32_t device_id;
+    void *instance_state;
+    uint64_t exec_count;
+    double total_exec_ms;
+};
+
+struct NxtInferRequest {
+    const char *request_id;
+    uint32_t batch_size;
+    uint32_t input_count;
+    NxtTensor *inputs;
+    uint32_t requested_output_count;
+    char **requested_output_names;
+    uint64_t enqueue_time_ns;
+    int32_t priority;
 };
 #endif /* XLLM_BACKEND_H */
 
@@ -123,6 +236,66 @@ int nxt_backend_fini(NxtBackend *backend);
 /* Additive: run with an explicit dtype (bf16) and partition length. */
 int nxt_backend_run_ex(NxtBackend *backend, const NxtPagedAttentionInputEx *input,
                        void *output);
+
+/* ------------------------------------------------ models and instances
+ * The optional plugin symbols the reference manager resolves
+ * (src/core/backend_manager.c:202-206), so that its scheduler's poll
+ * (src/core/scheduler.c:477-488: instance_exec(model->instances, &request, 1)
+ * for each scheduled request) reaches the decode path.
+ *
+ * nxt_model_init(model) is called by nxt_model_create
+ * (backend_manager.c:389-398).  It reads the decode geometry from
+ * model->config.inputs by name:
+ *   "key_cache"     4 dims [num_blocks, num_kv_heads, block_size, head_size];
+ *                   dtype NXT_TYPE_FP16, NXT_TYPE_FP32 or NXT_TYPE_BF16_HIP;
+ *   "query"         2 dims [num_heads, head_size];
+ *   "block_tables"  optional, 2 dims [*, max_blocks_per_seq] (default: every
+ *                   page of the cache);
+ * and model->config.max_batch_size (requests per exec, default 256).  It
+ * creates one instance on the current HIP device (the reference creates
+ * none, so model->instances would stay NULL), which holds the paged K/V
+ * caches in HBM and the KV-cache index (xllm_hip_kv_index.h) of its
+ * sequences.  Scale: 1/sqrt(head_size), as text_gen.c:732.
+ *
+ * A request carries no data pointers (NxtTensor has none), so its buffers
+ * are bound by request_id before the exec that consumes them
+ * (nxt_model_instance_bind).  exec then, for the batch of requests:
+ *   1. admits a request seen for the first time with its tokens (prompt
+ *      prefix matched against the cached sequences: shared pages reused,
+ *      a partly matched page copied) or appends the tokens of a known one;
+ *   2. writes the K/V rows of every new token that is not cached (one
+ *      launch for the batch);
+ *   3. runs the decode attention for the requests with a query (the
+ *      prefix-aware form when the batch has shared prefixes) and writes each
+ *      output;
+ *   4. ends the requests marked release (their tokens stay in the tree for
+ *      later prompts until evicted).
+ * It returns when the device work is done (0), or -1 on an unbound request,
+ * a bad binding or an exhausted cache; requests before the failing one stay
+ * applied.  Bindings are consumed by the exec.  Not thread-safe. */
+#define NXT_TYPE_BF16_HIP 256 /* bfloat16: no code in the reference's NxtDataType */
+
+typedef struct {
+    uint32_t struct_size;     /* sizeof(NxtDecodeIo) */
+    int32_t num_tokens;       /* new tokens of the request (its prompt the first time) */
+    const int32_t *token_ids; /* host [num_tokens] */
+    const void *key;          /* device [num_tokens][num_kv_heads][head_size], cache dtype */
+    const void *value;
+    const void *query;        /* device [num_heads][head_size] of the last token, or NULL */
+    void *output;             /* device [num_heads][head_size] (with query) */
+    int32_t release;          /* end the request after this exec */
+    int32_t reserved;
+} NxtDecodeIo;
+
+int nxt_model_init(NxtModel *model);
+int nxt_model_fini(NxtModel *model);
+int nxt_model_instance_init(NxtModelInstance *instance);
+int nxt_model_instance_fini(NxtModelInstance *instance);
+int nxt_model_instance_exec(NxtModelInstance *instance, NxtInferRequest **requests,
+                            uint32_t request_count);
+/* Additive: bind the buffers of the next exec of request_id (copied). */
+int nxt_model_instance_bind(NxtModelInstance *instance, const char *request_id,
+                            const NxtDecodeIo *io);
 
 #ifdef __cplusplus
 }

@@ -159,6 +159,14 @@ int main(int argc, char **argv) {
     FiniFn fini = (FiniFn)dlsym(h, "nxt_backend_fini");
     CHECK(init && run && fini, "dlsym nxt_backend_init/run/fini");
     if (!init || !run || !fini) return 1;
+    /* the optional model symbols the manager resolves when it registers a
+     * plugin (backend_manager.c:202-206), so the scheduler's poll can reach
+     * instance_exec (scheduler.c:482-486) */
+    static const char *const model_syms[] = {"nxt_model_init", "nxt_model_fini",
+                                             "nxt_model_instance_init", "nxt_model_instance_fini",
+                                             "nxt_model_instance_exec"};
+    for (size_t i = 0; i < sizeof(model_syms) / sizeof(model_syms[0]); i++)
+        CHECK(dlsym(h, model_syms[i]) != NULL, model_syms[i]);
 
     CHECK(init(NULL) == -1, "init(NULL) == -1");
     CHECK(fini(NULL) == -1, "fini(NULL) == -1");

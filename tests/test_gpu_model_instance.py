@@ -1,0 +1,118 @@
+"""The decode path behind the reference scheduler's call, on the GPU: a model
+created like nxt_model_create does (the plugin's nxt_model_init builds the
+instance: K/V caches in HBM and the KV-cache index), requests bound by id
+and executed like nxt_scheduler_poll executes them
+(src/core/scheduler.c:482-486: instance_exec(model->instances, &request, 1)),
+and also as whole batches.  Each output is checked against the oracle's
+attention (examples/text_gen.c:1284-1310 restated) over the request's
+logical K/V history, at the task's tolerance."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests.helpers import assert_close
+from tests.test_gpu_kv_index_decode import Driver
+from xllms_amd import backend as B
+from xllms_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+class Client:
+    """Holds each request's token history; K/V and queries come from the
+    same prefix-keyed rows as tests/test_gpu_kv_index_decode.py."""
+
+    def __init__(self, model: B.DecodeModel, ref: Driver, dtype):
+        self.m, self.ref, self.dtype = model, ref, dtype
+        self.hist: dict[str, list] = {}
+
+    def bind(self, rid, new_tokens, rng, release=False, attend=True):
+        import torch
+        toks = self.hist.setdefault(rid, [])
+        start = len(toks)
+        toks += [int(t) for t in new_tokens]
+        kv = np.stack([self.ref.rows(toks, t) for t in range(start, len(toks))]) \
+            if len(new_tokens) else None
+        keep = {}
+        if kv is not None:
+            keep["k"] = W.to_torch(np.ascontiguousarray(kv[:, 0]), self.dtype)
+            keep["v"] = W.to_torch(np.ascontiguousarray(kv[:, 1]), self.dtype)
+        if attend:
+            keep["q_bits"] = rng.standard_normal((self.ref.H, self.ref.D)).astype(np.float16) \
+                .view(np.uint16)
+            keep["q"] = W.to_torch(keep["q_bits"], self.dtype)
+            keep["o"] = torch.empty((self.ref.H, self.ref.D), dtype=torch.float16,
+                                    device="cuda")
+        rc = self.m.bind(rid, tokens=new_tokens if len(new_tokens) else None,
+                         key=keep.get("k"), value=keep.get("v"), query=keep.get("q"),
+                         output=keep.get("o"), release=release)
+        assert rc == 0
+        return keep
+
+    def check(self, rids, binds, what):
+        import torch
+        torch.cuda.synchronize()
+        for rid in rids:
+            self.ref.live[rid] = self.hist[rid]
+        q = np.stack([binds[r]["q_bits"] for r in rids])
+        want = self.ref.logical_oracle(rids, q)
+        got = np.stack([binds[r]["o"].float().cpu().numpy() for r in rids])
+        assert_close(got, want, W.FP16, what)
+        self.ref.live.clear()
+
+
+def test_scheduler_style_and_batched_exec(cuda):
+    import torch
+    rng = np.random.default_rng(99)
+    H, KVH, D, bs = 32, 8, 128, 16
+    ref = Driver.__new__(Driver)
+    ref.KVH, ref.H, ref.D, ref.bs = KVH, H, D, bs
+    ref.scale = 1.0 / np.sqrt(D)
+    ref.live, ref._rows = {}, {}
+    m = B.DecodeModel(num_blocks=512, num_kv_heads=KVH, block_size=bs, head_size=D,
+                      num_heads=H, max_batch_size=16, max_blocks_per_seq=64)
+    assert m.status == 0 and m.model.instance_count == 1 and m.model.instances
+    c = Client(m, ref, W.FP16)
+    system = list(rng.integers(0, 60, 45))
+    rids = [f"req{i}" for i in range(6)]
+    # prompts one request per exec, as the scheduler's poll issues them
+    for i, rid in enumerate(rids):
+        prompt = system + list(rng.integers(0, 60, 20 + 7 * i)) if i < 4 else \
+            list(rng.integers(60, 99, 30 + i))
+        b = c.bind(rid, prompt, rng)
+        assert m.exec([rid]) == 0
+        c.check([rid], {rid: b}, f"prefill {rid}")
+        if i == 0:
+            # make req0's prompt shareable: end it and start it again under a new id
+            b = c.bind(rid, [], rng, release=True, attend=False)
+            assert m.exec([rid]) == 0
+            del c.hist[rid]
+            b = c.bind(rid, prompt, rng)
+            assert m.exec([rid]) == 0
+            c.check([rid], {rid: b}, "re-admitted req0")
+    # decode steps: whole batches, then one request per exec
+    for step in range(8):
+        binds = {rid: c.bind(rid, [int(rng.integers(0, 60))], rng) for rid in rids}
+        if step % 2 == 0:
+            assert m.exec(rids) == 0
+        else:
+            for rid in rids:
+                assert m.exec([rid]) == 0
+        c.check(rids, binds, f"decode step {step}")
+    # release half, admit a request that extends a released one's history
+    for rid in rids[:3]:
+        c.bind(rid, [], rng, release=True, attend=False)
+    assert m.exec(rids[:3]) == 0
+    ext = c.hist["req1"][:70] + list(rng.integers(0, 60, 9))
+    b = c.bind("late", ext, rng)
+    assert m.exec(["late"]) == 0
+    c.check(["late"], {"late": b}, "late admission")
+    inst = m.model.instances[0]
+    assert inst.exec_count > 0 and inst.total_exec_ms > 0
+    # errors: unbound request, duplicate id in one batch
+    assert m.exec(["nobody"]) == -1
+    c.bind("late", [3], rng)
+    assert m.exec(["late", "late"]) == -1
+    assert m.close() == 0
+    torch.cuda.synchronize()

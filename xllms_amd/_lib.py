@@ -70,7 +70,9 @@ KV_INDEX_SYMBOLS = (
     "nxt_kv_seq_admit", "nxt_kv_seq_append", "nxt_kv_batch_append", "nxt_kv_seq_cache",
     "nxt_kv_seq_release", "nxt_kv_seq_len", "nxt_kv_batch_tables", "nxt_kv_batch_prefix_groups",
 )
-PLUGIN_SYMBOLS = ("nxt_backend_init", "nxt_backend_run", "nxt_backend_fini", "nxt_backend_run_ex")
+PLUGIN_SYMBOLS = ("nxt_backend_init", "nxt_backend_run", "nxt_backend_fini", "nxt_backend_run_ex",
+                  "nxt_model_init", "nxt_model_fini", "nxt_model_instance_init",
+                  "nxt_model_instance_fini", "nxt_model_instance_exec", "nxt_model_instance_bind")
 
 _LEGACY_ARGS = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                 c_int, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_int, c_void_p]

@@ -156,3 +156,150 @@ def make_input(query, key_cache, value_cache, block_tables, seq_lens, *, num_kv_
     d.kv_head_stride = key_cache.stride(1)
     d.stream = stream or None
     return d
+
+
+# ---------------------------------------------------------------- models
+# Layout mirrors of include/backend.h:54-189 (sizes 48 / 120 / 168 / 48 / 56
+# bytes, as the reference header compiles on LP64) and of NxtDecodeIo.
+NXT_TYPE_INT32, NXT_TYPE_FP16, NXT_TYPE_FP32, NXT_TYPE_BF16_HIP = 8, 10, 11, 256
+
+
+class NxtTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_int),
+                ("shape", ctypes.POINTER(ctypes.c_int64)), ("dims_count", ctypes.c_uint32),
+                ("byte_size", ctypes.c_uint64), ("memory_type", ctypes.c_int),
+                ("memory_type_id", ctypes.c_int32)]
+
+
+class _VersionConfig(ctypes.Structure):
+    _fields_ = [("policy", ctypes.c_int), ("num_versions", ctypes.c_uint32),
+                ("versions", ctypes.c_void_p), ("versions_count", ctypes.c_uint32)]
+
+
+class _BatchingConfig(ctypes.Structure):
+    _fields_ = [("preferred_batch_size_ratio", ctypes.c_float),
+                ("max_queue_delay_ms", ctypes.c_double), ("preserve_ordering", ctypes.c_bool),
+                ("priority_levels", ctypes.c_int32)]
+
+
+class NxtModelConfig(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("backend_name", ctypes.c_char_p),
+                ("model_path", ctypes.c_char_p), ("max_batch_size", ctypes.c_int32),
+                ("input_count", ctypes.c_uint32), ("inputs", ctypes.POINTER(ctypes.POINTER(NxtTensor))),
+                ("output_count", ctypes.c_uint32), ("outputs", ctypes.c_void_p),
+                ("instance_group_count", ctypes.c_uint32), ("instance_groups", ctypes.c_void_p),
+                ("version_config", _VersionConfig), ("dynamic_batching", _BatchingConfig)]
+
+
+class NxtModelInstance(ctypes.Structure):
+    _fields_ = [("model", ctypes.c_void_p), ("name", ctypes.c_char_p), ("kind", ctypes.c_int),
+                ("device_id", ctypes.c_int32), ("instance_state", ctypes.c_void_p),
+                ("exec_count", ctypes.c_uint64), ("total_exec_ms", ctypes.c_double)]
+
+
+class NxtModel(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("version", ctypes.c_int32),
+                ("config", NxtModelConfig), ("backend", ctypes.c_void_p),
+                ("instances", ctypes.POINTER(NxtModelInstance)), ("instance_count", ctypes.c_uint32),
+                ("state", ctypes.c_int), ("backend_state", ctypes.c_void_p)]
+
+
+class NxtInferRequest(ctypes.Structure):
+    _fields_ = [("request_id", ctypes.c_char_p), ("batch_size", ctypes.c_uint32),
+                ("input_count", ctypes.c_uint32), ("inputs", ctypes.c_void_p),
+                ("requested_output_count", ctypes.c_uint32),
+                ("requested_output_names", ctypes.c_void_p),
+                ("enqueue_time_ns", ctypes.c_uint64), ("priority", ctypes.c_int32)]
+
+
+class NxtDecodeIo(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("num_tokens", ctypes.c_int32),
+                ("token_ids", ctypes.c_void_p), ("key", ctypes.c_void_p),
+                ("value", ctypes.c_void_p), ("query", ctypes.c_void_p),
+                ("output", ctypes.c_void_p), ("release", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
+
+
+class DecodeModel:
+    """A decode model on the plugin, created the way nxt_model_create does
+    (src/core/backend_manager.c:373-402: the config copied into an NxtModel,
+    then the plugin's nxt_model_init), and executed the way the scheduler's
+    poll does (src/core/scheduler.c:482-486:
+    instance_exec(model->instances, requests, count))."""
+
+    def __init__(self, *, num_blocks: int, num_kv_heads: int, block_size: int, head_size: int,
+                 num_heads: int, dtype: int = NXT_TYPE_FP16, max_batch_size: int = 256,
+                 max_blocks_per_seq: int | None = None, name: str = "default"):
+        self.dl = ctypes.CDLL(_lib.BACKEND_SO, mode=os.RTLD_NOW | os.RTLD_LOCAL)
+        vp = ctypes.c_void_p
+        for fn in ("nxt_model_init", "nxt_model_fini"):
+            getattr(self.dl, fn).argtypes = [ctypes.POINTER(NxtModel)]
+            getattr(self.dl, fn).restype = ctypes.c_int
+        self.dl.nxt_model_instance_exec.argtypes = [ctypes.POINTER(NxtModelInstance), vp,
+                                                    ctypes.c_uint32]
+        self.dl.nxt_model_instance_exec.restype = ctypes.c_int
+        self.dl.nxt_model_instance_bind.argtypes = [ctypes.POINTER(NxtModelInstance),
+                                                    ctypes.c_char_p, ctypes.POINTER(NxtDecodeIo)]
+        self.dl.nxt_model_instance_bind.restype = ctypes.c_int
+        self._keep = []      # config structures, alive as long as the model
+        self._io_keep = []   # token arrays of bound requests, until their exec
+
+        def tensor(tname, dtype_code, shape):
+            sh = (ctypes.c_int64 * len(shape))(*shape)
+            t = NxtTensor(name=tname.encode(), dtype=dtype_code, shape=sh, dims_count=len(shape))
+            self._keep += [sh, t]
+            return ctypes.pointer(t)
+
+        ins = [tensor("key_cache", dtype, [num_blocks, num_kv_heads, block_size, head_size]),
+               tensor("query", dtype, [num_heads, head_size])]
+        if max_blocks_per_seq:
+            ins.append(tensor("block_tables", NXT_TYPE_INT32, [max_batch_size, max_blocks_per_seq]))
+        arr = (ctypes.POINTER(NxtTensor) * len(ins))(*ins)
+        self._keep.append(arr)
+        self._name = name.encode()
+        self.model = NxtModel()
+        self.model.name = self._name
+        self.model.version = 1
+        self.model.config.name = self._name
+        self.model.config.backend_name = b"hip"
+        self.model.config.max_batch_size = max_batch_size
+        self.model.config.input_count = len(ins)
+        self.model.config.inputs = arr
+        self.status = self.dl.nxt_model_init(ctypes.byref(self.model))
+        self.model.state = STATE_READY if self.status == 0 else STATE_ERROR
+
+    @property
+    def instance(self):
+        return self.model.instances
+
+    def bind(self, request_id: str, *, tokens=None, key=None, value=None, query=None,
+             output=None, release: bool = False) -> int:
+        import numpy as np
+        io = NxtDecodeIo(struct_size=ctypes.sizeof(NxtDecodeIo))
+        if tokens is not None and len(tokens):
+            t = np.ascontiguousarray(tokens, dtype=np.int32)
+            self._io_keep.append(t)
+            io.num_tokens = len(t)
+            io.token_ids = t.ctypes.data
+        ptr = lambda x: None if x is None else x.data_ptr()
+        io.key, io.value, io.query, io.output = ptr(key), ptr(value), ptr(query), ptr(output)
+        io.release = int(release)
+        return self.dl.nxt_model_instance_bind(self.instance, request_id.encode(),
+                                               ctypes.byref(io))
+
+    def exec(self, request_ids) -> int:
+        ids = [r.encode() for r in request_ids]
+        reqs = (NxtInferRequest * max(1, len(ids)))()
+        ptrs = (ctypes.POINTER(NxtInferRequest) * max(1, len(ids)))()
+        for i, rid in enumerate(ids):
+            reqs[i].request_id = rid
+            reqs[i].batch_size = 1
+            ptrs[i] = ctypes.pointer(reqs[i])
+        rc = self.dl.nxt_model_instance_exec(self.instance, ctypes.cast(ptrs, ctypes.c_void_p),
+                                             len(ids))
+        self._io_keep = []
+        return rc
+
+    def close(self) -> int:
+        rc = self.dl.nxt_model_fini(ctypes.byref(self.model))
+        return rc

@@ -1,0 +1,510 @@
+// Model and model-instance entry points of the plugin: the decode path
+// behind the reference scheduler's instance_exec call
+// (src/core/scheduler.c:477-488), with the sequences' pages managed by the
+// KV-cache index (kv_index.cpp) and the K/V caches resident in HBM.
+// Declared, with the conventions, in include/xllm_hip_backend.h.
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "paged_kv_append.h"
+#include "xllm_hip_backend.h"
+#include "xllm_hip_kv_index.h"
+
+#define XMI_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+constexpr uint32_t kModelMagic = 0x584d444cu;  // "XMDL"
+constexpr uint32_t kInstMagic = 0x58494e53u;   // "XINS"
+constexpr int kDefaultMaxBatch = 256;
+
+struct ModelSpec {
+    uint32_t magic = kModelMagic;
+    int num_blocks = 0, num_kv_heads = 0, block_size = 0, head_size = 0, num_heads = 0;
+    int kv_dtype = 0, elem_bytes = 0, max_batch = 0, max_blocks = 0;
+    float scale = 0.f;
+};
+
+int fail(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+int fail(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    std::fprintf(stderr, "[hip_backend] ");
+    std::vfprintf(stderr, fmt, ap);
+    std::fprintf(stderr, "\n");
+    va_end(ap);
+    return -1;
+}
+
+// Grow-only device / pinned host buffers, reused across execs (an exec
+// waits for its device work before returning, so reuse is safe).
+template <class T>
+struct DevBuf {
+    T *p = nullptr;
+    size_t cap = 0;
+    bool reserve(size_t n) {
+        if (n <= cap) return true;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+        if (hipMalloc((void **)&p, n * sizeof(T)) != hipSuccess) return false;
+        cap = n;
+        return true;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+};
+
+template <class T>
+struct HostBuf {
+    T *p = nullptr;
+    size_t cap = 0, n = 0;
+    bool reserve(size_t want) {
+        if (want <= cap) return true;
+        size_t c = cap ? cap : 256;
+        while (c < want) c *= 2;
+        T *q = nullptr;
+        if (hipHostMalloc((void **)&q, c * sizeof(T), hipHostMallocDefault) != hipSuccess)
+            return false;
+        if (p) {
+            std::memcpy(q, p, n * sizeof(T));
+            (void)hipHostFree(p);
+        }
+        p = q;
+        cap = c;
+        return true;
+    }
+    bool push(const T &v) {
+        if (!reserve(n + 1)) return false;
+        p[n++] = v;
+        return true;
+    }
+    void release() {
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        cap = n = 0;
+    }
+};
+
+struct InstanceState {
+    uint32_t magic = kInstMagic;
+    ModelSpec spec;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    void *key_cache = nullptr;
+    void *value_cache = nullptr;
+    NxtKvIndex *index = nullptr;
+    std::unordered_map<std::string, int32_t> seqs;       // request id -> sequence
+    std::unordered_map<std::string, NxtDecodeIo> bound;  // request id -> next exec's buffers
+    // staging of one exec
+    HostBuf<int32_t> h_slots, h_src, h_dst, h_bt, h_lens, h_group, h_pblocks, h_seqs;
+    HostBuf<const char *> h_kptr, h_vptr, h_qptr;
+    HostBuf<char *> h_optr;
+    DevBuf<int32_t> d_slots, d_src, d_dst, d_bt, d_lens, d_group, d_pblocks;
+    DevBuf<const char *> d_kptr, d_vptr, d_qptr;
+    DevBuf<char *> d_optr;
+    DevBuf<char> d_q, d_out;
+};
+
+const NxtTensor *find_input(const NxtModelConfig &c, const char *name) {
+    for (uint32_t i = 0; i < c.input_count; ++i)
+        if (c.inputs && c.inputs[i] && c.inputs[i]->name && !std::strcmp(c.inputs[i]->name, name))
+            return c.inputs[i];
+    return nullptr;
+}
+
+bool is_device(const void *ptr) {
+    hipPointerAttribute_t a;
+    std::memset(&a, 0, sizeof(a));
+    if (hipPointerGetAttributes(&a, ptr) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return a.type == hipMemoryTypeDevice || a.type == hipMemoryTypeManaged;
+}
+
+InstanceState *state_of(NxtModelInstance *inst) {
+    if (!inst || !inst->instance_state) return nullptr;
+    auto *st = (InstanceState *)inst->instance_state;
+    return st->magic == kInstMagic ? st : nullptr;
+}
+
+int parse_spec(const NxtModel *m, ModelSpec &s) {
+    const NxtTensor *kc = find_input(m->config, "key_cache");
+    const NxtTensor *q = find_input(m->config, "query");
+    if (!kc || !q || kc->dims_count != 4 || q->dims_count != 2 || !kc->shape || !q->shape)
+        return fail("model %s: needs inputs \"key_cache\" [blocks, kv_heads, block_size, "
+                    "head_size] and \"query\" [heads, head_size]",
+                    m->name ? m->name : "?");
+    s.num_blocks = (int)kc->shape[0];
+    s.num_kv_heads = (int)kc->shape[1];
+    s.block_size = (int)kc->shape[2];
+    s.head_size = (int)kc->shape[3];
+    s.num_heads = (int)q->shape[0];
+    if (q->shape[1] != kc->shape[3])
+        return fail("model: query head_size %lld != key_cache head_size %lld",
+                    (long long)q->shape[1], (long long)kc->shape[3]);
+    switch ((int)kc->dtype) {
+        case NXT_TYPE_FP16: s.kv_dtype = NXT_KV_FP16; s.elem_bytes = 2; break;
+        case NXT_TYPE_FP32: s.kv_dtype = NXT_KV_FP32; s.elem_bytes = 4; break;
+        case NXT_TYPE_BF16_HIP: s.kv_dtype = NXT_KV_BF16; s.elem_bytes = 2; break;
+        default: return fail("model: key_cache dtype %d is not FP16, FP32 or BF16", kc->dtype);
+    }
+    s.max_batch = m->config.max_batch_size > 0 ? m->config.max_batch_size : kDefaultMaxBatch;
+    const NxtTensor *bt = find_input(m->config, "block_tables");
+    s.max_blocks = (bt && bt->dims_count == 2 && bt->shape && bt->shape[1] > 0)
+                       ? (int)bt->shape[1]
+                       : s.num_blocks;
+    const long long bound = (1LL << 28) / std::max(1, s.block_size);
+    if (s.max_blocks > bound) s.max_blocks = (int)bound;
+    if (s.num_blocks <= 0 || s.num_kv_heads <= 0 || s.num_heads <= 0 ||
+        s.num_heads % s.num_kv_heads || s.head_size <= 0 || (s.head_size * s.elem_bytes) % 16 ||
+        s.block_size <= 0 || (s.block_size & (s.block_size - 1)))
+        return fail("model: unsupported geometry (blocks %d, kv heads %d, heads %d, head_size "
+                    "%d, block_size %d)",
+                    s.num_blocks, s.num_kv_heads, s.num_heads, s.head_size, s.block_size);
+    s.scale = 1.0f / std::sqrt((float)s.head_size);
+    return 0;
+}
+
+void destroy_state(InstanceState *st) {
+    if (!st) return;
+    if (st->stream) (void)hipStreamSynchronize(st->stream);
+    if (st->index) nxt_kv_index_destroy(st->index);
+    if (st->key_cache) (void)hipFree(st->key_cache);
+    if (st->value_cache) (void)hipFree(st->value_cache);
+    for (auto *b : {&st->h_slots, &st->h_src, &st->h_dst, &st->h_bt, &st->h_lens, &st->h_group,
+                    &st->h_pblocks, &st->h_seqs})
+        b->release();
+    st->h_kptr.release();
+    st->h_vptr.release();
+    st->h_qptr.release();
+    st->h_optr.release();
+    for (auto *b : {&st->d_slots, &st->d_src, &st->d_dst, &st->d_bt, &st->d_lens, &st->d_group,
+                    &st->d_pblocks})
+        b->release();
+    st->d_kptr.release();
+    st->d_vptr.release();
+    st->d_qptr.release();
+    st->d_optr.release();
+    st->d_q.release();
+    st->d_out.release();
+    if (st->stream) (void)hipStreamDestroy(st->stream);
+    st->magic = 0;
+    delete st;
+}
+
+template <class T>
+hipError_t upload(DevBuf<T> &d, const HostBuf<T> &h, hipStream_t s) {
+    if (h.n == 0) return hipSuccess;
+    if (!d.reserve(h.n)) return hipErrorOutOfMemory;
+    return hipMemcpyAsync(d.p, h.p, h.n * sizeof(T), hipMemcpyHostToDevice, s);
+}
+
+struct Item {
+    std::string id;
+    NxtDecodeIo io;
+    int32_t seq;  // -1: admitted by this exec
+};
+
+}  // namespace
+
+XMI_EXPORT int nxt_model_init(NxtModel *model) {
+    if (!model) return -1;
+    ModelSpec spec;
+    if (parse_spec(model, spec) != 0) return -1;
+    auto *ms = new (std::nothrow) ModelSpec(spec);
+    auto *inst = (NxtModelInstance *)std::calloc(1, sizeof(NxtModelInstance));
+    if (!ms || !inst) {
+        delete ms;
+        std::free(inst);
+        return -1;
+    }
+    model->backend_state = ms;
+    inst->model = model;
+    const std::string name = std::string(model->name ? model->name : "model") + "_0";
+    inst->name = strdup(name.c_str());
+    inst->kind = NXT_INSTANCE_KIND_GPU;
+    if (hipGetDevice(&inst->device_id) != hipSuccess || nxt_model_instance_init(inst) != 0) {
+        std::free(inst->name);
+        std::free(inst);
+        delete ms;
+        model->backend_state = nullptr;
+        return -1;
+    }
+    model->instances = inst;
+    model->instance_count = 1;
+    return 0;
+}
+
+XMI_EXPORT int nxt_model_fini(NxtModel *model) {
+    if (!model) return -1;
+    for (uint32_t i = 0; model->instances && i < model->instance_count; ++i) {
+        nxt_model_instance_fini(&model->instances[i]);
+        std::free(model->instances[i].name);
+    }
+    std::free(model->instances);
+    model->instances = nullptr;
+    model->instance_count = 0;
+    auto *ms = (ModelSpec *)model->backend_state;
+    if (ms && ms->magic == kModelMagic) delete ms;
+    model->backend_state = nullptr;
+    return 0;
+}
+
+XMI_EXPORT int nxt_model_instance_init(NxtModelInstance *instance) {
+    if (!instance || !instance->model || !instance->model->backend_state) return -1;
+    const auto *ms = (const ModelSpec *)instance->model->backend_state;
+    if (ms->magic != kModelMagic) return -1;
+    auto *st = new (std::nothrow) InstanceState;
+    if (!st) return -1;
+    st->spec = *ms;
+    st->device = instance->device_id;
+    const ModelSpec &s = st->spec;
+    const size_t cache_bytes = (size_t)s.num_blocks * s.num_kv_heads * s.block_size *
+                               s.head_size * s.elem_bytes;
+    hipError_t e = hipSetDevice(st->device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&st->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipMalloc(&st->key_cache, cache_bytes);
+    if (e == hipSuccess) e = hipMalloc(&st->value_cache, cache_bytes);
+    if (e != hipSuccess) {
+        destroy_state(st);
+        return fail("instance init: %s (K/V caches of %zu bytes each)", hipGetErrorString(e),
+                    cache_bytes);
+    }
+    st->index = nxt_kv_index_create(s.num_blocks, s.block_size, s.max_blocks);
+    const size_t row = (size_t)s.num_heads * s.head_size * s.elem_bytes;
+    if (!st->index || !st->d_q.reserve((size_t)s.max_batch * row) ||
+        !st->d_out.reserve((size_t)s.max_batch * row)) {
+        destroy_state(st);
+        return fail("instance init: out of memory");
+    }
+    instance->instance_state = st;
+    instance->exec_count = 0;
+    instance->total_exec_ms = 0.0;
+    return 0;
+}
+
+XMI_EXPORT int nxt_model_instance_fini(NxtModelInstance *instance) {
+    if (!instance) return -1;
+    InstanceState *st = state_of(instance);
+    destroy_state(st);
+    instance->instance_state = nullptr;
+    return 0;
+}
+
+XMI_EXPORT int nxt_model_instance_bind(NxtModelInstance *instance, const char *request_id,
+                                       const NxtDecodeIo *io) {
+    InstanceState *st = state_of(instance);
+    if (!st || !request_id || !io) return -1;
+    if (io->struct_size < sizeof(NxtDecodeIo)) return fail("bind: struct_size %u", io->struct_size);
+    if (io->num_tokens < 0) return fail("bind: num_tokens %d", io->num_tokens);
+    if (io->num_tokens > 0 && (!io->token_ids || !io->key || !io->value))
+        return fail("bind %s: tokens without token_ids / key / value", request_id);
+    if (!io->query != !io->output) return fail("bind %s: query and output go together", request_id);
+    for (const void *p : {io->key, io->value, io->query, (const void *)io->output}) {
+        if (!p) continue;
+        if (((uintptr_t)p & 15) || !is_device(p))
+            return fail("bind %s: buffers must be 16-byte aligned device memory", request_id);
+    }
+    NxtDecodeIo c = *io;
+    c.struct_size = sizeof(NxtDecodeIo);
+    st->bound[request_id] = c;
+    return 0;
+}
+
+XMI_EXPORT int nxt_model_instance_exec(NxtModelInstance *instance, NxtInferRequest **requests,
+                                       uint32_t request_count) {
+    InstanceState *st = state_of(instance);
+    if (!st || (request_count && !requests)) return -1;
+    const ModelSpec &s = st->spec;
+    const auto t0 = std::chrono::steady_clock::now();
+    if ((int)request_count > s.max_batch)
+        return fail("exec: %u requests > max_batch_size %d", request_count, s.max_batch);
+
+    // every request bound, each once
+    std::vector<Item> items;
+    items.reserve(request_count);
+    for (uint32_t i = 0; i < request_count; ++i) {
+        if (!requests[i] || !requests[i]->request_id) return fail("exec: request %u has no id", i);
+        const std::string id = requests[i]->request_id;
+        auto b = st->bound.find(id);
+        if (b == st->bound.end()) return fail("exec: request %s has no bound buffers", id.c_str());
+        for (const Item &it : items)
+            if (it.id == id) return fail("exec: request %s twice in one batch", id.c_str());
+        auto q = st->seqs.find(id);
+        items.push_back({id, b->second, q == st->seqs.end() ? -1 : q->second});
+        if (items.back().seq < 0 && b->second.num_tokens == 0)
+            return fail("exec: new request %s without tokens", id.c_str());
+    }
+    if (hipSetDevice(st->device) != hipSuccess) return fail("exec: hipSetDevice failed");
+
+    // 1. sequences: admissions and appends; the K/V rows to write and copy
+    const size_t kv_row = (size_t)s.num_kv_heads * s.head_size * s.elem_bytes;
+    st->h_slots.n = st->h_src.n = st->h_dst.n = st->h_kptr.n = st->h_vptr.n = 0;
+    std::vector<int32_t> mapping, src, dst, slots;
+    int rc = 0;
+    for (Item &it : items) {
+        const int n = it.io.num_tokens;
+        if (n == 0) continue;
+        slots.assign((size_t)n, -1);
+        if (it.seq < 0) {
+            mapping.resize((size_t)n);
+            src.resize((size_t)n);
+            dst.resize((size_t)n);
+            NxtKvAdmit a;
+            const int r = nxt_kv_seq_admit(st->index, it.io.token_ids, n, mapping.data(),
+                                           src.data(), dst.data(), &a);
+            if (r != NXT_KV_OK) {
+                rc = fail("exec: admitting %s failed (%d)", it.id.c_str(), r);
+                break;
+            }
+            it.seq = a.seq;
+            st->seqs[it.id] = a.seq;
+            slots = mapping;
+            for (int c = 0; c < a.copy_count; ++c) {
+                st->h_src.push(src[(size_t)c]);
+                st->h_dst.push(dst[(size_t)c]);
+            }
+        } else {
+            const int r = nxt_kv_seq_append(st->index, it.seq, it.io.token_ids, n, slots.data());
+            if (r != NXT_KV_OK) {
+                rc = fail("exec: appending to %s failed (%d)", it.id.c_str(), r);
+                break;
+            }
+        }
+        for (int t = 0; t < n; ++t) {
+            if (slots[(size_t)t] < 0) continue;
+            st->h_slots.push(slots[(size_t)t]);
+            st->h_kptr.push((const char *)it.io.key + (size_t)t * kv_row);
+            st->h_vptr.push((const char *)it.io.value + (size_t)t * kv_row);
+        }
+    }
+
+    // 2. copies of partly shared pages, then the new rows (one launch each)
+    hipError_t e = hipSuccess;
+    xhip::KvAppendParams p;
+    std::memset(&p, 0, sizeof(p));
+    p.key_cache = st->key_cache;
+    p.value_cache = st->value_cache;
+    p.kv_block_stride_bytes = (long long)s.num_kv_heads * s.block_size * s.head_size * s.elem_bytes;
+    p.kv_head_stride_bytes = (long long)s.block_size * s.head_size * s.elem_bytes;
+    p.num_kv_heads = s.num_kv_heads;
+    p.row_bytes = s.head_size * s.elem_bytes;
+    p.row_chunks = p.row_bytes / 16;
+    p.block_size = s.block_size;
+    p.bs_shift = __builtin_ctz((unsigned)s.block_size);
+    if (st->h_src.n) {
+        if ((e = upload(st->d_src, st->h_src, st->stream)) == hipSuccess &&
+            (e = upload(st->d_dst, st->h_dst, st->stream)) == hipSuccess) {
+            xhip::KvAppendParams c = p;
+            c.key = st->key_cache;
+            c.value = st->value_cache;
+            c.slots = st->d_dst.p;
+            c.src_slots = st->d_src.p;
+            c.num_tokens = (int)st->h_src.n;
+            e = xhip::launch_kv_append(c, st->stream);
+        }
+    }
+    if (e == hipSuccess && st->h_slots.n) {
+        if ((e = upload(st->d_slots, st->h_slots, st->stream)) == hipSuccess &&
+            (e = upload(st->d_kptr, st->h_kptr, st->stream)) == hipSuccess &&
+            (e = upload(st->d_vptr, st->h_vptr, st->stream)) == hipSuccess) {
+            xhip::KvAppendParams w = p;
+            w.slots = st->d_slots.p;
+            w.key_rows = st->d_kptr.p;
+            w.value_rows = st->d_vptr.p;
+            w.num_tokens = (int)st->h_slots.n;
+            e = xhip::launch_kv_append(w, st->stream);
+        }
+    }
+    if (e != hipSuccess) rc = fail("exec: K/V write: %s", hipGetErrorString(e));
+
+    // 3. decode attention for the requests with a query
+    if (rc == 0) {
+        st->h_seqs.n = st->h_qptr.n = st->h_optr.n = 0;
+        for (const Item &it : items) {
+            if (!it.io.query) continue;
+            st->h_seqs.push(it.seq);
+            st->h_qptr.push((const char *)it.io.query);
+            st->h_optr.push((char *)it.io.output);
+        }
+        const int B = (int)st->h_seqs.n;
+        if (B > 0) {
+            int width = 1;
+            for (int i = 0; i < B; ++i) {
+                const int len = nxt_kv_seq_len(st->index, st->h_seqs.p[i]);
+                width = std::max(width, (len + s.block_size - 1) / s.block_size);
+            }
+            const size_t row = (size_t)s.num_heads * s.head_size * s.elem_bytes;
+            int32_t ng = 0;
+            if (!st->h_bt.reserve((size_t)B * width) || !st->h_lens.reserve((size_t)B) ||
+                !st->h_group.reserve((size_t)B) || !st->h_pblocks.reserve((size_t)B / 2 + 1)) {
+                rc = fail("exec: out of host memory");
+            } else {
+                st->h_bt.n = (size_t)B * width;
+                st->h_lens.n = st->h_group.n = (size_t)B;
+                nxt_kv_batch_tables(st->index, st->h_seqs.p, B, width, st->h_bt.p, st->h_lens.p);
+                nxt_kv_batch_prefix_groups(st->index, st->h_seqs.p, B, st->h_group.p,
+                                           st->h_pblocks.p, &ng);
+                st->h_pblocks.n = (size_t)std::max(ng, 1);
+                if ((e = upload(st->d_bt, st->h_bt, st->stream)) == hipSuccess &&
+                    (e = upload(st->d_lens, st->h_lens, st->stream)) == hipSuccess &&
+                    (e = upload(st->d_qptr, st->h_qptr, st->stream)) == hipSuccess &&
+                    (e = upload(st->d_optr, st->h_optr, st->stream)) == hipSuccess)
+                    e = xhip::launch_gather_rows(st->d_q.p, st->d_qptr.p, (int)row, B, st->stream);
+                if (e == hipSuccess && ng > 0 &&
+                    (e = upload(st->d_group, st->h_group, st->stream)) == hipSuccess)
+                    e = upload(st->d_pblocks, st->h_pblocks, st->stream);
+                int a = NXT_ATTN_OK;
+                if (e == hipSuccess) {
+                    const int kbs = s.num_kv_heads * s.block_size * s.head_size;
+                    const int khs = s.block_size * s.head_size;
+                    a = ng > 0 ? nxt_paged_attention_cascade(
+                                     st->d_out.p, st->d_q.p, st->key_cache, st->value_cache,
+                                     st->d_bt.p, st->d_lens.p, st->d_group.p, st->d_pblocks.p, ng,
+                                     B, s.num_heads, s.head_size, s.num_kv_heads, s.scale, width,
+                                     s.block_size, kbs, khs, s.kv_dtype, st->stream)
+                               : nxt_paged_attention_ex(
+                                     st->d_out.p, st->d_q.p, st->key_cache, st->value_cache,
+                                     st->d_bt.p, st->d_lens.p, B, s.num_heads, s.head_size,
+                                     s.num_kv_heads, s.scale, width, s.block_size, s.elem_bytes,
+                                     kbs, khs, st->stream, s.kv_dtype, 0);
+                    if (a == NXT_ATTN_OK)
+                        e = xhip::launch_scatter_rows(st->d_optr.p, st->d_out.p, (int)row, B,
+                                                      st->stream);
+                }
+                if (e != hipSuccess) rc = fail("exec: attention: %s", hipGetErrorString(e));
+                if (a != NXT_ATTN_OK) rc = fail("exec: attention: %s", nxt_attn_last_error());
+            }
+        }
+    }
+
+    // 4. wait for the device, then end the released requests
+    e = hipStreamSynchronize(st->stream);
+    if (e != hipSuccess && rc == 0) rc = fail("exec: %s", hipGetErrorString(e));
+    for (const Item &it : items) {
+        st->bound.erase(it.id);
+        if (rc == 0 && it.io.release && it.seq >= 0) {
+            nxt_kv_seq_release(st->index, it.seq, 1);
+            st->seqs.erase(it.id);
+        }
+    }
+    instance->exec_count++;
+    instance->total_exec_ms +=
+        std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    return rc;
+}

@@ -13,6 +13,8 @@ struct KvAppendParams {
     const void *value;         // themselves when src_slots is set
     const int *src_slots;      // [num_tokens] copy mode: token i's rows are read from
                                // this cache slot (null: from key / value)
+    const char *const *key_rows;    // [num_tokens] gather mode: token i's [num_kv_heads]
+    const char *const *value_rows;  // rows start at key_rows[i] / value_rows[i]
     const int *slots;          // [num_tokens] flat slots, or null: use block_tables + positions
     const int *block_tables;   // [num_tokens][max_blocks] (decode: token s = sequence s)
     const int *positions;      // [num_tokens]
@@ -29,5 +31,13 @@ struct KvAppendParams {
 };
 
 hipError_t launch_kv_append(const KvAppendParams &p, hipStream_t stream);
+
+// Row i (row_bytes, a multiple of 16) of src[i] -> dst + i * row_bytes, and
+// back: the per-request query / output buffers of a batch to and from the
+// contiguous [num_seqs][num_heads][head_size] tensors of the decode kernels.
+hipError_t launch_gather_rows(void *dst, const char *const *src, int row_bytes, int n,
+                              hipStream_t stream);
+hipError_t launch_scatter_rows(char *const *dst, const void *src, int row_bytes, int n,
+                               hipStream_t stream);
 
 }  // namespace xhip

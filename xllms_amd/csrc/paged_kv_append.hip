@@ -53,6 +53,13 @@ __global__ __launch_bounds__(256) void paged_kv_append_kernel(const KvAppendPara
             src = (size_t)((from >> p.bs_shift) * p.kv_block_stride_bytes +
                            h * p.kv_head_stride_bytes +
                            (from & (p.block_size - 1)) * p.row_bytes) + (size_t)c * 16;
+        } else if (p.key_rows) {  // each token's rows at their own address
+            const size_t o = (size_t)h * p.row_bytes + (size_t)c * 16;
+            const u32x4 k = *(const u32x4 *)(p.key_rows[tok] + o);
+            const u32x4 v = *(const u32x4 *)(p.value_rows[tok] + o);
+            *(u32x4 *)((char *)p.key_cache + dst) = k;
+            *(u32x4 *)((char *)p.value_cache + dst) = v;
+            continue;
         } else {
             src = (size_t)row * p.row_bytes + (size_t)c * 16;
         }
@@ -69,6 +76,49 @@ hipError_t launch_kv_append(const KvAppendParams &p, hipStream_t stream) {
     long long blocks = (n_chunks + 255) / 256;
     if (blocks > 65536) blocks = 65536;  // grid-stride beyond
     paged_kv_append_kernel<<<(unsigned)blocks, 256, 0, stream>>>(p);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void gather_rows_kernel(char *dst, const char *const *src,
+                                                          int chunks, int n) {
+    const long long total = (long long)n * chunks;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const int r = (int)(i / chunks), c = (int)(i % chunks);
+        *(u32x4 *)(dst + i * 16) = *(const u32x4 *)(src[r] + (size_t)c * 16);
+    }
+}
+
+__global__ __launch_bounds__(256) void scatter_rows_kernel(char *const *dst, const char *src,
+                                                           int chunks, int n) {
+    const long long total = (long long)n * chunks;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const int r = (int)(i / chunks), c = (int)(i % chunks);
+        *(u32x4 *)(dst[r] + (size_t)c * 16) = *(const u32x4 *)(src + i * 16);
+    }
+}
+
+static unsigned copy_grid(long long chunks) {
+    long long blocks = (chunks + 255) / 256;
+    return (unsigned)(blocks > 4096 ? 4096 : blocks);
+}
+
+hipError_t launch_gather_rows(void *dst, const char *const *src, int row_bytes, int n,
+                              hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const int chunks = row_bytes / 16;
+    gather_rows_kernel<<<copy_grid((long long)n * chunks), 256, 0, stream>>>((char *)dst, src,
+                                                                              chunks, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_scatter_rows(char *const *dst, const void *src, int row_bytes, int n,
+                               hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const int chunks = row_bytes / 16;
+    scatter_rows_kernel<<<copy_grid((long long)n * chunks), 256, 0, stream>>>(
+        dst, (const char *)src, chunks, n);
     return hipGetLastError();
 }
 
