@@ -209,6 +209,84 @@ def bench_kv_append(args) -> int:
     return 0 if unchanged else 1
 
 
+def bench_serve(args) -> int:
+    """Decode steps through the plugin's model instance: the path the
+    reference scheduler's poll reaches (src/core/scheduler.c:482-486,
+    instance_exec).  The config's prompts are admitted first (their K/V
+    written through the KV-cache index; config 5's shared prefixes are
+    matched and shared), then each timed step binds one new token, its K/V
+    rows and a query for every request and runs one exec over the whole
+    batch: index work on the host, staging uploads, the K/V write, the decode
+    attention (prefix-aware when the batch shares prefixes) and the output
+    scatter, waited for.  The binding calls and the request array (Python)
+    are outside the timed region; the native exec call is timed with the host
+    clock.  XLLM_HIP_EXEC_TRACE=1 prints each exec's phase times."""
+    import numpy as np
+    import torch
+    from xllms_amd import backend as B
+    from xllms_amd import workloads as W
+
+    name, H, KVH, D, kv_dtype, prompts = W.serve_prompts(args.config)
+    tdt = W.torch_dtype(kv_dtype)
+    nreq, bs = len(prompts), 16
+    lens = np.array([len(p) for p in prompts])
+    pages = int(sum(-(-(int(L) + args.warmup + args.steps + 1) // bs) for L in lens))
+    max_blocks = int(-(-(int(lens.max()) + args.warmup + args.steps + 1) // bs))
+    dtype_code = {W.FP16: B.NXT_TYPE_FP16, W.BF16: B.NXT_TYPE_BF16_HIP,
+                  W.FP32: B.NXT_TYPE_FP32}[kv_dtype]
+    m = B.DecodeModel(num_blocks=pages + 64, num_kv_heads=KVH, block_size=bs, head_size=D,
+                      num_heads=H, dtype=dtype_code, max_batch_size=nreq,
+                      max_blocks_per_seq=max_blocks)
+    if m.status != 0:
+        raise RuntimeError("nxt_model_init failed")
+    rids = [f"r{i}" for i in range(nreq)]
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    t_prefill = time.perf_counter()
+    for i, (rid, prompt) in enumerate(zip(rids, prompts)):
+        kv = torch.randn((2, len(prompt), KVH, D), generator=gen, device="cuda").to(tdt)
+        assert m.bind(rid, tokens=prompt, key=kv[0], value=kv[1]) == 0
+        if m.exec([rid]) != 0:
+            raise RuntimeError(f"prefill of {rid} failed")
+    t_prefill = time.perf_counter() - t_prefill
+    kv_new = torch.randn((2, nreq, KVH, D), generator=gen, device="cuda").to(tdt)
+    q = torch.randn((nreq, H, D), generator=gen, device="cuda").to(tdt)
+    out = torch.empty_like(q)
+    rng = np.random.default_rng(11)
+    batch = m.requests(rids)
+    times = []
+    for step in range(args.warmup + args.steps):
+        toks = rng.integers(0, 32000, nreq)
+        for i, rid in enumerate(rids):
+            m.bind(rid, tokens=[int(toks[i])], key=kv_new[0, i:i + 1], value=kv_new[1, i:i + 1],
+                   query=q[i], output=out[i])
+        t0 = time.perf_counter()
+        rc = m.exec_requests(batch)
+        dt = time.perf_counter() - t0
+        if rc != 0:
+            raise RuntimeError(f"exec failed at step {step}")
+        if step >= args.warmup:
+            times.append(dt)
+    ok = bool(torch.isfinite(out.float()).all())
+    exec_count = int(m.model.instances[0].exec_count)
+    med = float(np.median(times))
+    m.close()
+    log(f"[bench] serve {name}: {nreq} requests, prefill {t_prefill:.2f} s; decode exec median "
+        f"{med * 1e6:.1f} us (min {min(times) * 1e6:.1f}, max {max(times) * 1e6:.1f}); "
+        f"finite outputs: {ok}")
+    print(json.dumps({
+        "metric": "decode step through the model instance (instance_exec, whole batch)",
+        "value": round(nreq / med, 1), "unit": "seqs/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(med * 1e3, 4), "higher_is_better": True,
+        "dtype": {W.FP16: "fp16", W.BF16: "bf16", W.FP32: "fp32"}[kv_dtype],
+        "data": "synthetic (seeded prompts of the config's lengths, random K/V on device)",
+        "config": {"workload": name, "requests": nreq, "context_tokens": int(lens.sum())},
+        "exec_us": {"median": round(med * 1e6, 1), "min": round(min(times) * 1e6, 1),
+                    "max": round(max(times) * 1e6, 1)},
+        "instance_exec_count": exec_count,
+        "check": {"outputs_finite": ok}}), flush=True)
+    return 0 if ok else 1
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -225,6 +303,8 @@ def main() -> int:
                     help="prefix-aware decode (nxt_paged_attention_cascade): shared prefixes found "
                          "once from the block tables (nxt_paged_prefix_groups, outside the timed "
                          "steps), each step one cascade call")
+    ap.add_argument("--serve", action="store_true",
+                    help="decode steps through the plugin's model instance (configs 2, 4, 5, 6)")
     ap.add_argument("--kv-append", action="store_true",
                     help="instead of the attention, time the KV append on the workload's shape: "
                          "every token of the batch written through nxt_paged_kv_write_slots "
@@ -259,6 +339,8 @@ def main() -> int:
     from xllms_amd import paged_attention as PA
     from xllms_amd import workloads as W
 
+    if args.serve:
+        return bench_serve(args)
     if args.kv_append:
         return bench_kv_append(args)
 

@@ -108,6 +108,13 @@ def test_scheduler_style_and_batched_exec(cuda):
     b = c.bind("late", ext, rng)
     assert m.exec(["late"]) == 0
     c.check(["late"], {"late": b}, "late admission")
+    # two new requests with a common new prefix in one exec: the second's copy
+    # of the partly shared page reads rows the same exec writes
+    twin = list(rng.integers(0, 60, 50))
+    binds = {"twinA": c.bind("twinA", twin + [1, 2, 3], rng),
+             "twinB": c.bind("twinB", twin + [4, 5], rng)}
+    assert m.exec(["twinA", "twinB"]) == 0
+    c.check(["twinA", "twinB"], binds, "twins admitted together")
     inst = m.model.instances[0]
     assert inst.exec_count > 0 and inst.total_exec_ms > 0
     # errors: unbound request, duplicate id in one batch

@@ -287,7 +287,9 @@ class DecodeModel:
         return self.dl.nxt_model_instance_bind(self.instance, request_id.encode(),
                                                ctypes.byref(io))
 
-    def exec(self, request_ids) -> int:
+    def requests(self, request_ids):
+        """The NxtInferRequest* array of a batch, built once and reusable
+        (exec_requests) while the ids stay the same."""
         ids = [r.encode() for r in request_ids]
         reqs = (NxtInferRequest * max(1, len(ids)))()
         ptrs = (ctypes.POINTER(NxtInferRequest) * max(1, len(ids)))()
@@ -295,10 +297,17 @@ class DecodeModel:
             reqs[i].request_id = rid
             reqs[i].batch_size = 1
             ptrs[i] = ctypes.pointer(reqs[i])
-        rc = self.dl.nxt_model_instance_exec(self.instance, ctypes.cast(ptrs, ctypes.c_void_p),
-                                             len(ids))
+        return (ids, reqs, ptrs, len(ids))
+
+    def exec_requests(self, prepared) -> int:
+        rc = self.dl.nxt_model_instance_exec(self.instance,
+                                             ctypes.cast(prepared[2], ctypes.c_void_p),
+                                             prepared[3])
         self._io_keep = []
         return rc
+
+    def exec(self, request_ids) -> int:
+        return self.exec_requests(self.requests(request_ids))
 
     def close(self) -> int:
         rc = self.dl.nxt_model_fini(ctypes.byref(self.model))

@@ -511,11 +511,11 @@ XKV_EXPORT int nxt_kv_batch_append(NxtKvIndex *ix, const int32_t *seqs, int32_t 
     if (!ix || n < 0 || (n > 0 && (!seqs || !tokens || !slots))) return NXT_KV_E_INVALID;
     const int bs = ix->block_size;
     int need = 0;
+    std::vector<char> seen(ix->seqs.size(), 0);
     for (int32_t i = 0; i < n; ++i) {
         const Sequence *s = ix->seq(seqs[i]);
-        if (!s) return NXT_KV_E_INVALID;
-        for (int32_t j = 0; j < i; ++j)
-            if (seqs[j] == seqs[i]) return NXT_KV_E_INVALID;
+        if (!s || seen[(size_t)seqs[i]]) return NXT_KV_E_INVALID;
+        seen[(size_t)seqs[i]] = 1;
         const long long len = (long long)s->tokens.size();
         if (len + 1 > (long long)ix->max_blocks * bs) return NXT_KV_E_CAPACITY;
         need += (len & (bs - 1)) == 0;

@@ -14,6 +14,7 @@
 #include <cstring>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "paged_kv_append.h"
@@ -113,10 +114,25 @@ struct InstanceState {
     HostBuf<int32_t> h_slots, h_src, h_dst, h_bt, h_lens, h_group, h_pblocks, h_seqs;
     HostBuf<const char *> h_kptr, h_vptr, h_qptr;
     HostBuf<char *> h_optr;
-    DevBuf<int32_t> d_slots, d_src, d_dst, d_bt, d_lens, d_group, d_pblocks;
-    DevBuf<const char *> d_kptr, d_vptr, d_qptr;
-    DevBuf<char *> d_optr;
     DevBuf<char> d_q, d_out;
+    HostBuf<char> h_pack;  // every array an exec uploads, 256-byte aligned parts
+    DevBuf<char> d_pack;
+
+    // Appends h's contents to h_pack at a 256-byte boundary; returns its
+    // offset (h_pack.n becomes -1 when host memory runs out).
+    template <class T>
+    size_t pack(const HostBuf<T> &h) {
+        if (h_pack.n == (size_t)-1) return 0;
+        const size_t off = (h_pack.n + 255) & ~(size_t)255;
+        const size_t bytes = h.n * sizeof(T);
+        if (!h_pack.reserve(off + bytes)) {
+            h_pack.n = (size_t)-1;
+            return 0;
+        }
+        if (bytes) std::memcpy(h_pack.p + off, h.p, bytes);
+        h_pack.n = bytes ? off + bytes : h_pack.n;
+        return off;
+    }
 };
 
 const NxtTensor *find_input(const NxtModelConfig &c, const char *name) {
@@ -193,13 +209,8 @@ void destroy_state(InstanceState *st) {
     st->h_vptr.release();
     st->h_qptr.release();
     st->h_optr.release();
-    for (auto *b : {&st->d_slots, &st->d_src, &st->d_dst, &st->d_bt, &st->d_lens, &st->d_group,
-                    &st->d_pblocks})
-        b->release();
-    st->d_kptr.release();
-    st->d_vptr.release();
-    st->d_qptr.release();
-    st->d_optr.release();
+    st->h_pack.release();
+    st->d_pack.release();
     st->d_q.release();
     st->d_out.release();
     if (st->stream) (void)hipStreamDestroy(st->stream);
@@ -207,12 +218,37 @@ void destroy_state(InstanceState *st) {
     delete st;
 }
 
-template <class T>
-hipError_t upload(DevBuf<T> &d, const HostBuf<T> &h, hipStream_t s) {
-    if (h.n == 0) return hipSuccess;
-    if (!d.reserve(h.n)) return hipErrorOutOfMemory;
-    return hipMemcpyAsync(d.p, h.p, h.n * sizeof(T), hipMemcpyHostToDevice, s);
-}
+// With XLLM_HIP_EXEC_TRACE=1 in the environment, each exec prints the host
+// time of its phases (microseconds) to stderr.
+struct PhaseTrace {
+    using clock = std::chrono::steady_clock;
+    explicit PhaseTrace(clock::time_point t0) : last(t0), on(enabled()) {}
+    static bool enabled() {
+        static const bool e = [] {
+            const char *v = std::getenv("XLLM_HIP_EXEC_TRACE");
+            return v && *v && *v != '0';
+        }();
+        return e;
+    }
+    void mark(const char *name) {
+        if (!on || n >= 8) return;
+        const clock::time_point t = clock::now();
+        names[n] = name;
+        us[n++] = std::chrono::duration<double, std::micro>(t - last).count();
+        last = t;
+    }
+    void report(uint32_t requests) const {
+        if (!on) return;
+        std::fprintf(stderr, "[hip_backend] exec %u requests:", requests);
+        for (int i = 0; i < n; ++i) std::fprintf(stderr, " %s %.1f", names[i], us[i]);
+        std::fprintf(stderr, " us\n");
+    }
+    clock::time_point last;
+    bool on;
+    int n = 0;
+    const char *names[8];
+    double us[8];
+};
 
 struct Item {
     std::string id;
@@ -332,19 +368,22 @@ XMI_EXPORT int nxt_model_instance_exec(NxtModelInstance *instance, NxtInferReque
     if (!st || (request_count && !requests)) return -1;
     const ModelSpec &s = st->spec;
     const auto t0 = std::chrono::steady_clock::now();
+    PhaseTrace tr(t0);
     if ((int)request_count > s.max_batch)
         return fail("exec: %u requests > max_batch_size %d", request_count, s.max_batch);
 
     // every request bound, each once
     std::vector<Item> items;
     items.reserve(request_count);
+    std::unordered_set<std::string> ids;
+    ids.reserve(request_count * 2);
     for (uint32_t i = 0; i < request_count; ++i) {
         if (!requests[i] || !requests[i]->request_id) return fail("exec: request %u has no id", i);
         const std::string id = requests[i]->request_id;
         auto b = st->bound.find(id);
         if (b == st->bound.end()) return fail("exec: request %s has no bound buffers", id.c_str());
-        for (const Item &it : items)
-            if (it.id == id) return fail("exec: request %s twice in one batch", id.c_str());
+        if (!ids.insert(id).second)
+            return fail("exec: request %s twice in one batch", id.c_str());
         auto q = st->seqs.find(id);
         items.push_back({id, b->second, q == st->seqs.end() ? -1 : q->second});
         if (items.back().seq < 0 && b->second.num_tokens == 0)
@@ -352,6 +391,7 @@ XMI_EXPORT int nxt_model_instance_exec(NxtModelInstance *instance, NxtInferReque
     }
     if (hipSetDevice(st->device) != hipSuccess) return fail("exec: hipSetDevice failed");
 
+    tr.mark("validate");
     // 1. sequences: admissions and appends; the K/V rows to write and copy
     const size_t kv_row = (size_t)s.num_kv_heads * s.head_size * s.elem_bytes;
     st->h_slots.n = st->h_src.n = st->h_dst.n = st->h_kptr.n = st->h_vptr.n = 0;
@@ -374,6 +414,9 @@ XMI_EXPORT int nxt_model_instance_exec(NxtModelInstance *instance, NxtInferReque
             }
             it.seq = a.seq;
             st->seqs[it.id] = a.seq;
+            // the prompt becomes shareable at once: later admissions (also in
+            // this exec: their copies run after this exec's writes) find it
+            nxt_kv_seq_cache(st->index, a.seq);
             slots = mapping;
             for (int c = 0; c < a.copy_count; ++c) {
                 st->h_src.push(src[(size_t)c]);
@@ -394,8 +437,65 @@ XMI_EXPORT int nxt_model_instance_exec(NxtModelInstance *instance, NxtInferReque
         }
     }
 
-    // 2. copies of partly shared pages, then the new rows (one launch each)
+    tr.mark("index");
+    // 2. the attention batch: requests with a query, their tables and groups
+    const size_t qrow = (size_t)s.num_heads * s.head_size * s.elem_bytes;
+    st->h_seqs.n = st->h_qptr.n = st->h_optr.n = 0;
+    st->h_bt.n = st->h_lens.n = st->h_group.n = st->h_pblocks.n = 0;
+    int width = 1, ng = 0;
+    if (rc == 0) {
+        for (const Item &it : items) {
+            if (!it.io.query) continue;
+            st->h_seqs.push(it.seq);
+            st->h_qptr.push((const char *)it.io.query);
+            st->h_optr.push((char *)it.io.output);
+            const int len = nxt_kv_seq_len(st->index, it.seq);
+            width = std::max(width, (len + s.block_size - 1) / s.block_size);
+        }
+        const int B = (int)st->h_seqs.n;
+        if (B > 0) {
+            if (!st->h_bt.reserve((size_t)B * width) || !st->h_lens.reserve((size_t)B) ||
+                !st->h_group.reserve((size_t)B) || !st->h_pblocks.reserve((size_t)B / 2 + 1)) {
+                rc = fail("exec: out of host memory");
+            } else {
+                st->h_bt.n = (size_t)B * width;
+                st->h_lens.n = st->h_group.n = (size_t)B;
+                nxt_kv_batch_tables(st->index, st->h_seqs.p, B, width, st->h_bt.p, st->h_lens.p);
+                nxt_kv_batch_prefix_groups(st->index, st->h_seqs.p, B, st->h_group.p,
+                                           st->h_pblocks.p, &ng);
+                st->h_pblocks.n = (size_t)std::max(ng, 1);
+            }
+        }
+    }
+
+    tr.mark("tables");
+    // 3. one upload of everything the launches read, then the launches: the
+    //    new rows, the copies of partly shared pages (a copy may read rows
+    //    this exec writes), the query gather, the attention, the output scatter
     hipError_t e = hipSuccess;
+    st->h_pack.n = 0;
+    const size_t o_slots = st->pack(st->h_slots), o_kptr = st->pack(st->h_kptr),
+                 o_vptr = st->pack(st->h_vptr), o_src = st->pack(st->h_src),
+                 o_dst = st->pack(st->h_dst), o_bt = st->pack(st->h_bt),
+                 o_lens = st->pack(st->h_lens), o_group = st->pack(st->h_group),
+                 o_pblocks = st->pack(st->h_pblocks), o_qptr = st->pack(st->h_qptr),
+                 o_optr = st->pack(st->h_optr);
+    // The rows of requests admitted or extended before a failure are still
+    // written: the index already holds their tokens.
+    bool staged = false;
+    if (st->h_pack.n == (size_t)-1) {
+        rc = fail("exec: out of host memory");
+    } else if (st->h_pack.n > 0) {
+        if (!st->d_pack.reserve(st->h_pack.n)) {
+            rc = fail("exec: out of device memory");
+        } else {
+            e = hipMemcpyAsync(st->d_pack.p, st->h_pack.p, st->h_pack.n, hipMemcpyHostToDevice,
+                               st->stream);
+            staged = e == hipSuccess;
+        }
+    }
+    char *const dp = st->d_pack.p;
+    auto at = [dp](size_t off) { return (void *)(dp + off); };
     xhip::KvAppendParams p;
     std::memset(&p, 0, sizeof(p));
     p.key_cache = st->key_cache;
@@ -407,92 +507,52 @@ XMI_EXPORT int nxt_model_instance_exec(NxtModelInstance *instance, NxtInferReque
     p.row_chunks = p.row_bytes / 16;
     p.block_size = s.block_size;
     p.bs_shift = __builtin_ctz((unsigned)s.block_size);
-    if (st->h_src.n) {
-        if ((e = upload(st->d_src, st->h_src, st->stream)) == hipSuccess &&
-            (e = upload(st->d_dst, st->h_dst, st->stream)) == hipSuccess) {
-            xhip::KvAppendParams c = p;
-            c.key = st->key_cache;
-            c.value = st->value_cache;
-            c.slots = st->d_dst.p;
-            c.src_slots = st->d_src.p;
-            c.num_tokens = (int)st->h_src.n;
-            e = xhip::launch_kv_append(c, st->stream);
-        }
+    if (staged && st->h_slots.n) {
+        xhip::KvAppendParams w = p;
+        w.slots = (const int *)at(o_slots);
+        w.key_rows = (const char *const *)at(o_kptr);
+        w.value_rows = (const char *const *)at(o_vptr);
+        w.num_tokens = (int)st->h_slots.n;
+        e = xhip::launch_kv_append(w, st->stream);
     }
-    if (e == hipSuccess && st->h_slots.n) {
-        if ((e = upload(st->d_slots, st->h_slots, st->stream)) == hipSuccess &&
-            (e = upload(st->d_kptr, st->h_kptr, st->stream)) == hipSuccess &&
-            (e = upload(st->d_vptr, st->h_vptr, st->stream)) == hipSuccess) {
-            xhip::KvAppendParams w = p;
-            w.slots = st->d_slots.p;
-            w.key_rows = st->d_kptr.p;
-            w.value_rows = st->d_vptr.p;
-            w.num_tokens = (int)st->h_slots.n;
-            e = xhip::launch_kv_append(w, st->stream);
-        }
+    if (staged && e == hipSuccess && st->h_src.n) {
+        xhip::KvAppendParams c = p;
+        c.key = st->key_cache;
+        c.value = st->value_cache;
+        c.slots = (const int *)at(o_dst);
+        c.src_slots = (const int *)at(o_src);
+        c.num_tokens = (int)st->h_src.n;
+        e = xhip::launch_kv_append(c, st->stream);
     }
     if (e != hipSuccess) rc = fail("exec: K/V write: %s", hipGetErrorString(e));
-
-    // 3. decode attention for the requests with a query
-    if (rc == 0) {
-        st->h_seqs.n = st->h_qptr.n = st->h_optr.n = 0;
-        for (const Item &it : items) {
-            if (!it.io.query) continue;
-            st->h_seqs.push(it.seq);
-            st->h_qptr.push((const char *)it.io.query);
-            st->h_optr.push((char *)it.io.output);
+    const int B = (int)st->h_seqs.n;
+    if (rc == 0 && staged && B > 0) {
+        int a = NXT_ATTN_OK;
+        e = xhip::launch_gather_rows(st->d_q.p, (const char *const *)at(o_qptr), (int)qrow, B,
+                                     st->stream);
+        if (e == hipSuccess) {
+            const int kbs = s.num_kv_heads * s.block_size * s.head_size;
+            const int khs = s.block_size * s.head_size;
+            const int *bt = (const int *)at(o_bt), *lens = (const int *)at(o_lens);
+            a = ng > 0 ? nxt_paged_attention_cascade(
+                             st->d_out.p, st->d_q.p, st->key_cache, st->value_cache, bt, lens,
+                             (const int *)at(o_group), (const int *)at(o_pblocks), ng, B,
+                             s.num_heads, s.head_size, s.num_kv_heads, s.scale, width,
+                             s.block_size, kbs, khs, s.kv_dtype, st->stream)
+                       : nxt_paged_attention_ex(st->d_out.p, st->d_q.p, st->key_cache,
+                                                st->value_cache, bt, lens, B, s.num_heads,
+                                                s.head_size, s.num_kv_heads, s.scale, width,
+                                                s.block_size, s.elem_bytes, kbs, khs, st->stream,
+                                                s.kv_dtype, 0);
+            if (a == NXT_ATTN_OK)
+                e = xhip::launch_scatter_rows((char *const *)at(o_optr), st->d_out.p, (int)qrow,
+                                              B, st->stream);
         }
-        const int B = (int)st->h_seqs.n;
-        if (B > 0) {
-            int width = 1;
-            for (int i = 0; i < B; ++i) {
-                const int len = nxt_kv_seq_len(st->index, st->h_seqs.p[i]);
-                width = std::max(width, (len + s.block_size - 1) / s.block_size);
-            }
-            const size_t row = (size_t)s.num_heads * s.head_size * s.elem_bytes;
-            int32_t ng = 0;
-            if (!st->h_bt.reserve((size_t)B * width) || !st->h_lens.reserve((size_t)B) ||
-                !st->h_group.reserve((size_t)B) || !st->h_pblocks.reserve((size_t)B / 2 + 1)) {
-                rc = fail("exec: out of host memory");
-            } else {
-                st->h_bt.n = (size_t)B * width;
-                st->h_lens.n = st->h_group.n = (size_t)B;
-                nxt_kv_batch_tables(st->index, st->h_seqs.p, B, width, st->h_bt.p, st->h_lens.p);
-                nxt_kv_batch_prefix_groups(st->index, st->h_seqs.p, B, st->h_group.p,
-                                           st->h_pblocks.p, &ng);
-                st->h_pblocks.n = (size_t)std::max(ng, 1);
-                if ((e = upload(st->d_bt, st->h_bt, st->stream)) == hipSuccess &&
-                    (e = upload(st->d_lens, st->h_lens, st->stream)) == hipSuccess &&
-                    (e = upload(st->d_qptr, st->h_qptr, st->stream)) == hipSuccess &&
-                    (e = upload(st->d_optr, st->h_optr, st->stream)) == hipSuccess)
-                    e = xhip::launch_gather_rows(st->d_q.p, st->d_qptr.p, (int)row, B, st->stream);
-                if (e == hipSuccess && ng > 0 &&
-                    (e = upload(st->d_group, st->h_group, st->stream)) == hipSuccess)
-                    e = upload(st->d_pblocks, st->h_pblocks, st->stream);
-                int a = NXT_ATTN_OK;
-                if (e == hipSuccess) {
-                    const int kbs = s.num_kv_heads * s.block_size * s.head_size;
-                    const int khs = s.block_size * s.head_size;
-                    a = ng > 0 ? nxt_paged_attention_cascade(
-                                     st->d_out.p, st->d_q.p, st->key_cache, st->value_cache,
-                                     st->d_bt.p, st->d_lens.p, st->d_group.p, st->d_pblocks.p, ng,
-                                     B, s.num_heads, s.head_size, s.num_kv_heads, s.scale, width,
-                                     s.block_size, kbs, khs, s.kv_dtype, st->stream)
-                               : nxt_paged_attention_ex(
-                                     st->d_out.p, st->d_q.p, st->key_cache, st->value_cache,
-                                     st->d_bt.p, st->d_lens.p, B, s.num_heads, s.head_size,
-                                     s.num_kv_heads, s.scale, width, s.block_size, s.elem_bytes,
-                                     kbs, khs, st->stream, s.kv_dtype, 0);
-                    if (a == NXT_ATTN_OK)
-                        e = xhip::launch_scatter_rows(st->d_optr.p, st->d_out.p, (int)row, B,
-                                                      st->stream);
-                }
-                if (e != hipSuccess) rc = fail("exec: attention: %s", hipGetErrorString(e));
-                if (a != NXT_ATTN_OK) rc = fail("exec: attention: %s", nxt_attn_last_error());
-            }
-        }
+        if (e != hipSuccess) rc = fail("exec: attention: %s", hipGetErrorString(e));
+        if (a != NXT_ATTN_OK) rc = fail("exec: attention: %s", nxt_attn_last_error());
     }
 
+    tr.mark("launch");
     // 4. wait for the device, then end the released requests
     e = hipStreamSynchronize(st->stream);
     if (e != hipSuccess && rc == 0) rc = fail("exec: %s", hipGetErrorString(e));
@@ -504,6 +564,8 @@ XMI_EXPORT int nxt_model_instance_exec(NxtModelInstance *instance, NxtInferReque
         }
     }
     instance->exec_count++;
+    tr.mark("wait");
+    tr.report(request_count);
     instance->total_exec_ms +=
         std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     return rc;

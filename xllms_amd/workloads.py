@@ -331,6 +331,39 @@ def config5(seed: int = 20260005, num_seqs: int = 256, groups: int = 16,
     return wl
 
 
+def serve_prompts(config: int, token_seed: int = 7):
+    """Token-level prompts with the sequence lengths of a config's batch (the
+    same seeded draws as its generator) for the serving path, which builds
+    its own K/V; no K/V pool is made here.  Config 5 keeps its sharing: each
+    group's members start with the same P-token prefix.  Returns
+    (workload name, num_heads, num_kv_heads, head_size, kv_dtype, prompts)."""
+    tok = np.random.default_rng(token_seed)
+    if config == 5:
+        rng = np.random.default_rng(20260005)
+        B, groups, n_fresh = 256, 16, 25
+        prefix = rng.integers(256, 2048, size=groups, endpoint=True)
+        suffix = rng.integers(1, 1024, size=B, endpoint=True)
+        heads = [tok.integers(0, 32000, int(p)).astype(np.int32) for p in prefix]
+        prompts = [tok.integers(0, 32000, 1).astype(np.int32) for _ in range(n_fresh)]
+        for s in range(n_fresh, B):
+            g = (s - n_fresh) % groups
+            prompts.append(np.concatenate([heads[g], tok.integers(0, 32000, int(suffix[s]))
+                                           .astype(np.int32)]))
+        return "radix-shared-prefix-fp16", 32, 8, 128, FP16, prompts
+    if config == 2:
+        rng = np.random.default_rng(20260002)
+        L = rng.integers(512, 4096, size=64, endpoint=True)
+        name, H, KVH, D, dt = "llama3-8b-gqa4-fp16", 32, 8, 128, FP16
+    elif config in (4, 6):
+        rng = np.random.default_rng(20260004)
+        L = np.clip(np.round(np.exp(rng.normal(math.log(1024.0), 0.8, size=128))), 1, 8192)
+        KVH = 8 if config == 4 else 4
+        name, H, D, dt = f"llama-70b-gqa{64 // KVH}-bf16", 64, 128, BF16
+    else:
+        raise ValueError(f"serving prompts are defined for configs 2, 4, 5, 6, not {config}")
+    return name, H, KVH, D, dt, [tok.integers(0, 32000, int(n)).astype(np.int32) for n in L]
+
+
 CONFIGS = {
     1: config1,
     2: config2,
