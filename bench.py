@@ -209,6 +209,124 @@ def bench_kv_append(args) -> int:
     return 0 if unchanged else 1
 
 
+ACT_OPS = {"silu_and_mul": 1, "mul_and_silu": 2, "gelu_and_mul": 3, "gelu_tanh_and_mul": 4,
+           "gelu": 5, "silu": 6}
+
+
+def bench_activation(args) -> int:
+    """The MLP activation of the Llama-3-8B shape (intermediate size 14336,
+    fp16) over a prefill chunk of --act-tokens tokens, through the
+    reference-named entry point (nxt_silu_and_mul etc.).  Algorithmic bytes
+    per launch = input (2d or d elements per token) + output (d per token).
+    Steps alternate between two input/output pairs (each > the 256 MB MALL at
+    the default size).  Also times the decode-sized call (64 tokens)."""
+    import numpy as np
+    import torch
+    from oracle import oracle as O
+    from xllms_amd import activation as A
+    from xllms_amd import paged_attention as PA
+
+    op = ACT_OPS[args.activation]
+    entry = {v: k for k, v in A.ENTRY_POINTS.items()}[op]
+    gated = A.is_gated(op)
+    n, d = args.act_tokens, 14336
+    cols = 2 * d if gated else d
+    gen = torch.Generator(device="cuda").manual_seed(20260100 + op)
+    ins = [(torch.randn((n, cols), generator=gen, device="cuda") * 3).half() for _ in range(2)]
+    outs = [torch.empty((n, d), dtype=torch.float16, device="cuda") for _ in range(2)]
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream().cuda_stream
+    lib = PA._lib.backend()
+    fn = getattr(lib, entry)
+    call = [(outs[i].data_ptr(), ins[i].data_ptr(), n, d, 2, stream) for i in range(2)]
+    for i in range(args.warmup):
+        fn(*call[i % 2])
+    # one kernel per call: the launches run back to back between two events,
+    # so the average is the kernel's duration plus the short dispatch gap
+    ev = HipEvents()
+    e0, e1 = ev.create(), ev.create()
+    torch.cuda.synchronize()
+    ev.record(e0, stream)
+    for i in range(args.steps):
+        fn(*call[i % 2])
+    ev.record(e1, stream)
+    torch.cuda.synchronize()
+    st, msg = PA.last_status()
+    if st != 0:
+        raise RuntimeError(f"activation failed: {msg}")
+    avg_ms = ev.elapsed_ms(e0, e1) / args.steps
+    alg = n * (cols + d) * 2
+    gbs = alg / (avg_ms / 1e3) / 1e9
+    # decode-sized call: 64 tokens
+    dn = 64
+    for _ in range(args.warmup):
+        fn(outs[0].data_ptr(), ins[0].data_ptr(), dn, d, 2, stream)
+    torch.cuda.synchronize()
+    ev.record(e0, stream)
+    for _ in range(args.steps):
+        fn(outs[0].data_ptr(), ins[0].data_ptr(), dn, d, 2, stream)
+    ev.record(e1, stream)
+    torch.cuda.synchronize()
+    dec_us = ev.elapsed_ms(e0, e1) / args.steps * 1e3
+    ev.destroy_all()
+    # check 16 rows against the oracle: within 2 ulps, >= 99% bit-identical
+    fn(outs[0].data_ptr(), ins[0].data_ptr(), n, d, 2, stream)
+    torch.cuda.synchronize()
+    rows = np.linspace(0, n - 1, 16).astype(int)
+    xb = ins[0][rows].view(torch.int16).cpu().numpy().view(np.uint16)
+    got = outs[0][rows].view(torch.int16).cpu().numpy().astype(np.int64)
+    ref = O.activation(op, xb, O.FP16).view(np.int16).astype(np.int64)
+    mono = lambda b: np.where(b < 0, -(b & 0x7FFF), b)  # noqa: E731
+    dist = np.abs(mono(got) - mono(ref))
+    check = {"rows_checked": int(rows.size), "max_ulp": int(dist.max()),
+             "identical": round(float((dist == 0).mean()), 5)}
+    ok = check["max_ulp"] <= 2 and check["identical"] >= 0.99
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = O.lib().oracle_num_threads()
+        res = {}
+        for name, nthr in (("all", threads), ("single", 1)):
+            probe = xb[:2]
+            t0 = time.perf_counter()
+            O.activation(op, probe, O.FP16, threads=nthr)
+            per_tok = max(time.perf_counter() - t0, 1e-6) / 2
+            ntok = int(max(2, min(n, args.cpu_budget / 2 / per_tok)))
+            sample = ins[0][:ntok].view(torch.int16).cpu().numpy().view(np.uint16)
+            t0 = time.perf_counter()
+            O.activation(op, sample, O.FP16, threads=nthr)
+            dt = time.perf_counter() - t0
+            res[name] = {"tokens": ntok, "seconds": dt, "threads": nthr}
+        a = res["all"]
+        cpu = {"value": round(a["tokens"] / a["seconds"], 1), "unit": "tokens/s",
+               "cores": a["threads"], "kind": "port",
+               "sample": f"oracle/activation_oracle.c (C restatement of activation_kernels.cu:"
+                         f"24-134, gcc -O2, OpenMP over tokens) on {a['tokens']} tokens of this "
+                         f"batch in {a['seconds']:.1f}s",
+               "gbs_all_threads": round(a["tokens"] * (cols + d) * 2 / a["seconds"] / 1e9, 2),
+               "single_thread": {"value": round(res["single"]["tokens"] /
+                                                res["single"]["seconds"], 1),
+                                 "cores": 1, "sample": f"{res['single']['tokens']} tokens in "
+                                                       f"{res['single']['seconds']:.1f}s"}}
+    log(f"[bench] {entry} {n}x{d} fp16: {avg_ms * 1e3:.1f} us = "
+        f"{gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s); decode call ({dn} tokens) "
+        f"{dec_us:.2f} us; check {check}")
+    print(json.dumps({
+        "metric": f"{args.activation} tokens/s + achieved HBM GB/s (% peak), Llama-3-8B MLP shape",
+        "value": round(n / (avg_ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(avg_ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1)*3 activations)",
+        "config": {"workload": f"llama3-8b-mlp-{args.activation}-fp16", "tokens": n,
+                   "intermediate_size": d, "entry_point": entry},
+        "algorithmic_bytes": alg,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "activation_vec_kernel", "kernel_avg_us": round(avg_ms * 1e3, 2)},
+        "decode_call_us": round(dec_us, 2), "decode_tokens": dn,
+        "cpu_baseline": cpu, "check": check}), flush=True)
+    return 0 if ok else 1
+
+
 def bench_serve(args) -> int:
     """Decode steps through the plugin's model instance: the path the
     reference scheduler's poll reaches (src/core/scheduler.c:482-486,
@@ -309,6 +427,10 @@ def main() -> int:
                     help="instead of the attention, time the KV append on the workload's shape: "
                          "every token of the batch written through nxt_paged_kv_write_slots "
                          "(HBM-bound) and one decode step through nxt_paged_kv_append")
+    ap.add_argument("--activation", choices=sorted(ACT_OPS), default=None,
+                    help="instead of the attention, time this MLP activation (reference entry "
+                         "point, fp16, Llama-3-8B intermediate size 14336) over --act-tokens")
+    ap.add_argument("--act-tokens", type=int, default=8192)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run 5 plain device copies of MIB MiB "
                          "(the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -343,6 +465,8 @@ def main() -> int:
         return bench_serve(args)
     if args.kv_append:
         return bench_kv_append(args)
+    if args.activation:
+        return bench_activation(args)
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)

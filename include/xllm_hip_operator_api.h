@@ -219,6 +219,72 @@ int nxt_paged_kv_copy_slots(void *key_cache, void *value_cache, const int *src_s
                             int block_size, int kv_block_stride, int kv_head_stride, int kv_dtype,
                             nxt_stream_t stream);
 
+/* ---------------------------------------------------------- activations
+ * The MLP activations of the reference's operator API (include/operator_api.h:
+ * 118-150, implemented there by operators/activation_kernels.cu:52-239).
+ * Same names, argument order and meaning: input is [num_tokens][2*d] for the
+ * gated ops (row = gate | up, the gate being the first d elements) and
+ * [num_tokens][d] for the element-wise ones; out is [num_tokens][d].
+ * dtype_size 2 = fp16, 4 = fp32.  Per element, in fp32:
+ *   silu(x)      = x / (1 + exp(-x))
+ *   gelu(x)      = (x * 0.5) * (1 + erf(x / sqrt(2)))
+ *   gelu_tanh(x) = (0.5 * x) * (1 + tanh(sqrt(2/pi) * (x + 0.044715 x^3)))
+ * The activation is rounded to the element type and, for the gated ops,
+ * multiplied by the other operand in the element type (one rounding of the
+ * exact product), as the reference does (activation_kernels.cu:24-48, :65-69).
+ * Contract points the reference leaves undefined, fixed here: num_tokens or
+ * d of 0 does nothing (the reference's launch of 0 threads fails silently);
+ * a negative size, a NULL tensor or a dtype_size other than 2 / 4 (the
+ * reference treats every value but 2 as fp32) does nothing and records an
+ * error for nxt_attn_last_status(); offsets are 64-bit (no wrap at 2^32
+ * elements).  out must not overlap input, except that an element-wise op may
+ * run in place (out == input).  Asynchronous on `stream`. */
+
+/* Replaces nxt_silu_and_mul, include/operator_api.h:122-125:
+ * out = silu(gate) * up. */
+void nxt_silu_and_mul(void *out, const void *input, int num_tokens, int d, int dtype_size,
+                      nxt_stream_t stream);
+
+/* Replaces nxt_mul_and_silu, include/operator_api.h:127-130:
+ * out = gate * silu(up). */
+void nxt_mul_and_silu(void *out, const void *input, int num_tokens, int d, int dtype_size,
+                      nxt_stream_t stream);
+
+/* Replaces nxt_gelu_and_mul, include/operator_api.h:132-135:
+ * out = gelu(gate) * up (erf form). */
+void nxt_gelu_and_mul(void *out, const void *input, int num_tokens, int d, int dtype_size,
+                      nxt_stream_t stream);
+
+/* Replaces nxt_gelu_tanh_and_mul, include/operator_api.h:137-140:
+ * out = gelu_tanh(gate) * up. */
+void nxt_gelu_tanh_and_mul(void *out, const void *input, int num_tokens, int d, int dtype_size,
+                           nxt_stream_t stream);
+
+/* Replaces nxt_gelu_elementwise, include/operator_api.h:142-145:
+ * out = gelu(input). */
+void nxt_gelu_elementwise(void *out, const void *input, int num_tokens, int d, int dtype_size,
+                          nxt_stream_t stream);
+
+/* Replaces nxt_silu_elementwise, include/operator_api.h:147-150:
+ * out = silu(input). */
+void nxt_silu_elementwise(void *out, const void *input, int num_tokens, int d, int dtype_size,
+                          nxt_stream_t stream);
+
+/* Additive: the six activations above behind one entry point, with the
+ * element type named explicitly (NxtKvDtype codes, so bf16 too) and a 64-bit
+ * token count.  Returns NXT_ATTN_OK or a negative status. */
+typedef enum {
+    NXT_ACT_SILU_AND_MUL = 1,
+    NXT_ACT_MUL_AND_SILU = 2,
+    NXT_ACT_GELU_AND_MUL = 3,
+    NXT_ACT_GELU_TANH_AND_MUL = 4,
+    NXT_ACT_GELU = 5,
+    NXT_ACT_SILU = 6,
+} NxtActivationOp;
+
+int nxt_activation_ex(int op, void *out, const void *input, int64_t num_tokens, int d, int dtype,
+                      nxt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -209,3 +209,50 @@ def paged_kv_copy_slots(key_cache: np.ndarray, value_cache: np.ndarray, src, dst
     return paged_kv_append(key_cache, value_cache, k, v, block_size=block_size,
                            kv_block_stride=kv_block_stride, kv_head_stride=kv_head_stride,
                            slots=dst)
+
+
+ACT_SILU_AND_MUL, ACT_MUL_AND_SILU, ACT_GELU_AND_MUL, ACT_GELU_TANH_AND_MUL, ACT_GELU, ACT_SILU = \
+    range(1, 7)
+
+
+def _act_lib():
+    L = lib()
+    if not getattr(L, "_act_typed", False):
+        vp, ci, ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong
+        L.oracle_activation.argtypes = [ci, vp, vp, ll, ci, ci]
+        L.oracle_activation.restype = ci
+        L.oracle_activation_mt.argtypes = [ci, vp, vp, ll, ci, ci, ci]
+        L.oracle_activation_mt.restype = ci
+        L.oracle_float_to_half.argtypes = [ctypes.c_float]
+        L.oracle_float_to_half.restype = ctypes.c_uint16
+        L.oracle_float_to_bf16.argtypes = [ctypes.c_float]
+        L.oracle_float_to_bf16.restype = ctypes.c_uint16
+        L._act_typed = True
+    return L
+
+
+def activation(op: int, x: np.ndarray, dtype: int, threads: int = 0) -> np.ndarray:
+    """operators/activation_kernels.cu semantics (see oracle_activation):
+    x holds the element bits (uint16 for fp16/bf16, float32 for fp32), shape
+    [num_tokens, 2d] for the gated ops and [num_tokens, d] otherwise.
+    Returns the output bits [num_tokens, d] in the same numpy dtype."""
+    x = _c(x)
+    n = x.shape[0]
+    d = x.shape[1] // 2 if op <= ACT_GELU_TANH_AND_MUL else x.shape[1]
+    out = np.empty((n, d), dtype=x.dtype)
+    L = _act_lib()
+    if threads > 0:
+        rc = L.oracle_activation_mt(op, out.ctypes.data, x.ctypes.data, n, d, dtype, threads)
+    else:
+        rc = L.oracle_activation(op, out.ctypes.data, x.ctypes.data, n, d, dtype)
+    if rc != 0:
+        raise ValueError("oracle_activation rejected its arguments")
+    return out
+
+
+def float_to_half_bits(x: float) -> int:
+    return int(_act_lib().oracle_float_to_half(x))
+
+
+def float_to_bf16_bits(x: float) -> int:
+    return int(_act_lib().oracle_float_to_bf16(x))

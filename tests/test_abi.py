@@ -200,6 +200,30 @@ def test_kv_append_validation_without_launch():
     assert PA.last_status()[0] == PA.NXT_ATTN_E_UNSUPPORTED
 
 
+def test_activation_validation_without_launch():
+    """The activation entry points check their arguments before any device
+    call (these return without touching a GPU)."""
+    lib = _lib.backend()
+    p = 256
+    assert lib.nxt_activation_ex(0, p, p, 4, 16, PA.NXT_KV_FP16, None) == PA.NXT_ATTN_E_INVALID
+    assert lib.nxt_activation_ex(7, p, p, 4, 16, PA.NXT_KV_FP16, None) == PA.NXT_ATTN_E_INVALID
+    assert lib.nxt_activation_ex(1, p, p, 4, 16, 9, None) == PA.NXT_ATTN_E_UNSUPPORTED
+    assert lib.nxt_activation_ex(1, p, p, -1, 16, PA.NXT_KV_FP16, None) == PA.NXT_ATTN_E_INVALID
+    assert lib.nxt_activation_ex(1, p, p, 4, -16, PA.NXT_KV_FP16, None) == PA.NXT_ATTN_E_INVALID
+    assert lib.nxt_activation_ex(1, None, p, 4, 16, PA.NXT_KV_FP16, None) == PA.NXT_ATTN_E_INVALID
+    assert lib.nxt_activation_ex(1, p + 1, p, 4, 16, PA.NXT_KV_FP16, None) == PA.NXT_ATTN_E_INVALID
+    # nothing to do: OK without a device
+    assert lib.nxt_activation_ex(1, None, None, 0, 16, PA.NXT_KV_FP16, None) == PA.NXT_ATTN_OK
+    assert lib.nxt_activation_ex(6, None, None, 4, 0, PA.NXT_KV_FP32, None) == PA.NXT_ATTN_OK
+    # the reference's void entry points record their status; dtype_size other
+    # than 2 / 4 is refused (the reference would run it as fp32)
+    for name in _lib.ACTIVATION_ENTRY_POINTS:
+        getattr(lib, name)(p, p, 4, 16, 8, None)
+        assert lib.nxt_attn_last_status() == PA.NXT_ATTN_E_UNSUPPORTED, name
+        getattr(lib, name)(p, p, 0, 16, 2, None)
+        assert lib.nxt_attn_last_status() == PA.NXT_ATTN_OK, name
+
+
 def test_product_never_imports_the_oracle():
     """The product path (package + native sources) has no route to oracle/."""
     pkg = os.path.join(ROOT, "xllms_amd")

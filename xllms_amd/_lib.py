@@ -59,7 +59,16 @@ OPERATOR_SYMBOLS = (
     "nxt_paged_attention_cascade",
     "nxt_paged_prefix_groups",
     "nxt_paged_kv_copy_slots",
+    "nxt_silu_and_mul",
+    "nxt_mul_and_silu",
+    "nxt_gelu_and_mul",
+    "nxt_gelu_tanh_and_mul",
+    "nxt_gelu_elementwise",
+    "nxt_silu_elementwise",
+    "nxt_activation_ex",
 )
+# The reference-named activation entry points (include/operator_api.h:122-150).
+ACTIVATION_ENTRY_POINTS = OPERATOR_SYMBOLS[-7:-1]
 # include/xllm_hip_kv_index.h (host code in the same library)
 KV_INDEX_SYMBOLS = (
     "nxt_kv_index_create", "nxt_kv_index_destroy",
@@ -111,6 +120,13 @@ def backend() -> ctypes.CDLL:
         lib.nxt_paged_prefix_groups.restype = c_int
         lib.nxt_paged_kv_copy_slots.argtypes = [c_void_p] * 4 + [c_int] * 7 + [c_void_p]
         lib.nxt_paged_kv_copy_slots.restype = c_int
+        for name in ACTIVATION_ENTRY_POINTS:
+            fn = getattr(lib, name)
+            fn.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]
+            fn.restype = None
+        lib.nxt_activation_ex.argtypes = [c_int, c_void_p, c_void_p, ctypes.c_int64, c_int, c_int,
+                                          c_void_p]
+        lib.nxt_activation_ex.restype = c_int
         _type_kv_index(lib)
         lib._xllm_typed = True
     return lib

@@ -14,6 +14,7 @@
 #include <mutex>
 #include <vector>
 
+#include "activation.h"
 #include "paged_decode_cascade.h"
 #include "paged_decode_launch.h"
 #include "paged_decode_params.h"
@@ -579,6 +580,72 @@ int dtype_from_size(int dtype_size) {
     return 0;
 }
 
+// ------------------------------------------------------------- activations
+// Largest number of 16-byte output chunks one vector launch covers (its
+// indices are 32-bit, with headroom for the unrolled stride).
+constexpr long long kActMaxChunks = (1LL << 31) - 1;
+
+int activation_run(int op, void *out, const void *input, long long num_tokens, int d, int dtype,
+                   nxt_stream_t stream_handle) {
+    if (op < NXT_ACT_SILU_AND_MUL || op > NXT_ACT_SILU)
+        return set_status(NXT_ATTN_E_INVALID, "activation op %d is not an NxtActivationOp", op);
+    if (dtype != NXT_KV_FP16 && dtype != NXT_KV_BF16 && dtype != NXT_KV_FP32)
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "dtype %d is not FP16/BF16/FP32", dtype);
+    if (num_tokens < 0 || d < 0)
+        return set_status(NXT_ATTN_E_INVALID, "num_tokens %lld / d %d must be >= 0", num_tokens, d);
+    if (num_tokens == 0 || d == 0) return ok();
+    if (!out || !input) return set_status(NXT_ATTN_E_INVALID, "NULL tensor pointer");
+    const int eb = elem_bytes(dtype);
+    if (((uintptr_t)out | (uintptr_t)input) % (uintptr_t)eb)
+        return set_status(NXT_ATTN_E_INVALID, "tensors must be aligned to their element size");
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return set_status(NXT_ATTN_E_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    const int cus = cu_count(device);
+    const long long row_bytes = (long long)d * eb;
+    const bool vec = row_bytes % 16 == 0 && ((uintptr_t)out % 16) == 0 && ((uintptr_t)input % 16) == 0;
+    const int in_row_mult = xhip::act_is_gated(op) ? 2 : 1;
+    xhip::ActivationParams p;
+    memset(&p, 0, sizeof(p));
+    p.d = d;
+    p.dtype = dtype;
+    p.op = op;
+    if (!vec) {
+        p.out = out;
+        p.input = input;
+        p.num_tokens = num_tokens;
+        e = xhip::launch_activation(p, false, cus, (hipStream_t)stream_handle);
+        if (e != hipSuccess)
+            return set_status(NXT_ATTN_E_HIP, "activation launch: %s", hipGetErrorString(e));
+        return ok();
+    }
+    // Vector path: rows split into launches of < 2^31 output chunks each.
+    const long long rc = row_bytes / 16;
+    const long long rows_per_launch = kActMaxChunks / rc;
+    p.row_chunks = xhip::div_magic((uint32_t)rc);
+    for (long long t0 = 0; t0 < num_tokens; t0 += rows_per_launch) {
+        const long long rows = num_tokens - t0 < rows_per_launch ? num_tokens - t0 : rows_per_launch;
+        p.out = (char *)out + t0 * row_bytes;
+        p.input = (const char *)input + t0 * row_bytes * in_row_mult;
+        p.num_tokens = rows;
+        p.chunks = (uint32_t)(rows * rc);
+        e = xhip::launch_activation(p, true, cus, (hipStream_t)stream_handle);
+        if (e != hipSuccess)
+            return set_status(NXT_ATTN_E_HIP, "activation launch: %s", hipGetErrorString(e));
+    }
+    return ok();
+}
+
+void activation_legacy(int op, void *out, const void *input, int num_tokens, int d, int dtype_size,
+                       nxt_stream_t stream) {
+    const int dtype = dtype_from_size(dtype_size);
+    if (!dtype) {
+        set_status(NXT_ATTN_E_UNSUPPORTED, "dtype_size %d is not 2 (fp16) or 4 (fp32)", dtype_size);
+        return;
+    }
+    (void)activation_run(op, out, input, num_tokens, d, dtype, stream);
+}
+
 void run_legacy(void *out, const void *query, const void *key_cache, const void *value_cache,
                 const int *block_tables, const int *seq_lens, int num_seqs, int num_heads,
                 int head_size, int num_kv_heads, float scale, int max_num_blocks_per_seq,
@@ -690,6 +757,25 @@ __attribute__((visibility("default"))) int nxt_paged_kv_copy_slots(
     return kv_append_run(key_cache, value_cache, key_cache, value_cache, dst_slots, nullptr,
                          nullptr, num_tokens, num_kv_heads, head_size, 0, block_size,
                          kv_block_stride, kv_head_stride, kv_dtype, stream, src_slots);
+}
+
+#define XLLM_ACTIVATION_ENTRY(name, op)                                                            \
+    __attribute__((visibility("default"))) void name(void *out, const void *input, int num_tokens, \
+                                                     int d, int dtype_size, nxt_stream_t stream) { \
+        activation_legacy(op, out, input, num_tokens, d, dtype_size, stream);                      \
+    }
+XLLM_ACTIVATION_ENTRY(nxt_silu_and_mul, NXT_ACT_SILU_AND_MUL)
+XLLM_ACTIVATION_ENTRY(nxt_mul_and_silu, NXT_ACT_MUL_AND_SILU)
+XLLM_ACTIVATION_ENTRY(nxt_gelu_and_mul, NXT_ACT_GELU_AND_MUL)
+XLLM_ACTIVATION_ENTRY(nxt_gelu_tanh_and_mul, NXT_ACT_GELU_TANH_AND_MUL)
+XLLM_ACTIVATION_ENTRY(nxt_gelu_elementwise, NXT_ACT_GELU)
+XLLM_ACTIVATION_ENTRY(nxt_silu_elementwise, NXT_ACT_SILU)
+#undef XLLM_ACTIVATION_ENTRY
+
+__attribute__((visibility("default"))) int nxt_activation_ex(int op, void *out, const void *input,
+                                                             int64_t num_tokens, int d, int dtype,
+                                                             nxt_stream_t stream) {
+    return activation_run(op, out, input, num_tokens, d, dtype, stream);
 }
 
 __attribute__((visibility("default"))) int nxt_paged_attention_cascade(
