@@ -114,9 +114,23 @@ def test_unaligned_input(cuda, op, dt):
 
 @pytest.mark.parametrize("dt", DTYPES)
 @pytest.mark.parametrize("op", OPS)
+def test_vector_and_element_kernels_agree(cuda, op, dt):
+    """The same rows through the 16-byte chunk kernel (aligned input) and the
+    element kernel (input one element off alignment) give identical bits."""
+    d = 2048
+    xb = inputs(6, 2 * d if is_gated(op) else d, dt, seed=11 * op + dt, scale=30.0)
+    a = run(op, xb, dt, cuda)
+    b = run(op, xb, dt, cuda, offset=1)
+    assert (a.view(np.uint32 if dt == O.FP32 else np.uint16) ==
+            b.view(np.uint32 if dt == O.FP32 else np.uint16)).all()
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("op", OPS)
 def test_special_values(cuda, op, dt):
+    # -87.5 / -88: silu's fast form underflows there, bf16 takes the reference formula
     vals = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, -100.0, 100.0, 1e-6, -1e-6, 6e4, -6e4,
-                     -5.0, -9.0, 3.0, 2.0 ** -20, -(2.0 ** -20)])
+                     -5.0, -9.0, 3.0, 2.0 ** -20, -(2.0 ** -20), -87.5, -88.0])
     x = np.stack([np.roll(vals, k) for k in range(vals.size)])  # every value meets every other
     xb = to_bits(x, dt)
     if is_gated(op):
