@@ -19,10 +19,9 @@
 //
 // HBM-bound: a gated op reads 2d and writes d elements per row, an
 // element-wise op reads d and writes d.  The vector kernel gives each lane
-// whole 16-byte output chunks (8 fp16/bf16 or 4 fp32 elements) with the gate
-// and up chunks it needs loaded first, kUnroll chunks per lane per pass so
-// several 16-byte loads are in flight per lane; loads and stores are
-// nontemporal (streamed once).  Output chunk i lies in row t = i / (d*e/16),
+// one 16-byte output chunk (8 fp16/bf16 or 4 fp32 elements) and the gate and
+// up chunks it needs; loads and stores are nontemporal (streamed once).
+// Output chunk i lies in row t = i / (d*e/16),
 // and the gate chunk is at i + t*(d*e/16) of the input (the up chunk one row
 // half later), so a single division per chunk (a multiply-high) is the only
 // index work.  The element kernel covers every other shape (any d, any
@@ -44,8 +43,8 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
+constexpr int kBlock = 256;     // element kernel
+constexpr int kVecBlock = 64;   // vector kernel: one wavefront
 
 // The reference's fp32 formulas, with the device library's expf / erff /
 // tanhf and an IEEE divide.  Used for fp32 tensors (whose kernels are
@@ -220,53 +219,44 @@ template <int DT> __device__ __forceinline__ u32x4 pack(const float (&f)[Chunk<D
     return c;
 }
 
+// One 16-byte output chunk per lane, one pass, one wavefront per workgroup.
+// Measured on MI355X for fp16 silu_and_mul over 8192 x 14336 (704 MB): 104 us
+// (6.8 TB/s) this way, against 109 us with 256-lane workgroups and 116-125 us
+// for grid-stride loops of 2-8 chunks per lane; nontemporal loads and stores
+// are worth 8% together.
 template <int OP, int DT>
-__global__ __launch_bounds__(kBlock) void activation_vec_kernel(const ActivationParams p) {
+__global__ __launch_bounds__(kVecBlock) void activation_vec_kernel(const ActivationParams p) {
     constexpr int V = Chunk<DT>::kVec;
     const u32x4 *in = (const u32x4 *)p.input;
     u32x4 *out = (u32x4 *)p.out;
-    const uint32_t n = p.chunks;
-    const uint32_t rc = p.row_chunks.d;
-    const uint32_t stride = gridDim.x * kBlock;
-    for (uint32_t base = blockIdx.x * kBlock + threadIdx.x; base < n;
-         base += stride * kUnroll) {
-        u32x4 g[kUnroll], u[kUnroll];
-#pragma unroll
-        for (int k = 0; k < kUnroll; k++) {
-            const uint32_t i = base + k * stride;
-            if (i < n) {
-                if constexpr (act_is_gated(OP)) {
-                    const uint32_t t = div_by(i, p.row_chunks);
-                    const size_t gi = (size_t)i + (size_t)t * rc;
-                    g[k] = __builtin_nontemporal_load(in + gi);
-                    u[k] = __builtin_nontemporal_load(in + gi + rc);
-                } else {
-                    g[k] = __builtin_nontemporal_load(in + i);
-                }
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < kUnroll; k++) {
-            const uint32_t i = base + k * stride;
-            if (i < n) {
-                float gf[V], uf[V], of[V];
-                unpack<DT>(g[k], gf);
-                if constexpr (act_is_gated(OP)) unpack<DT>(u[k], uf);
-                else {
-#pragma unroll
-                    for (int e = 0; e < V; e++) uf[e] = 0.0f;
-                }
-                if (__builtin_expect(needs_ref<OP, DT>(gf, uf), 0)) {
-#pragma unroll
-                    for (int e = 0; e < V; e++) of[e] = apply<OP, DT, true>(gf[e], uf[e]);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < V; e++) of[e] = apply<OP, DT>(gf[e], uf[e]);
-                }
-                __builtin_nontemporal_store(pack<DT>(of), out + i);
-            }
-        }
+    const uint32_t i = blockIdx.x * kVecBlock + threadIdx.x;
+    if (i >= p.chunks) return;
+    u32x4 g, u;
+    if constexpr (act_is_gated(OP)) {
+        const uint32_t rc = p.row_chunks.d;
+        const uint32_t t = div_by(i, p.row_chunks);
+        const size_t gi = (size_t)i + (size_t)t * rc;
+        g = __builtin_nontemporal_load(in + gi);
+        u = __builtin_nontemporal_load(in + gi + rc);
+    } else {
+        g = __builtin_nontemporal_load(in + i);
     }
+    float gf[V], uf[V], of[V];
+    unpack<DT>(g, gf);
+    if constexpr (act_is_gated(OP)) {
+        unpack<DT>(u, uf);
+    } else {
+#pragma unroll
+        for (int e = 0; e < V; e++) uf[e] = 0.0f;
+    }
+    if (__builtin_expect(needs_ref<OP, DT>(gf, uf), 0)) {
+#pragma unroll
+        for (int e = 0; e < V; e++) of[e] = apply<OP, DT, true>(gf[e], uf[e]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < V; e++) of[e] = apply<OP, DT>(gf[e], uf[e]);
+    }
+    __builtin_nontemporal_store(pack<DT>(of), out + i);
 }
 
 template <int DT> __device__ __forceinline__ float load_elem(const void *base, size_t idx) {
@@ -305,13 +295,13 @@ __global__ __launch_bounds__(kBlock) void activation_elem_kernel(const Activatio
 template <int OP, int DT>
 hipError_t launch_typed(const ActivationParams &p, bool vector_path, int num_cus,
                         hipStream_t stream) {
-    // One resident round: 8 workgroups of 4 waves per CU (32 waves per CU).
+    // element kernel: a grid-stride loop over one resident round, 8
+    // workgroups of 4 wavefronts per CU
     const long long cap = (long long)(num_cus > 0 ? num_cus : 256) * 8;
     if (vector_path) {
-        long long blocks = ((long long)p.chunks + kBlock * kUnroll - 1) / (kBlock * kUnroll);
-        if (blocks > cap) blocks = cap;
-        if (blocks < 1) blocks = 1;
-        activation_vec_kernel<OP, DT><<<(unsigned)blocks, kBlock, 0, stream>>>(p);
+        const long long blocks = ((long long)p.chunks + kVecBlock - 1) / kVecBlock;
+        if (blocks < 1) return hipSuccess;
+        activation_vec_kernel<OP, DT><<<(unsigned)blocks, kVecBlock, 0, stream>>>(p);
     } else {
         long long blocks = (p.num_tokens * p.d + kBlock - 1) / kBlock;
         if (blocks > cap) blocks = cap;

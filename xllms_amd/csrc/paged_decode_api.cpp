@@ -581,8 +581,8 @@ int dtype_from_size(int dtype_size) {
 }
 
 // ------------------------------------------------------------- activations
-// Largest number of 16-byte output chunks one vector launch covers (its
-// indices are 32-bit, with headroom for the unrolled stride).
+// Largest number of 16-byte output chunks one vector launch covers: one lane
+// per chunk, and a launch's work-items and the kernel's indices are 32-bit.
 constexpr long long kActMaxChunks = (1LL << 31) - 1;
 
 int activation_run(int op, void *out, const void *input, long long num_tokens, int d, int dtype,
