@@ -7,9 +7,29 @@
  * page pool (the reference's own tests do the same,
  * tests/test_prefix_sharing.c:28-29).
  */
+#include <stdint.h>
 #include <stdlib.h>
+#include <time.h>
 
 #include "prefix_sharing.h"
+
+/* The tree stamps nodes with clock_gettime(CLOCK_MONOTONIC) in microseconds
+ * (prefix_sharing.c:18-23) and evicts the leaf with the oldest stamp.  In
+ * this test build that clock is a counter: this hidden definition binds the
+ * source's calls at link time, and every reading is one microsecond later
+ * than the one before.  The stamps then follow the order in which the tree
+ * reads its clock (a match or insert first, then each node it creates),
+ * which is the restatement's logical clock, whatever the host's scheduling
+ * does to real time between and inside calls. */
+static uint64_t g_now_us = 0;
+
+__attribute__((visibility("hidden"))) int clock_gettime(clockid_t id, struct timespec *ts) {
+    (void)id;
+    g_now_us++;
+    ts->tv_sec = (time_t)(g_now_us / 1000000u);
+    ts->tv_nsec = (long)(g_now_us % 1000000u) * 1000L;
+    return 0;
+}
 
 void *refps_new(void) {
     NxtPrefixTree *t = (NxtPrefixTree *)calloc(1, sizeof(NxtPrefixTree));

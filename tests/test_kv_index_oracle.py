@@ -19,7 +19,6 @@ from __future__ import annotations
 
 import os
 import random
-import time
 
 import numpy as np
 import pytest
@@ -167,15 +166,15 @@ def _rand_tokens(rng, stems, max_len=24):
 def test_tree_matches_reference_tree(seed):
     """Same operations on the restatement and on prefix_sharing.c: same match
     lengths and page lists, insert results, eviction results and statistics.
-    Each reference call is separated by 50 us so its microsecond timestamps
-    order the nodes the way the logical clock does."""
+    The reference's microsecond clock is, in the test build, a counter that
+    advances by one at every reading (oracle/ref_prefix_sharing_wrap.c), so its
+    timestamps order the nodes the way the logical clock does."""
     rng = random.Random(seed)
     ours, ref = K.PrefixTree(), K.RefPrefixTree()
     try:
         stems, handles, next_slot = [], [], 1000
         for step in range(260):
             op = rng.random()
-            time.sleep(50e-6)
             if op < 0.4:
                 tok = _rand_tokens(rng, stems)
                 slots = list(range(next_slot, next_slot + len(tok)))
