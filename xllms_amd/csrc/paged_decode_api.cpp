@@ -189,11 +189,13 @@ int partition_occupancy(int kv_dtype, int head_size, int head_tile, bool mfma, s
     }
 }
 
-// Workgroups per CU of the MFMA partition kernel's plan: two (8 wavefronts
-// per CU, 2 per SIMD).  Measured on MI355X against the three that fit: 4-10%
-// less time on configs 2, 3 and 4 (fewer concurrent page streams per HBM
-// channel, and an even finish across wavefronts).
-constexpr int kMfmaGroupsPerCu = 2;
+// Wavefronts per CU of the MFMA partition kernel's plan: eight (2 per SIMD).
+// Measured on MI355X against the twelve that fit: 4-10% less time on configs
+// 2, 3 and 4 (fewer concurrent page streams per HBM channel, and an even
+// finish across wavefronts).
+constexpr int kMfmaWavesPerCu = 8;
+
+int waves_per_group(bool mfma) { return mfma ? xhip::kMfmaWavesPerGroup : xhip::kWavesPerGroup; }
 
 // Wavefronts of the automatic plan: one resident round of the partition
 // kernel on every CU, but no more than the batch could keep busy with
@@ -201,14 +203,16 @@ constexpr int kMfmaGroupsPerCu = 2;
 long long auto_waves(int kv_dtype, int head_size, int head_tile, bool mfma, int nseq,
                      long long ub_tiles, int cus) {
     const size_t lds = (size_t)(nseq + 1) * sizeof(int);
-    int occ = partition_occupancy(kv_dtype, head_size, head_tile, mfma, lds);
+    const int occ = partition_occupancy(kv_dtype, head_size, head_tile, mfma, lds);
     if (occ <= 0) return 0;
-    if (mfma && occ > kMfmaGroupsPerCu) occ = kMfmaGroupsPerCu;
-    long long w = (long long)cus * occ * xhip::kWavesPerGroup;
+    const int wpg = waves_per_group(mfma);
+    int per_cu = occ * wpg;
+    if (mfma && per_cu > kMfmaWavesPerCu) per_cu = kMfmaWavesPerCu;
+    long long w = (long long)cus * per_cu;
     const long long need = (ub_tiles + kMinTilesPerWave - 1) / kMinTilesPerWave;
     if (need < w) w = need;
-    w = (w + xhip::kWavesPerGroup - 1) / xhip::kWavesPerGroup * xhip::kWavesPerGroup;
-    return w > 0 ? w : xhip::kWavesPerGroup;
+    w = (w + wpg - 1) / wpg * wpg;
+    return w > 0 ? w : wpg;
 }
 
 constexpr long long kMaxWaves = 1LL << 22;
@@ -325,8 +329,8 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         } else {
             min_tpw = partition_tokens / tile;
             waves = (ub_tiles + min_tpw - 1) / min_tpw;
-            waves = (waves + xhip::kWavesPerGroup - 1) / xhip::kWavesPerGroup *
-                    xhip::kWavesPerGroup;
+            const int wpg = waves_per_group(mfma);
+            waves = (waves + wpg - 1) / wpg * wpg;
             if (waves > kMaxWaves)
                 return set_status(NXT_ATTN_E_UNSUPPORTED,
                                   "partition_tokens %d gives %lld wavefronts; raise it",

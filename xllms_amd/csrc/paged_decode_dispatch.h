@@ -64,7 +64,9 @@ static hipError_t launch_for_head_size(const DecodeParams &p, int head_tile, boo
     if (mfma) {
         if constexpr (has_mfma<KV, D>()) {
             if (head_tile != kMfmaHeads) return hipErrorInvalidValue;
-            paged_decode_partition_mfma_kernel<KV, D><<<grid, block, lds, st>>>(p);
+            paged_decode_partition_mfma_kernel<KV, D>
+                <<<(unsigned)(p.num_waves / kMfmaWavesPerGroup), 64 * kMfmaWavesPerGroup, lds, st>>>(
+                    p, p.seq_lens, p.block_tables);
             return launch_merge<KV, D, kMfmaHeads, MfmaGeometry<D>::kTile>(p, st, after_partition);
         }
         return hipErrorInvalidValue;
@@ -103,8 +105,9 @@ static int occupancy_for_dtype(int head_size, int head_tile, bool mfma, size_t l
     const void *fn = partition_fn_dtype<KV>(head_size, head_tile, mfma);
     if (!fn) return 0;
     int blocks = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 64 * kWavesPerGroup,
-                                                     lds_bytes) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &blocks, fn, 64 * (mfma ? kMfmaWavesPerGroup : kWavesPerGroup), lds_bytes) !=
+        hipSuccess)
         return 0;
     return blocks;
 }

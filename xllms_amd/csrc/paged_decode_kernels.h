@@ -375,10 +375,10 @@ __device__ __forceinline__ int tiles_per_wave(int total, int num_waves, int min_
 // Exclusive prefix over sequences of the tiles of all their segments, into
 // LDS (num_seqs + 1 entries), by the whole workgroup.  Workgroup 0 also
 // stores it for the merge kernel.
-template <int TT>
+template <int TT, int WPG>
 __device__ __forceinline__ void batch_prefix(const DecodeParams &p, int *pre) {
-    __shared__ int part[64 * kWavesPerGroup];
-    const int nthr = 64 * kWavesPerGroup;
+    __shared__ int part[64 * WPG];
+    const int nthr = 64 * WPG;
     const int tid = threadIdx.x;
     const int B = p.num_seqs;
     const int per = (B + nthr - 1) / nthr;
@@ -422,12 +422,13 @@ __device__ __forceinline__ void batch_prefix(const DecodeParams &p, int *pre) {
 // fn(s, L, kvh, ht, t_begin, t_end, whole, slot) where [t_begin, t_end) are
 // the piece's tokens, `whole` says the piece is the entire segment (write the
 // output) and `slot` is the partial slot otherwise.  `pre` is the LDS tile
-// prefix (num_seqs + 1 ints); every thread of the workgroup must call this.
-template <int TT, typename Fn>
+// prefix (num_seqs + 1 ints); every thread of the workgroup (WPG wavefronts)
+// must call this.
+template <int TT, int WPG, typename Fn>
 __device__ __forceinline__ void stream_k_walk(const DecodeParams &p, int *pre, Fn &&fn) {
-    batch_prefix<TT>(p, pre);
+    batch_prefix<TT, WPG>(p, pre);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int w = blockIdx.x * kWavesPerGroup + wave;
+    const int w = blockIdx.x * WPG + wave;
     const int B = p.num_seqs;
     const int total = pre[B];
     const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);
@@ -484,7 +485,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
     const int row = lane / RL;
     const bool col_ok = (NCH == RL) || (col < NCH);
 
-    stream_k_walk<TT>(p, pre, [&](int s, int L, int kvh, int ht, int t_begin, int t_end,
+    stream_k_walk<TT, kWavesPerGroup>(p, pre, [&](int s, int L, int kvh, int ht, int t_begin, int t_end,
                                   bool whole, size_t slot) {
         (void)L;
         const int g0 = ht * GT;

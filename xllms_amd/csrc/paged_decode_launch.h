@@ -10,14 +10,16 @@ namespace xhip {
 
 // Resident workgroups per CU of the partition kernel for this
 // (head_size, head_tile, tile path) with `lds_bytes` of dynamic LDS; 0 when
-// there is no such instantiation.  mfma selects the MFMA tile path (16-bit
-// types, head_size % 32 == 0, head_tile 16).
+// there is no such instantiation.  A workgroup is kWavesPerGroup wavefronts
+// on the VALU path and kMfmaWavesPerGroup on the MFMA path.  mfma selects the
+// MFMA tile path (16-bit types, head_size % 32 == 0, head_tile 16).
 int partition_occupancy_f16(int head_size, int head_tile, bool mfma, size_t lds_bytes);
 int partition_occupancy_bf16(int head_size, int head_tile, bool mfma, size_t lds_bytes);
 int partition_occupancy_f32(int head_size, int head_tile, bool mfma, size_t lds_bytes);
 
-// Launches the partition kernel on num_waves/kWavesPerGroup workgroups, then
-// the merge kernel over every (sequence, kv head, head tile).  A non-null
+// Launches the partition kernel on num_waves / (wavefronts per workgroup)
+// workgroups, then the merge kernel over every (sequence, kv head, head
+// tile).  A non-null
 // `after_partition` event is recorded on the stream between the two.
 // Returns hipErrorInvalidValue for a head_size / head_tile with no
 // instantiation, else the launch status.

@@ -221,40 +221,72 @@ __device__ __forceinline__ void mfma_tile(const DecodeParams &p, const u32x4 *q,
     }
 }
 
-// Stream tokens [t_begin, t_end) of one segment through the MFMA tiles.
-template <int KV, int D>
-__device__ __forceinline__ void mfma_segment(const DecodeParams &p, const int *bt, const char *kb,
-                                             const char *vb, int t_begin, int t_end, int lane,
-                                             bool cached, char *lds, const u32x4 *q,
-                                             MfmaState<D> &st) {
-    const int ntiles = (t_end - t_begin + 15) >> 4;
-    // Block ids of up to 64 tiles at a time, one per lane (vector loads, so
-    // the tile loop issues no scalar memory traffic).
-    int ids = 0;
-    MfmaTileRegs<D> ra, rb;
-    int blk_a = 0;
-    for (int i = 0; i < ntiles; i++) {
-        if ((i & 63) == 0) {
-            const int ti = t_begin + 16 * (i + lane);
-            ids = bt[(ti < t_end ? ti : t_end - 1) >> p.bs_shift];
-            if (i == 0) {
-                blk_a = __builtin_amdgcn_readlane(ids, 0);
-                mfma_load_tile<D>(p, kb, vb, t_begin, t_end, blk_a, lane, cached, ra);
-            }
-        }
-        const int t0 = t_begin + 16 * i;
-        // Prefetch tile i+1 (all rows out of range past the segment end).
-        const int nl = (i + 1) & 63;
-        int blk_b = (i + 1 < ntiles && nl != 0) ? __builtin_amdgcn_readlane(ids, nl) : -1;
-        if (i + 1 < ntiles && nl == 0) {
-            const int ti = t0 + 16;
-            blk_b = bt[ti >> p.bs_shift];
-        }
-        mfma_load_tile<D>(p, kb, vb, t0 + 16, t_end, blk_b, lane, cached, rb);
-        mfma_tile<KV, D>(p, q, t0, t_end, blk_a >= 0, lane, lds, ra, st);
-        ra = rb;
-        blk_a = blk_b;
+// One piece of a wavefront's stream-K range: tokens [t_begin, t_end) of the
+// segment (sequence s, kv head kvh, head tile ht).  `whole`: the piece is the
+// entire segment (the output is written directly); else its partial goes to
+// `slot`.  All fields are wavefront-uniform.
+struct MfmaPiece {
+    int s, kvh, ht, t_begin, t_end, whole, slot;
+};
+
+// Cursor over the pieces of one wavefront's range [g, g_end) of the batch's
+// tiles; s is the sequence holding tile g.
+struct RangeCursor {
+    int g, g_end, s, first, w;
+};
+
+// The next piece of the range (false at its end).  Same decomposition as
+// stream_k_walk, one piece at a time, so the kernel can look one piece ahead.
+template <int TT>
+__device__ __forceinline__ bool next_piece(const DecodeParams &p, const int *__restrict__ lens,
+                                           const int *pre, RangeCursor &c, MfmaPiece &pc) {
+    if (c.g >= c.g_end) return false;
+    const int segs = p.num_kv_heads * p.head_tiles;
+    const int L = min(max(lens[c.s], 0), p.max_ctx);
+    const int Ts = (L + TT - 1) / TT;
+    const int local = c.g - __builtin_amdgcn_readfirstlane(pre[c.s]);
+    const int seg = local / Ts;
+    const int t0 = local - seg * Ts;
+    const int n = min(Ts - t0, c.g_end - c.g);
+    pc.s = c.s;
+    pc.kvh = seg / p.head_tiles;
+    pc.ht = seg - pc.kvh * p.head_tiles;
+    pc.t_begin = t0 * TT;
+    pc.t_end = min(L, (t0 + n) * TT);
+    pc.whole = t0 == 0 && n == Ts;
+    pc.slot = c.w * 2 + (c.first ? 0 : 1);
+    c.g += n;
+    c.first = 0;
+    if (c.g - __builtin_amdgcn_readfirstlane(pre[c.s]) >= Ts * segs) {  // sequence done
+        int s = c.s + 1;
+        while (s < p.num_seqs - 1 && pre[s + 1] == pre[s]) s++;
+        c.s = __builtin_amdgcn_readfirstlane(s);
     }
+    return true;
+}
+
+// Q rows of the piece's (up to) 16 query heads in the MFMA B layout (lane:
+// head j, dims 32c+8g..+7); heads past the group read as zero.
+template <int D>
+__device__ __forceinline__ void mfma_load_q(const DecodeParams &p, const MfmaPiece &pc, int lane,
+                                            u32x4 (&q)[MfmaGeometry<D>::kQkSteps]) {
+    const int j = lane & 15, g = lane >> 4;
+    const int g0 = pc.ht * kMfmaHeads;
+    const int nh = min(kMfmaHeads, p.group - g0);
+    const size_t qrow0 = ((size_t)pc.s * p.num_heads + (size_t)pc.kvh * p.group + g0) * D;
+#pragma unroll
+    for (int c = 0; c < MfmaGeometry<D>::kQkSteps; c++)
+        q[c] = (j < nh) ? load16((const char *)p.q + (qrow0 + (size_t)j * D + 32 * c + 8 * g) * 2)
+                        : u32x4{0, 0, 0, 0};
+}
+
+// Block ids of the piece's tiles first .. first+63, lane i holding tile
+// first+i (clamped to the piece's last tile).
+__device__ __forceinline__ int mfma_load_ids(const DecodeParams &p, const int *__restrict__ tables,
+                                             const MfmaPiece &pc, int first, int lane) {
+    const int *bt = tables + (size_t)pc.s * p.max_blocks;
+    const int ti = pc.t_begin + 16 * (first + lane);
+    return bt[(ti < pc.t_end ? ti : pc.t_end - 1) >> p.bs_shift];
 }
 
 }  // namespace xhip
@@ -262,72 +294,159 @@ __device__ __forceinline__ void mfma_segment(const DecodeParams &p, const int *b
 namespace xhip {
 
 // Partition kernel, MFMA tile path (head tile of 16 query heads).
+//
+// A wavefront walks the pieces of its stream-K range (usually one or two
+// segments) as one pipeline: while the last tile of a piece is computed, the
+// next piece's first K/V tile is already in flight, and its Q rows and block
+// ids were requested when the current piece began.  Without this look-ahead a
+// wavefront whose range crosses a segment boundary waited on a chain of
+// dependent loads (block ids, then the first tile) at the crossing, and those
+// wavefronts finished the launch last (measured on MI355X: 3 us later on
+// average at config 2).  Head sizes above 128 load the next piece's Q when it
+// begins instead, which keeps their register budget.
 template <int KV, int D>
-__global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_mfma_kernel(
-    const DecodeParams p) {
+__global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partition_mfma_kernel(
+    const DecodeParams p, const int *__restrict__ lens, const int *__restrict__ tables) {
+    // lens / tables are p.seq_lens / p.block_tables again: as restrict
+    // kernel arguments their wavefront-uniform reads become scalar loads,
+    // which do not wait behind the K/V loads in flight.
     using G = MfmaGeometry<D>;
     constexpr int GT = kMfmaHeads;
+    constexpr bool kPrefetchQ = D <= 128;
     extern __shared__ int pre[];  // num_seqs + 1 tile prefixes
-    __shared__ __attribute__((aligned(16))) char vtile[kWavesPerGroup][G::kLdsTile];
+    __shared__ __attribute__((aligned(16))) char vtile[kMfmaWavesPerGroup][G::kLdsTile];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     char *lds = vtile[wave];
     const int j = lane & 15, gq = lane >> 4;
 
-    stream_k_walk<16>(p, pre, [&](int s, int L, int kvh, int ht, int t_begin, int t_end,
-                                  bool whole, size_t slot) {
-        (void)L;
-        const int g0 = ht * GT;
-        const int nh = min(GT, p.group - g0);
-        const size_t qrow0 = ((size_t)s * p.num_heads + (size_t)kvh * p.group + g0) * D;
-        u32x4 q[G::kQkSteps];
-#pragma unroll
-        for (int c = 0; c < G::kQkSteps; c++)
-            q[c] = (j < nh) ? load16((const char *)p.q + (qrow0 + (size_t)j * D + 32 * c + 8 * gq) * 2)
-                            : u32x4{0, 0, 0, 0};
+    batch_prefix<16, kMfmaWavesPerGroup>(p, pre);
+    const int w = blockIdx.x * kMfmaWavesPerGroup + wave;
+    const int B = p.num_seqs;
+    const int total = pre[B];
+    const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);
+    const long long g_lo = (long long)w * tpw;
+    if (g_lo >= total) return;
+    RangeCursor cur;
+    cur.g = (int)g_lo;
+    cur.g_end = min(total, cur.g + tpw);
+    cur.first = 1;
+    cur.w = w;
+    {
+        // the sequence holding tile g: the last s with pre[s] <= g (empty
+        // sequences share their successor's prefix, so this lands on one
+        // with tiles)
+        int lo = 0, hi = B - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (pre[mid] <= cur.g) lo = mid; else hi = mid - 1;
+        }
+        cur.s = __builtin_amdgcn_readfirstlane(lo);
+    }
+
+    MfmaPiece pc;
+    next_piece<16>(p, lens, pre, cur, pc);
+    u32x4 q[G::kQkSteps];
+    mfma_load_q<D>(p, pc, lane, q);
+    int ids = mfma_load_ids(p, tables, pc, 0, lane);
+    MfmaTileRegs<D> ra, rb;
+    int blk_a = __builtin_amdgcn_readlane(ids, 0);
+    {
+        const char *kb = (const char *)p.k + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
+        const char *vb = (const char *)p.v + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
+        mfma_load_tile<D>(p, kb, vb, pc.t_begin, pc.t_end, blk_a, lane, pc.s < p.cached_seqs, ra);
+    }
+
+    while (true) {
+        MfmaPiece pn = pc;
+        const bool has_next = next_piece<16>(p, lens, pre, cur, pn);
+        u32x4 qn[kPrefetchQ ? G::kQkSteps : 1];
+        int ids_n = 0;
+        if (has_next) {
+            if constexpr (kPrefetchQ) mfma_load_q<D>(p, pn, lane, qn);
+            ids_n = mfma_load_ids(p, tables, pn, 0, lane);
+        }
+        const char *kb = (const char *)p.k + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
+        const char *vb = (const char *)p.v + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
+        const char *kb_n = (const char *)p.k + (size_t)pn.kvh * (size_t)p.kv_head_stride * 2;
+        const char *vb_n = (const char *)p.v + (size_t)pn.kvh * (size_t)p.kv_head_stride * 2;
+        const bool cached = pc.s < p.cached_seqs;
+        const bool cached_n = has_next && pn.s < p.cached_seqs;
+        const int *bt = tables + (size_t)pc.s * p.max_blocks;
+
         MfmaState<D> st;
 #pragma unroll
         for (int n = 0; n < G::kDimBlocks; n++) st.o[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         st.m = -INFINITY;
         st.l = 0.0f;
-        const int *bt = p.block_tables + (size_t)s * p.max_blocks;
-        const char *kb = (const char *)p.k + (size_t)kvh * (size_t)p.kv_head_stride * 2;
-        const char *vb = (const char *)p.v + (size_t)kvh * (size_t)p.kv_head_stride * 2;
-        mfma_segment<KV, D>(p, bt, kb, vb, t_begin, t_end, lane, s < p.cached_seqs, lds, q, st);
+        const int ntiles = (pc.t_end - pc.t_begin + 15) >> 4;
+        for (int i = 0; i < ntiles; i++) {
+            if (i > 0 && (i & 63) == 0) ids = mfma_load_ids(p, tables, pc, i, lane);
+            const int t0 = pc.t_begin + 16 * i;
+            // The next tile: this piece's, else the next piece's first (all
+            // rows out of range when there is none).
+            const int nl = (i + 1) & 63;
+            const bool in_piece = i + 1 < ntiles;
+            int blk_b;
+            if (in_piece)
+                blk_b = nl != 0 ? __builtin_amdgcn_readlane(ids, nl) : bt[(t0 + 16) >> p.bs_shift];
+            else
+                blk_b = has_next ? __builtin_amdgcn_readlane(ids_n, 0) : -1;
+            mfma_load_tile<D>(p, in_piece ? kb : kb_n, in_piece ? vb : vb_n,
+                              in_piece ? t0 + 16 : pn.t_begin,
+                              in_piece ? pc.t_end : (has_next ? pn.t_end : 0), blk_b, lane,
+                              in_piece ? cached : cached_n, rb);
+            mfma_tile<KV, D>(p, q, t0, pc.t_end, blk_a >= 0, lane, lds, ra, st);
+            ra = rb;
+            blk_a = blk_b;
+        }
 
         float l = st.l;
         l += __shfl_xor(l, 16);
         l += __shfl_xor(l, 32);
-        if (j >= nh) return;
-        if (whole && p.out_f32) {
-            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-            float *dst = p.out_f32 + qrow0 + (size_t)j * D + 4 * gq;
+        const int g0 = pc.ht * GT;
+        const int nh = min(GT, p.group - g0);
+        const size_t qrow0 = ((size_t)pc.s * p.num_heads + (size_t)pc.kvh * p.group + g0) * D;
+        if (j < nh) {
+            if (pc.whole && p.out_f32) {
+                const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+                float *dst = p.out_f32 + qrow0 + (size_t)j * D + 4 * gq;
 #pragma unroll
-            for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st.o[n] * inv;
-            if (gq == 0) p.out_lse[qrow0 / D + j] = l > 0.0f ? st.m + log2f(l) : -INFINITY;
-        } else if (whole) {
-            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-            char *dst = (char *)p.out + (qrow0 + (size_t)j * D + 4 * gq) * 2;
+                for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st.o[n] * inv;
+                if (gq == 0) p.out_lse[qrow0 / D + j] = l > 0.0f ? st.m + log2f(l) : -INFINITY;
+            } else if (pc.whole) {
+                const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+                char *dst = (char *)p.out + (qrow0 + (size_t)j * D + 4 * gq) * 2;
 #pragma unroll
-            for (int n = 0; n < G::kDimBlocks; n++) {
-                float f0, f1, f2, f3;
-                const uint32_t b0 = round16<KV>(st.o[n][0] * inv, f0);
-                const uint32_t b1 = round16<KV>(st.o[n][1] * inv, f1);
-                const uint32_t b2 = round16<KV>(st.o[n][2] * inv, f2);
-                const uint32_t b3 = round16<KV>(st.o[n][3] * inv, f3);
-                *(u32x2 *)(dst + 32 * n) = u32x2{b0 | (b1 << 16), b2 | (b3 << 16)};
-            }
-        } else {
-            float *dst = p.ws_o + (slot * GT + j) * D + 4 * gq;
+                for (int n = 0; n < G::kDimBlocks; n++) {
+                    float f0, f1, f2, f3;
+                    const uint32_t b0 = round16<KV>(st.o[n][0] * inv, f0);
+                    const uint32_t b1 = round16<KV>(st.o[n][1] * inv, f1);
+                    const uint32_t b2 = round16<KV>(st.o[n][2] * inv, f2);
+                    const uint32_t b3 = round16<KV>(st.o[n][3] * inv, f3);
+                    *(u32x2 *)(dst + 32 * n) = u32x2{b0 | (b1 << 16), b2 | (b3 << 16)};
+                }
+            } else {
+                float *dst = p.ws_o + ((size_t)pc.slot * GT + j) * D + 4 * gq;
 #pragma unroll
-            for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st.o[n];
-            if (gq == 0) {
-                p.ws_ml[(slot * GT + j) * 2] = st.m;
-                p.ws_ml[(slot * GT + j) * 2 + 1] = l;
+                for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st.o[n];
+                if (gq == 0) {
+                    p.ws_ml[((size_t)pc.slot * GT + j) * 2] = st.m;
+                    p.ws_ml[((size_t)pc.slot * GT + j) * 2 + 1] = l;
+                }
             }
         }
-    });
+        if (!has_next) break;
+        pc = pn;
+        ids = ids_n;
+        if constexpr (kPrefetchQ) {
+#pragma unroll
+            for (int c = 0; c < G::kQkSteps; c++) q[c] = qn[c];
+        } else {
+            mfma_load_q<D>(p, pc, lane, q);
+        }
+    }
 }
 
 }  // namespace xhip

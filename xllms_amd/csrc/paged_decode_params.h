@@ -22,7 +22,8 @@ enum KvType : int { KV_F16 = 1, KV_BF16 = 2, KV_F32 = 3 };
 // wavefront's slot 0 (the segment holds the wavefront's first tile) or
 // slot 1 (it holds the wavefront's last tile but not its first), and
 // paged_decode_merge_kernel combines them.
-constexpr int kWavesPerGroup = 4;
+constexpr int kWavesPerGroup = 4;    // VALU tile path: wavefronts per workgroup
+constexpr int kMfmaWavesPerGroup = 4;  // MFMA tile path
 constexpr int kMaxHeadTile = 8;      // query heads per wavefront, VALU tile path
 constexpr int kMfmaHeads = 16;       // query heads per wavefront, MFMA tile path
 constexpr int kLoadsPerTile = 4;     // 16-byte K (and V) loads per lane per tile
