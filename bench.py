@@ -320,7 +320,8 @@ def bench_activation(args) -> int:
                    "intermediate_size": d, "entry_point": entry},
         "algorithmic_bytes": alg,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic(f"llama3-8b-mlp-{args.activation}-fp16"),
                      "kernel": "activation_vec_kernel", "kernel_avg_us": round(avg_ms * 1e3, 2)},
         "decode_call_us": round(dec_us, 2), "decode_tokens": dn,
         "cpu_baseline": cpu, "check": check}), flush=True)

@@ -297,13 +297,14 @@ namespace xhip {
 //
 // A wavefront walks the pieces of its stream-K range (usually one or two
 // segments) as one pipeline: while the last tile of a piece is computed, the
-// next piece's first K/V tile is already in flight, and its Q rows and block
-// ids were requested when the current piece began.  Without this look-ahead a
+// next piece's first K/V tile is already in flight, and its block ids were
+// requested when the current piece began.  Without this look-ahead a
 // wavefront whose range crosses a segment boundary waited on a chain of
 // dependent loads (block ids, then the first tile) at the crossing, and those
 // wavefronts finished the launch last (measured on MI355X: 3 us later on
-// average at config 2).  Head sizes above 128 load the next piece's Q when it
-// begins instead, which keeps their register budget.
+// average at config 2).  Q is loaded when its piece begins: requesting the
+// next piece's Q a piece early as well gained ~1% at configs 2-4 but cost 5%
+// (cascade) to 10% (plain decode) at config 5 (measured, same box).
 template <int KV, int D>
 __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partition_mfma_kernel(
     const DecodeParams p, const int *__restrict__ lens, const int *__restrict__ tables) {
@@ -312,7 +313,6 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
     // which do not wait behind the K/V loads in flight.
     using G = MfmaGeometry<D>;
     constexpr int GT = kMfmaHeads;
-    constexpr bool kPrefetchQ = D <= 128;
     extern __shared__ int pre[];  // num_seqs + 1 tile prefixes
     __shared__ __attribute__((aligned(16))) char vtile[kMfmaWavesPerGroup][G::kLdsTile];
 
@@ -361,12 +361,10 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
     while (true) {
         MfmaPiece pn = pc;
         const bool has_next = next_piece<16>(p, lens, pre, cur, pn);
-        u32x4 qn[kPrefetchQ ? G::kQkSteps : 1];
-        int ids_n = 0;
-        if (has_next) {
-            if constexpr (kPrefetchQ) mfma_load_q<D>(p, pn, lane, qn);
-            ids_n = mfma_load_ids(p, tables, pn, 0, lane);
-        }
+        // Issued whether or not there is a next piece (pn is then the
+        // current one again), so every path through the loop below has the
+        // same loads in flight and the compiler's wait counts stay exact.
+        const int ids_n = mfma_load_ids(p, tables, pn, 0, lane);
         const char *kb = (const char *)p.k + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
         const char *vb = (const char *)p.v + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
         const char *kb_n = (const char *)p.k + (size_t)pn.kvh * (size_t)p.kv_head_stride * 2;
@@ -440,12 +438,7 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
         if (!has_next) break;
         pc = pn;
         ids = ids_n;
-        if constexpr (kPrefetchQ) {
-#pragma unroll
-            for (int c = 0; c < G::kQkSteps; c++) q[c] = qn[c];
-        } else {
-            mfma_load_q<D>(p, pc, lane, q);
-        }
+        mfma_load_q<D>(p, pc, lane, q);
     }
 }
 
