@@ -123,6 +123,23 @@ def test_merge_per_segment_paths(cuda, shape):
                      f"H={H} KVH={KVH} d={D} part={part}")
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+def test_auto_split_many_short_segments(cuda, dtype):
+    """Automatic plans charge every segment a start-up cost on top of its
+    tiles: runs of one-tile sequences between long ones put wavefront range
+    boundaries inside segments' start-up units, at their first tile and in
+    their middle, and the merge must find the same pieces."""
+    rng = np.random.default_rng(7)
+    lens = rng.integers(1, 24, size=160)
+    lens[::9] = rng.integers(1200, 2600, size=lens[::9].size)
+    lens[3] = 0
+    lens[4] = 16
+    wl = W.small_case(num_seqs=lens.size, H=32, KVH=8, D=128, kv_dtype=DT[dtype], seed=77,
+                      lens=lens.tolist())
+    print(f"case {dtype} seqs={lens.size} tokens={int(lens.sum())}", flush=True)
+    assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"auto split {dtype}")
+
+
 def test_back_to_back_launches_reuse_counters(cuda):
     """The in-kernel merge counters are left at zero by every launch: many
     launches of different shapes on one stream (one shared workspace), each

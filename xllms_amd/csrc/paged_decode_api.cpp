@@ -218,6 +218,14 @@ long long auto_waves(int kv_dtype, int head_size, int head_tile, bool mfma, int 
 constexpr long long kMaxWaves = 1LL << 22;
 constexpr long long kMaxLaunchTiles = 1LL << 30;  // bounds the partial workspace of explicit plans
 
+// Split units an automatic plan charges each segment on top of its tiles
+// (paged_decode_params.h): on MI355X a segment's first tile computes ~1.5
+// tiles' time after the piece begins (block ids, then K, then the softmax
+// chain), and a batch of fresh one-tile sequences otherwise piles dozens of
+// such starts on one wavefront.  Explicit partition_tokens plans charge 0,
+// so each wavefront's range is exactly partition_tokens of K/V.
+constexpr int kSegmentCost = 2;
+
 const char *dtype_name(int kv_dtype) {
     switch (kv_dtype) {
     case NXT_KV_FP16: return "fp16";
@@ -302,22 +310,23 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
     hipStream_t stream = (hipStream_t)stream_handle;
     const int cus = cu_count(device);
     const int segs = num_kv_heads * tiling.head_tiles;
-    const long long tiles_per_seg = (max_ctx + tile - 1) / tile;
+    const int seg_cost = partition_tokens == 0 ? kSegmentCost : 0;
+    const long long units_per_seg = (max_ctx + tile - 1) / tile + seg_cost;
 
     // Batches go in consecutive launches of at most kMaxSeqsPerLaunch
     // sequences (the per-workgroup prefix scan of the partition kernel lives
-    // in LDS) and at most kMaxLaunchTiles tiles by the context bound (tile
-    // indices are 32-bit on the device).
-    const long long seq_tiles = (long long)segs * tiles_per_seg;
-    if (seq_tiles >= kMaxLaunchTiles)
+    // in LDS) and at most kMaxLaunchTiles split units by the context bound
+    // (unit indices are 32-bit on the device).
+    const long long seq_units = (long long)segs * units_per_seg;
+    if (seq_units >= kMaxLaunchTiles)
         return set_status(NXT_ATTN_E_UNSUPPORTED,
                           "one sequence bounds %lld tiles (kv heads x context); limit %lld",
-                          seq_tiles, kMaxLaunchTiles);
-    const long long fit = kMaxLaunchTiles / seq_tiles;
+                          seq_units, kMaxLaunchTiles);
+    const long long fit = kMaxLaunchTiles / seq_units;
     const int per_launch = fit < xhip::kMaxSeqsPerLaunch ? (int)fit : xhip::kMaxSeqsPerLaunch;
     for (int s0 = 0; s0 < num_seqs; s0 += per_launch) {
         const int nseq = num_seqs - s0 < per_launch ? num_seqs - s0 : per_launch;
-        const long long ub_tiles = (long long)nseq * seq_tiles;
+        const long long ub_tiles = (long long)nseq * seq_units;
         long long waves;
         int min_tpw;
         if (partition_tokens == 0) {
@@ -376,6 +385,7 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         p.max_ctx = (int)max_ctx;
         p.num_waves = (int)waves;
         p.min_tiles_per_wave = min_tpw;
+        p.seg_cost = seg_cost;
         p.scale_log2 = scale * 1.4426950408889634f;
         // One merge workgroup per segment once the segments alone fill two
         // workgroups per CU; fewer, longer segments (few sequences, long

@@ -372,8 +372,14 @@ __device__ __forceinline__ int tiles_per_wave(int total, int num_waves, int min_
     return t > min_tpw ? t : min_tpw;
 }
 
-// Exclusive prefix over sequences of the tiles of all their segments, into
-// LDS (num_seqs + 1 entries), by the whole workgroup.  Workgroup 0 also
+// Split units of a segment of Ts tiles (paged_decode_params.h): its tiles
+// plus the start-up cost; an empty segment costs nothing.
+__device__ __forceinline__ int segment_units(const DecodeParams &p, int Ts) {
+    return Ts > 0 ? Ts + p.seg_cost : 0;
+}
+
+// Exclusive prefix over sequences of the split units of all their segments,
+// into LDS (num_seqs + 1 entries), by the whole workgroup.  Workgroup 0 also
 // stores it for the merge kernel.
 template <int TT, int WPG>
 __device__ __forceinline__ void batch_prefix(const DecodeParams &p, int *pre) {
@@ -388,8 +394,8 @@ __device__ __forceinline__ void batch_prefix(const DecodeParams &p, int *pre) {
     for (int i = 0; i < per; i++) {
         const int s = s0 + i;
         if (s < B) {
-            const int t = (seq_len_of(p, s) + TT - 1) / TT * segs;
-            pre[s] = t;  // tiles of sequence s, scanned below
+            const int t = segment_units(p, (seq_len_of(p, s) + TT - 1) / TT) * segs;
+            pre[s] = t;  // units of sequence s, scanned below
             local += t;
         }
     }
@@ -421,9 +427,10 @@ __device__ __forceinline__ void batch_prefix(const DecodeParams &p, int *pre) {
 // Walk this wavefront's stream-K range: for every segment piece in it call
 // fn(s, L, kvh, ht, t_begin, t_end, whole, slot) where [t_begin, t_end) are
 // the piece's tokens, `whole` says the piece is the entire segment (write the
-// output) and `slot` is the partial slot otherwise.  `pre` is the LDS tile
+// output) and `slot` is the partial slot otherwise.  `pre` is the LDS unit
 // prefix (num_seqs + 1 ints); every thread of the workgroup (WPG wavefronts)
-// must call this.
+// must call this.  A range that ends inside a segment's start-up units holds
+// none of its tiles and makes no piece of it.
 template <int TT, int WPG, typename Fn>
 __device__ __forceinline__ void stream_k_walk(const DecodeParams &p, int *pre, Fn &&fn) {
     batch_prefix<TT, WPG>(p, pre);
@@ -437,7 +444,7 @@ __device__ __forceinline__ void stream_k_walk(const DecodeParams &p, int *pre, F
     int g = (int)g_lo;
     const int g_end = min(total, g + tpw);
 
-    // Sequence holding tile g: the last s with pre[s] <= g (empty sequences
+    // Sequence holding unit g: the last s with pre[s] <= g (empty sequences
     // share their successor's prefix, so this lands on one with tiles).
     int lo = 0, hi = B - 1;
     while (lo < hi) {
@@ -450,17 +457,21 @@ __device__ __forceinline__ void stream_k_walk(const DecodeParams &p, int *pre, F
     while (g < g_end) {
         const int L = seq_len_of(p, s);
         const int Ts = (L + TT - 1) / TT;  // tiles per segment of sequence s
+        const int Cs = segment_units(p, Ts);
         const int local = g - pre[s];
-        const int seg = local / Ts;
-        const int t0 = local - seg * Ts;
-        const int n = min(Ts - t0, g_end - g);
-        const int kvh = seg / p.head_tiles;
-        const int ht = seg - kvh * p.head_tiles;
-        fn(s, L, kvh, ht, t0 * TT, min(L, (t0 + n) * TT), t0 == 0 && n == Ts,
-           (size_t)w * 2 + (first ? 0 : 1));
-        g += n;
-        first = false;
-        if (g - pre[s] >= Ts * segs) {  // sequence done: next one with tiles
+        const int seg = local / Cs;
+        const int u0 = local - seg * Cs;
+        const int u1 = min(Cs, u0 + (g_end - g));
+        const int t0 = max(u0 - p.seg_cost, 0), t1 = max(u1 - p.seg_cost, 0);
+        if (t1 > t0) {
+            const int kvh = seg / p.head_tiles;
+            const int ht = seg - kvh * p.head_tiles;
+            fn(s, L, kvh, ht, t0 * TT, min(L, t1 * TT), t0 == 0 && t1 == Ts,
+               (size_t)w * 2 + (first ? 0 : 1));
+            first = false;
+        }
+        g += u1 - u0;
+        if (g - pre[s] >= Cs * segs) {  // sequence done: next one with tiles
             s++;
             while (s < B - 1 && pre[s + 1] == pre[s]) s++;
         }
@@ -624,12 +635,15 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
     const int total = p.ws_prefix[p.num_seqs];
     const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);
     const int Ts = (L + TT - 1) / TT;
-    const int seg_start = p.ws_prefix[s] + seg * Ts;
-    const int w_first = seg_start / tpw;
-    const int w_last = (seg_start + Ts - 1) / tpw;
+    const int seg_start = p.ws_prefix[s] + seg * segment_units(p, Ts);  // in split units
+    const int first_tile = seg_start + p.seg_cost;
+    const int w_first = first_tile / tpw;
+    const int w_last = (first_tile + Ts - 1) / tpw;
     if (w_first == w_last) return;
     const int np = w_last - w_first + 1;
-    const int slot0 = (seg_start == w_first * tpw) ? 0 : 1;
+    // the segment is w_first's first piece when w_first's range begins in the
+    // segment's start-up units or at its first tile
+    const int slot0 = (w_first * tpw >= seg_start) ? 0 : 1;
     // partial j of the segment lives in slot (w_first + j)*2 + (j == 0 ? slot0 : 0)
     const size_t sbase = (size_t)w_first * 2;
 
@@ -728,12 +742,15 @@ __global__ __launch_bounds__(kMergeSegThreads) void paged_decode_merge_segment_k
     const int total = p.ws_prefix[p.num_seqs];
     const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);
     const int Ts = (L + TT - 1) / TT;
-    const int seg_start = p.ws_prefix[s] + seg * Ts;
-    const int w_first = seg_start / tpw;
-    const int w_last = (seg_start + Ts - 1) / tpw;
+    const int seg_start = p.ws_prefix[s] + seg * segment_units(p, Ts);  // in split units
+    const int first_tile = seg_start + p.seg_cost;
+    const int w_first = first_tile / tpw;
+    const int w_last = (first_tile + Ts - 1) / tpw;
     if (w_first == w_last) return;
     const int np = w_last - w_first + 1;
-    const int slot0 = (seg_start == w_first * tpw) ? 0 : 1;
+    // the segment is w_first's first piece when w_first's range begins in the
+    // segment's start-up units or at its first tile
+    const int slot0 = (w_first * tpw >= seg_start) ? 0 : 1;
     const size_t sbase = (size_t)w_first * 2;
 
     // Column span per split: all 256 threads when ncols >= 256, else pow2(ncols).

@@ -230,39 +230,47 @@ struct MfmaPiece {
 };
 
 // Cursor over the pieces of one wavefront's range [g, g_end) of the batch's
-// tiles; s is the sequence holding tile g.
+// split units; s is the sequence holding unit g.
 struct RangeCursor {
     int g, g_end, s, first, w;
 };
 
 // The next piece of the range (false at its end).  Same decomposition as
 // stream_k_walk, one piece at a time, so the kernel can look one piece ahead.
+// A range that ends inside a segment's start-up units makes no piece of it.
 template <int TT>
 __device__ __forceinline__ bool next_piece(const DecodeParams &p, const int *__restrict__ lens,
                                            const int *pre, RangeCursor &c, MfmaPiece &pc) {
-    if (c.g >= c.g_end) return false;
     const int segs = p.num_kv_heads * p.head_tiles;
-    const int L = min(max(lens[c.s], 0), p.max_ctx);
-    const int Ts = (L + TT - 1) / TT;
-    const int local = c.g - __builtin_amdgcn_readfirstlane(pre[c.s]);
-    const int seg = local / Ts;
-    const int t0 = local - seg * Ts;
-    const int n = min(Ts - t0, c.g_end - c.g);
-    pc.s = c.s;
-    pc.kvh = seg / p.head_tiles;
-    pc.ht = seg - pc.kvh * p.head_tiles;
-    pc.t_begin = t0 * TT;
-    pc.t_end = min(L, (t0 + n) * TT);
-    pc.whole = t0 == 0 && n == Ts;
-    pc.slot = c.w * 2 + (c.first ? 0 : 1);
-    c.g += n;
-    c.first = 0;
-    if (c.g - __builtin_amdgcn_readfirstlane(pre[c.s]) >= Ts * segs) {  // sequence done
-        int s = c.s + 1;
-        while (s < p.num_seqs - 1 && pre[s + 1] == pre[s]) s++;
-        c.s = __builtin_amdgcn_readfirstlane(s);
+    while (c.g < c.g_end) {
+        const int L = min(max(lens[c.s], 0), p.max_ctx);
+        const int Ts = (L + TT - 1) / TT;
+        const int Cs = segment_units(p, Ts);
+        const int base = __builtin_amdgcn_readfirstlane(pre[c.s]);
+        const int local = c.g - base;
+        const int seg = local / Cs;
+        const int u0 = local - seg * Cs;
+        const int u1 = min(Cs, u0 + (c.g_end - c.g));
+        const int t0 = max(u0 - p.seg_cost, 0), t1 = max(u1 - p.seg_cost, 0);
+        c.g += u1 - u0;
+        const int cur_s = c.s;
+        if (c.g - base >= Cs * segs) {  // sequence done: next one with tiles
+            int s = c.s + 1;
+            while (s < p.num_seqs - 1 && pre[s + 1] == pre[s]) s++;
+            c.s = __builtin_amdgcn_readfirstlane(s);
+        }
+        if (t1 <= t0) continue;  // only start-up units of this segment (the range's end)
+        pc.s = cur_s;
+        pc.kvh = seg / p.head_tiles;
+        pc.ht = seg - pc.kvh * p.head_tiles;
+        pc.t_begin = t0 * TT;
+        pc.t_end = min(L, t1 * TT);
+        pc.whole = t0 == 0 && t1 == Ts;
+        pc.slot = c.w * 2 + (c.first ? 0 : 1);
+        c.first = 0;
+        return true;
     }
-    return true;
+    return false;
 }
 
 // Q rows of the piece's (up to) 16 query heads in the MFMA B layout (lane:
@@ -334,7 +342,7 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
     cur.first = 1;
     cur.w = w;
     {
-        // the sequence holding tile g: the last s with pre[s] <= g (empty
+        // the sequence holding unit g: the last s with pre[s] <= g (empty
         // sequences share their successor's prefix, so this lands on one
         // with tiles)
         int lo = 0, hi = B - 1;
@@ -346,7 +354,9 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
     }
 
     MfmaPiece pc;
-    next_piece<16>(p, lens, pre, cur, pc);
+    // A range inside one segment's start-up units holds no tile (only when
+    // tpw <= seg_cost); the segment's tiles belong to the next wavefront.
+    if (!next_piece<16>(p, lens, pre, cur, pc)) return;
     u32x4 q[G::kQkSteps];
     mfma_load_q<D>(p, pc, lane, q);
     int ids = mfma_load_ids(p, tables, pc, 0, lane);

@@ -12,10 +12,15 @@ enum KvType : int { KV_F16 = 1, KV_BF16 = 2, KV_F32 = 3 };
 //
 // The batch is the sequence of segments (sequence s, kv head, head tile) in
 // that order; segment (s, .) holds T_s = ceil(L_s / tile_tokens) tiles.  All
-// segments laid end to end form `total` tiles.  Wavefront w of the launch owns
-// the contiguous tile range [w*tpw, min((w+1)*tpw, total)) with
-// tpw = max(min_tiles_per_wave, ceil(total / num_waves)), so every
-// wavefront streams the same number of K/V bytes whatever the ragged lengths.
+// segments laid end to end form `total` split units, where a segment of T
+// tiles costs T + seg_cost units: its tiles, after seg_cost units of
+// start-up (the dependent loads before its first tile computes; measured on
+// MI355X at ~1.5 tiles' time).  Wavefront w of the launch owns the
+// contiguous unit range [w*tpw, min((w+1)*tpw, total)) with
+// tpw = max(min_tiles_per_wave, ceil(total / num_waves)) and computes the
+// tiles that fall in it, so every wavefront spends the same time whatever
+// the ragged lengths -- a run of one-tile segments no longer lands on one
+// wavefront as tiles of equal weight.
 // A segment that lies inside one wavefront's range is finished there and
 // written straight to the output; a segment cut by range boundaries leaves
 // one fp32 partial (m, l, o) per wavefront that touched it, in that
@@ -51,7 +56,8 @@ struct DecodeParams {
     int bs_shift;              // log2(block_size)
     int max_ctx;               // max_blocks * block_size
     int num_waves;             // wavefronts of the partition kernel launch
-    int min_tiles_per_wave;    // lower bound of tpw (>= 1)
+    int min_tiles_per_wave;    // lower bound of tpw (>= 1), in split units
+    int seg_cost;              // split units a segment costs on top of its tiles
     float scale_log2;          // scale * log2(e)
     int merge_per_segment;     // 1: merge with one workgroup per segment
     // Partial-output mode (cascade passes): when out_f32 is set, every
