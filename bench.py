@@ -12,7 +12,9 @@ one.
 Prints ONE JSON line:
   value        seqs/s = num_seqs / (GPU time per step), whole job on 1 GPU
   roofline     algorithmic bytes of one launch / average duration of the
-               partition kernel (HIP events on its stream), against 8 TB/s;
+               partition kernel (HIP events on its stream around each launch,
+               over K further steps: the events are kept out of the K timed
+               steps that give `value`), against 8 TB/s;
                `traffic` = HBM bytes per launch from the committed rocprofv3
                PMC summary for this workload (profiles/), else null
   cpu_baseline the oracle (C restatement of the reference CPU attention)
@@ -532,18 +534,14 @@ def main() -> int:
     if st != 0:
         raise RuntimeError(f"launch failed: {msg}")
 
+    # The K timed steps: back-to-back calls bracketed by two events.
     ev = HipEvents()
     begin, end = ev.create(), ev.create()
-    k_start = [ev.create() for _ in range(args.steps)]
-    k_done = [ev.create() for _ in range(args.steps)]
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     ev.record(begin, stream)
     for i in range(args.steps):
-        if not args.cascade:
-            lib.nxt_attn_set_trace_events(k_start[i], k_done[i])
         step(args.warmup + i)
-    lib.nxt_attn_set_trace_events(None, None)
     ev.record(end, stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
@@ -551,8 +549,24 @@ def main() -> int:
     if st != 0:
         raise RuntimeError(f"launch failed: {msg}")
     total_ms = ev.elapsed_ms(begin, end)
-    kern_ms = (np.array([total_ms / args.steps]) if args.cascade else
-               np.array([ev.elapsed_ms(a, b) for a, b in zip(k_start, k_done)]))
+    # The partition kernel's launch durations: K more steps of the same
+    # calls, the library recording an event on the stream before and after
+    # each partition launch.  Kept out of the timed steps: the two extra
+    # event packets per step lengthen it by ~5 us on MI355X.
+    if args.cascade:
+        kern_ms = np.array([total_ms / args.steps])
+    else:
+        k_start = [ev.create() for _ in range(args.steps)]
+        k_done = [ev.create() for _ in range(args.steps)]
+        for i in range(args.steps):
+            lib.nxt_attn_set_trace_events(k_start[i], k_done[i])
+            step(args.warmup + args.steps + i)
+        lib.nxt_attn_set_trace_events(None, None)
+        torch.cuda.synchronize()
+        st, msg = PA.last_status()
+        if st != 0:
+            raise RuntimeError(f"launch failed: {msg}")
+        kern_ms = np.array([ev.elapsed_ms(a, b) for a, b in zip(k_start, k_done)])
     ev.destroy_all()
 
     ms_per_step = total_ms / args.steps

@@ -43,11 +43,22 @@ static hipError_t launch_merge(const DecodeParams &p, hipStream_t st, hipEvent_t
         if (e != hipSuccess) return e;
     }
     const unsigned segs = (unsigned)(p.num_seqs * p.num_kv_heads * p.head_tiles);
+    const int heads = p.group < GT ? p.group : GT;
     if (p.merge_per_segment) {
-        paged_decode_merge_segment_kernel<KV, D, GT, TT><<<segs, kMergeSegThreads, 0, st>>>(p);
+        // float4 columns per thread: the segment's heads * D/4 over 256 threads
+        constexpr int kMaxKc = (GT * (D / 4) + kMergeSegThreads - 1) / kMergeSegThreads;
+        const int cols = heads * (D / 4);
+        // (cols <= kMaxKc * 256, so the "1" alternatives below are never launched)
+        if (cols <= kMergeSegThreads)
+            paged_decode_merge_segment_kernel<KV, D, GT, TT, 1><<<segs, kMergeSegThreads, 0, st>>>(p);
+        else if (cols <= 2 * kMergeSegThreads)
+            paged_decode_merge_segment_kernel<KV, D, GT, TT, (kMaxKc > 1 ? 2 : 1)>
+                <<<segs, kMergeSegThreads, 0, st>>>(p);
+        else
+            paged_decode_merge_segment_kernel<KV, D, GT, TT, (kMaxKc > 2 ? 4 : 1)>
+                <<<segs, kMergeSegThreads, 0, st>>>(p);
         return hipGetLastError();
     }
-    const int heads = p.group < GT ? p.group : GT;
     const unsigned chunks = (unsigned)((heads * (D / 4) + kMergeCols - 1) / kMergeCols);
     paged_decode_merge_kernel<KV, D, GT, TT>
         <<<dim3(segs, chunks), kMergeCols * kMergeSplit, 0, st>>>(p);

@@ -585,6 +585,62 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
     });
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Online log-sum-exp merge, into (m, l, acc) of KC columns, of a segment's
+// partials j = j0, j0 + step, ... < np (partial j in slot
+// sbase + 2j + (j == 0 ? slot0 : 0)).  The partials go in batches of up to
+// NB whose loads are all issued before any is used, so a thread waits for
+// one memory round trip per batch, not per partial; batch slots past np
+// load and combine nothing.  Column k's (m, l) and float4 of o sit at
+// off_ml[k] and off_o[k] floats into a slot.
+template <int GT, int D, int KC, int NB>
+__device__ __forceinline__ void merge_partials(const DecodeParams &p, size_t sbase, int slot0,
+                                               int j0, int step, int np, const int (&off_ml)[KC],
+                                               const int (&off_o)[KC], float (&m)[KC],
+                                               float (&l)[KC], f32x4 (&acc)[KC]) {
+    for (int jb = j0; jb < np; jb += NB * step) {
+        f32x2 mlv[NB][KC];
+        f32x4 ov[NB][KC];
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const int j = jb + b * step;
+#pragma unroll
+            for (int k = 0; k < KC; k++) {  // (defined values for the slots left unread)
+                mlv[b][k] = f32x2{-INFINITY, 0.0f};
+                ov[b][k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+            if (j < np) {
+                const size_t slot = sbase + 2 * (size_t)j + (j == 0 ? slot0 : 0);
+                const float *mlb = p.ws_ml + slot * GT * 2;
+                const float *ob = p.ws_o + slot * GT * D;
+#pragma unroll
+                for (int k = 0; k < KC; k++) {
+                    mlv[b][k] = *(const f32x2 *)(mlb + off_ml[k]);
+                    ov[b][k] = *(const f32x4 *)(ob + off_o[k]);
+                }
+            }
+        }
+        // keep the scheduler from starting the combine (and waiting on the
+        // first loads) before the whole batch is issued
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            if (jb + b * step >= np) break;
+#pragma unroll
+            for (int k = 0; k < KC; k++) {
+                const float mj = mlv[b][k].x;
+                const float M = fmaxf(m[k], mj);
+                const float Ms = (M == -INFINITY) ? 0.0f : M;
+                const float a = fast_exp2(m[k] - Ms), w = fast_exp2(mj - Ms);
+                l[k] = l[k] * a + mlv[b][k].y * w;
+                acc[k] = acc[k] * a + ov[b][k] * w;
+                m[k] = M;
+            }
+        }
+    }
+}
+
 // Merge kernel: one workgroup per (segment, chunk of kMergeCols output
 // float4 columns), where a segment is (sequence, kv head, head tile) and the
 // columns run over (head h < nh, dims 4c..4c+3).  It writes zeros for an
@@ -616,7 +672,13 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
     const int col0 = blockIdx.y * kMergeCols;
     if (col0 >= ncols) return;
     const int tid = threadIdx.x;
+    // the three scalars the merge needs, requested together (the empty asm
+    // keeps the compiler from sinking the prefix loads past the L == 0 exit,
+    // which would cost a second round trip)
     const int L = seq_len_of(p, s);
+    const int total = p.ws_prefix[p.num_seqs];
+    const int pre_s = p.ws_prefix[s];
+    asm volatile("" ::"s"(total), "s"(pre_s));
     const size_t qrow0 = ((size_t)s * p.num_heads + (size_t)kvh * p.group + g0) * D;
 
     if (L == 0) {
@@ -632,10 +694,9 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
         }
         return;
     }
-    const int total = p.ws_prefix[p.num_seqs];
     const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);
     const int Ts = (L + TT - 1) / TT;
-    const int seg_start = p.ws_prefix[s] + seg * segment_units(p, Ts);  // in split units
+    const int seg_start = pre_s + seg * segment_units(p, Ts);  // in split units
     const int first_tile = seg_start + p.seg_cost;
     const int w_first = first_tile / tpw;
     const int w_last = (first_tile + Ts - 1) / tpw;
@@ -652,48 +713,37 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
     const int col = col0 + cl;
     const bool active = col < ncols;
     const int h = active ? col / C4 : 0;
-    const int c = col - h * C4;
-    float m = -INFINITY, l = 0.0f;
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (active) {
-#pragma unroll 4
-        for (int jj = ps; jj < np; jj += kMergeSplit) {
-            const size_t slot = sbase + 2 * jj + (jj == 0 ? slot0 : 0);
-            const float mj = p.ws_ml[(slot * GT + h) * 2];
-            const float lj = p.ws_ml[(slot * GT + h) * 2 + 1];
-            const f32x4 o = *(const f32x4 *)(p.ws_o + (slot * GT + h) * D + c * 4);
-            const float M = fmaxf(m, mj);
-            const float Ms = (M == -INFINITY) ? 0.0f : M;
-            const float a = fast_exp2(m - Ms), b = fast_exp2(mj - Ms);
-            l = l * a + lj * b;
-            acc = acc * a + o * b;
-            m = M;
-        }
-    }
-    s_acc[ps][cl] = acc;
-    s_m[ps][cl] = m;
-    s_l[ps][cl] = l;
+    const int c = active ? col - h * C4 : 0;
+    float m[1] = {-INFINITY}, l[1] = {0.0f};
+    f32x4 acc[1] = {{0.0f, 0.0f, 0.0f, 0.0f}};
+    const int off_ml[1] = {h * 2}, off_o[1] = {h * D + c * 4};
+    if (active) merge_partials<GT, D, 1, 8>(p, sbase, slot0, ps, kMergeSplit, np, off_ml, off_o, m, l, acc);
+    s_acc[ps][cl] = acc[0];
+    s_m[ps][cl] = m[0];
+    s_l[ps][cl] = l[0];
     __syncthreads();
     if (ps != 0 || !active) return;
+    float mm = m[0], ll = l[0];
+    f32x4 aa = acc[0];
 #pragma unroll
     for (int k = 1; k < kMergeSplit; k++) {
         const float mk = s_m[k][cl];
-        const float M = fmaxf(m, mk);
+        const float M = fmaxf(mm, mk);
         const float Ms = (M == -INFINITY) ? 0.0f : M;
-        const float a = fast_exp2(m - Ms), b = fast_exp2(mk - Ms);
-        l = l * a + s_l[k][cl] * b;
-        acc = acc * a + s_acc[k][cl] * b;
-        m = M;
+        const float a = fast_exp2(mm - Ms), b = fast_exp2(mk - Ms);
+        ll = ll * a + s_l[k][cl] * b;
+        aa = aa * a + s_acc[k][cl] * b;
+        mm = M;
     }
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const float inv = ll > 0.0f ? 1.0f / ll : 0.0f;
     const size_t base = qrow0 + (size_t)h * D + c * 4;
     if (p.out_f32) {
-        *(f32x4 *)(p.out_f32 + base) = acc * inv;
-        if (c == 0) p.out_lse[qrow0 / D + h] = l > 0.0f ? m + log2f(l) : -INFINITY;
+        *(f32x4 *)(p.out_f32 + base) = aa * inv;
+        if (c == 0) p.out_lse[qrow0 / D + h] = ll > 0.0f ? mm + log2f(ll) : -INFINITY;
         return;
     }
 #pragma unroll
-    for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, acc[e] * inv);
+    for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, aa[e] * inv);
 }
 
 
@@ -701,17 +751,17 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
 // to fill the GPU (where the (segment, chunk) grid above would launch several
 // thousand short workgroups, each costing ~2 ns of dispatch).  The 256
 // threads cover the segment's ncols float4 columns: with ncols >= 256 each
-// thread owns columns t, t + 256, ...; with fewer, the S = 256 / pow2(ncols)
+// thread owns the KC columns t, t + 256, ... (KC = ceil(ncols / 256), a
+// power of two chosen at launch); with fewer, the S = 256 / pow2(ncols)
 // threads of a column split its partials (every S-th one) and combine in LDS.
-// Each thread runs the online log-sum-exp merge with four partials' loads in
-// flight.
+// Each thread runs the online log-sum-exp merge over its columns together,
+// a batch of partials' loads in flight at a time.
 constexpr int kMergeSegThreads = 256;
 
-template <int KV, int D, int GT, int TT>
+template <int KV, int D, int GT, int TT, int KC>
 __global__ __launch_bounds__(kMergeSegThreads) void paged_decode_merge_segment_kernel(
     const DecodeParams p) {
     constexpr int C4 = D / 4;
-    constexpr int KC = (GT * C4 + kMergeSegThreads - 1) / kMergeSegThreads;
     __shared__ f32x4 s_acc[kMergeSegThreads];
     __shared__ float s_m[kMergeSegThreads];
     __shared__ float s_l[kMergeSegThreads];
@@ -723,7 +773,13 @@ __global__ __launch_bounds__(kMergeSegThreads) void paged_decode_merge_segment_k
     const int nh = min(GT, p.group - g0);
     const int ncols = nh * C4;
     const int tid = threadIdx.x;
+    // the three scalars the merge needs, requested together (the empty asm
+    // keeps the compiler from sinking the prefix loads past the L == 0 exit,
+    // which would cost a second round trip)
     const int L = seq_len_of(p, s);
+    const int total = p.ws_prefix[p.num_seqs];
+    const int pre_s = p.ws_prefix[s];
+    asm volatile("" ::"s"(total), "s"(pre_s));
     const size_t qrow0 = ((size_t)s * p.num_heads + (size_t)kvh * p.group + g0) * D;
 
     if (L == 0) {
@@ -739,10 +795,9 @@ __global__ __launch_bounds__(kMergeSegThreads) void paged_decode_merge_segment_k
         }
         return;
     }
-    const int total = p.ws_prefix[p.num_seqs];
     const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);
     const int Ts = (L + TT - 1) / TT;
-    const int seg_start = p.ws_prefix[s] + seg * segment_units(p, Ts);  // in split units
+    const int seg_start = pre_s + seg * segment_units(p, Ts);  // in split units
     const int first_tile = seg_start + p.seg_cost;
     const int w_first = first_tile / tpw;
     const int w_last = (first_tile + Ts - 1) / tpw;
@@ -762,29 +817,22 @@ __global__ __launch_bounds__(kMergeSegThreads) void paged_decode_merge_segment_k
 
     float m[KC], l[KC];
     f32x4 acc[KC];
+    int off_ml[KC], off_o[KC];
 #pragma unroll
     for (int k = 0; k < KC; k++) {
         m[k] = -INFINITY;
         l[k] = 0.0f;
         acc[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        const int col = cl + k * kMergeSegThreads;
-        if (col >= ncols) continue;
+        // a column past ncols (last head tile of a group) reads column cl
+        // again and is never stored
+        const int col = cl + k * kMergeSegThreads < ncols ? cl + k * kMergeSegThreads : cl;
         const int h = col / C4;
-        const int c = col - h * C4;
-#pragma unroll 4
-        for (int j = split; j < np; j += nsplit) {
-            const size_t slot = sbase + 2 * j + (j == 0 ? slot0 : 0);
-            const float mj = p.ws_ml[(slot * GT + h) * 2];
-            const float lj = p.ws_ml[(slot * GT + h) * 2 + 1];
-            const f32x4 o = *(const f32x4 *)(p.ws_o + (slot * GT + h) * D + c * 4);
-            const float M = fmaxf(m[k], mj);
-            const float Ms = (M == -INFINITY) ? 0.0f : M;
-            const float a = fast_exp2(m[k] - Ms), b = fast_exp2(mj - Ms);
-            l[k] = l[k] * a + lj * b;
-            acc[k] = acc[k] * a + o * b;
-            m[k] = M;
-        }
+        off_ml[k] = h * 2;
+        off_o[k] = h * D + (col - h * C4) * 4;
     }
+    if (cl < ncols)
+        merge_partials<GT, D, KC, (KC <= 2 ? 8 : 4)>(p, sbase, slot0, split, nsplit, np, off_ml,
+                                                     off_o, m, l, acc);
     if (nsplit > 1) {  // KC == 1 here: ncols < 256
         s_acc[tid] = acc[0];
         s_m[tid] = m[0];
