@@ -412,7 +412,8 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=200,
+                    help="untimed steps first (>= ~20 ms of work: the GPU clocks ramp up over it)")
     ap.add_argument("--config", type=int, default=2, help="1..5, 6 = config 4b (GQA16)")
     ap.add_argument("--partition", type=int, default=0,
                     help="split-K tokens per wavefront (0 = automatic stream-K plan)")

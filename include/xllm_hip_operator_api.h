@@ -146,8 +146,9 @@ const char *nxt_attn_version(void);
  * even where sequences share them (radix-shared prefixes,
  * src/core/prefix_sharing.c).  Same result as nxt_paged_attention_ex (same
  * arguments and layouts, within the dtype's rounding), but the pages of a
- * shared prefix are read once per 16 (sequence, query head) rows of the
- * sequences that share them instead of once per sequence.
+ * shared prefix are read once per 32 (sequence, query head) rows of the
+ * sequences that share them (16 for fp32 or head_size > 128) instead of
+ * once per sequence.
  *   prefix_group[num_seqs]  device int32: group of each sequence, -1 = none
  *   prefix_blocks[max_groups] device int32: the number of leading pages (full
  *                           pages, block_size tokens each) that every member

@@ -1,7 +1,8 @@
 """GPU parity of the prefix-aware (cascade) decode and of the shared-prefix
 detection.  The cascade computes the same attention as nxt_paged_attention
 (the oracle's, examples/text_gen.c:1284-1310 over the paged layout) with
-shared prefix pages read once per 16 rows; results are checked against the
+shared prefix pages read once per prefix-batch sequence of 16 or 32 query
+rows per kv head; results are checked against the
 oracle at the task's tolerances.  Detection is checked against its
 restatement (tests/cascade_cases.py), itself pinned on config 5's known
 sharing in test_prefix_detect.py."""
@@ -86,11 +87,12 @@ def test_cascade_config5_matches_oracle(cuda):
 @pytest.mark.parametrize("dtype,D,H,KVH", [("fp16", 128, 32, 8), ("bf16", 128, 64, 8),
                                           ("fp16", 64, 8, 8), ("bf16", 256, 16, 1),
                                           ("fp16", 80, 16, 4), ("fp32", 64, 12, 12),
-                                          ("fp32", 128, 32, 8)])
+                                          ("fp32", 128, 32, 8), ("fp16", 96, 64, 2)])
 def test_cascade_groups_match_oracle(cuda, dtype, D, H, KVH):
-    """Groups of 1..21 members (prefix rows spanning several 16-row prefix
-    sequences), members with an empty suffix, unshared sequences (L = 1,
-    L = 0, long), on the MFMA and VALU tile paths."""
+    """Groups of 1..21 members (prefix rows spanning several 16- or 32-row
+    prefix sequences), members with an empty suffix, unshared sequences
+    (L = 1, L = 0, long), on the MFMA (one and two 16-head row blocks per
+    wavefront) and VALU tile paths."""
     spec = [(5, [3, 0, 40, 16, 1]), (1, [7] * 21), (12, [100]), (2, [0, 0])]
     wl, pg, pb = shared_case(spec, singles=[1, 0, 333], H=H, KVH=KVH, D=D, kv_dtype=DT[dtype],
                              seed=D + H)

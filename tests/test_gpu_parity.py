@@ -98,12 +98,15 @@ def test_split_k_every_tile_path(cuda, dtype, head_size):
     # (H, KVH, D, dtype, num_seqs): >= 512 segments, so the merge runs one
     # workgroup per segment; float4 columns per segment 128 (two threads per
     # column split the partials), 512 and 1024 (threads own 2 / 4 columns),
-    # and the VALU head tiles of 8 query heads (one and four per kv head).
+    # the VALU head tiles of 8 query heads (one and four per kv head), and
+    # the MFMA tiles of 32 query heads (384 and 1024 columns).
     (32, 8, 128, "fp16", 64),
     (64, 4, 128, "bf16", 128),
     (32, 2, 256, "fp16", 256),
     (64, 8, 64, "fp32", 64),
     (64, 2, 64, "fp32", 64),
+    (48, 2, 64, "bf16", 256),
+    (64, 2, 128, "fp16", 256),
 ])
 def test_merge_per_segment_paths(cuda, shape):
     """Batches with enough segments merge with one workgroup per segment:
@@ -121,6 +124,25 @@ def test_merge_per_segment_paths(cuda, shape):
         print(f"case H={H} KVH={KVH} d={D} {dtype} seqs={nseq} partition={part}", flush=True)
         assert_close(run_gpu(wl, partition_tokens=part), ref, wl.kv_dtype,
                      f"H={H} KVH={KVH} d={D} part={part}")
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("head_size", [32, 64, 96, 128, 256])
+@pytest.mark.parametrize("heads", [(34, 2), (24, 1), (64, 2)])
+def test_mfma_groups_of_17_to_32(cuda, dtype, head_size, heads):
+    """Groups of 17-32 query heads on the MFMA path: one wavefront carries two
+    16-head row blocks over every K/V tile (head_size <= 128; two wavefronts
+    of one block above), with a partly filled second block for 17 and 24
+    heads; automatic plans and explicit partitions (partials of 32 heads
+    merged)."""
+    H, KVH = heads
+    wl = W.small_case(num_seqs=5, H=H, KVH=KVH, D=head_size, kv_dtype=DT[dtype],
+                      seed=H * head_size + KVH, lens=[0, 1, 40, 700, 1500])
+    ref = oracle(wl)
+    for part in (0, 64):
+        print(f"case H={H} KVH={KVH} d={head_size} {dtype} partition={part}", flush=True)
+        assert_close(run_gpu(wl, partition_tokens=part), ref, wl.kv_dtype,
+                     f"H={H} KVH={KVH} d={head_size} part={part}")
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])

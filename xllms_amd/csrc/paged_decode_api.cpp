@@ -160,11 +160,15 @@ struct HeadTiling {
     int head_tiles;  // wavefronts per (seq, kv head, partition)
 };
 
-bool head_tiling(int group, bool mfma, HeadTiling *t) {
+bool head_tiling(int group, bool mfma, int head_size, HeadTiling *t) {
     if (group <= 0 || group > xhip::kMaxHeadTile * xhip::kWavesPerGroup) return false;
     if (mfma) {
-        t->head_tile = xhip::kMfmaHeads;
-        t->head_tiles = (group + xhip::kMfmaHeads - 1) / xhip::kMfmaHeads;
+        // groups of 17-32 heads: one wavefront with two row blocks reads each
+        // K/V tile once for all of them (head_size <= 128), else two
+        // wavefronts of one block each
+        const bool wide = group > xhip::kMfmaHeads && head_size <= xhip::kMfmaWideMaxHeadSize;
+        t->head_tile = wide ? 2 * xhip::kMfmaHeads : xhip::kMfmaHeads;
+        t->head_tiles = (group + t->head_tile - 1) / t->head_tile;
         return true;
     }
     if (group <= xhip::kMaxHeadTile) {
@@ -180,6 +184,7 @@ bool head_tiling(int group, bool mfma, HeadTiling *t) {
 // Smallest stream-K range, in tiles, the automatic plan gives a wavefront:
 // below this the per-range setup (prefix lookup, Q load, merge) dominates.
 constexpr int kMinTilesPerWave = 4;
+
 
 int partition_occupancy(int kv_dtype, int head_size, int head_tile, bool mfma, size_t lds) {
     switch (kv_dtype) {
@@ -199,7 +204,7 @@ int waves_per_group(bool mfma) { return mfma ? xhip::kMfmaWavesPerGroup : xhip::
 
 // Wavefronts of the automatic plan: one resident round of the partition
 // kernel on every CU, but no more than the batch could keep busy with
-// kMinTilesPerWave tiles each.
+// kMinTilesPerWave units each.
 long long auto_waves(int kv_dtype, int head_size, int head_tile, bool mfma, int nseq,
                      long long ub_tiles, int cus) {
     const size_t lds = (size_t)(nseq + 1) * sizeof(int);
@@ -281,7 +286,7 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
     const int group = num_heads / num_kv_heads;
     const bool mfma = use_mfma(kv_dtype, head_size, block_size);
     HeadTiling tiling;
-    if (!head_tiling(group, mfma, &tiling))
+    if (!head_tiling(group, mfma, head_size, &tiling))
         return set_status(NXT_ATTN_E_UNSUPPORTED, "GQA group %d > %d", group,
                           xhip::kMaxHeadTile * xhip::kWavesPerGroup);
     if (num_seqs == 0) return ok();
@@ -388,9 +393,17 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         p.seg_cost = seg_cost;
         p.scale_log2 = scale * 1.4426950408889634f;
         // One merge workgroup per segment once the segments alone fill two
-        // workgroups per CU; fewer, longer segments (few sequences, long
-        // contexts) take the (segment, column chunk) merge grid.
-        p.merge_per_segment = (long long)nseq * segs >= 2LL * cus ? 1 : 0;
+        // workgroups per CU, or once the (segment, column chunk) grid would
+        // launch more than four workgroups per CU (each costs ~2 ns of
+        // dispatch; 32-head tiles have 32 chunks per segment at head_size
+        // 128).  Fewer, longer segments of few heads (few sequences, long
+        // contexts) take the chunk grid, whose 8 threads per column split
+        // the many partials.
+        const int mheads = group < tiling.head_tile ? group : tiling.head_tile;
+        const long long chunks = (mheads * (head_size / 4) + xhip::kMergeCols - 1) / xhip::kMergeCols;
+        p.merge_per_segment =
+            ((long long)nseq * segs >= 2LL * cus || (long long)nseq * segs * chunks > 4LL * cus) ? 1
+                                                                                                : 0;
 
         if (t_trace_start) {
             e = hipEventRecord(t_trace_start, stream);
@@ -442,7 +455,14 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
         max_num_blocks_per_seq <= 0 || !is_pow2(block_size))
         return set_status(NXT_ATTN_E_INVALID, "bad cascade arguments");
     const int group = num_heads / num_kv_heads;
-    const int rows = (group + xhip::kCascadeRows - 1) / xhip::kCascadeRows * xhip::kCascadeRows;
+    // Query rows per kv head of a prefix-batch sequence: 32 where the MFMA
+    // path serves 32 heads per wavefront (each shared page then feeds twice
+    // as many members per read), else a multiple of the 16-head tile.
+    const bool wide = use_mfma(kv_dtype, head_size, block_size) &&
+                      head_size <= xhip::kMfmaWideMaxHeadSize && group <= 2 * xhip::kCascadeRows;
+    const int rows = wide ? 2 * xhip::kCascadeRows
+                          : (group + xhip::kCascadeRows - 1) / xhip::kCascadeRows *
+                                xhip::kCascadeRows;
     const long long v_max = ((long long)num_seqs * group + rows - 1) / rows + max_groups;
     const size_t mb = (size_t)max_num_blocks_per_seq;
     const size_t KR = (size_t)num_kv_heads * rows;
@@ -730,13 +750,15 @@ __attribute__((visibility("default"))) int nxt_paged_attention_auto_waves(
     if (!is_pow2(block_size)) return NXT_ATTN_E_UNSUPPORTED;
     const bool mfma = use_mfma(kv_dtype, head_size, block_size);
     HeadTiling tiling;
-    if (!head_tiling(num_heads / num_kv_heads, mfma, &tiling)) return NXT_ATTN_E_UNSUPPORTED;
+    if (!head_tiling(num_heads / num_kv_heads, mfma, head_size, &tiling))
+        return NXT_ATTN_E_UNSUPPORTED;
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess) return NXT_ATTN_E_HIP;
     const int nseq = num_seqs < xhip::kMaxSeqsPerLaunch ? num_seqs : xhip::kMaxSeqsPerLaunch;
     const int tile = tile_tokens(head_size, kv_dtype, mfma);
     const long long ub = (long long)nseq * num_kv_heads * tiling.head_tiles *
-                         (((long long)max_num_blocks_per_seq * block_size + tile - 1) / tile);
+                         (((long long)max_num_blocks_per_seq * block_size + tile - 1) / tile +
+                          kSegmentCost);
     const long long w = auto_waves(kv_dtype, head_size, tiling.head_tile, mfma, nseq, ub,
                                    cu_count(device));
     return w > 0 ? (int)w : NXT_ATTN_E_HIP;

@@ -24,13 +24,23 @@ template <int KV, int D> constexpr bool has_mfma() {
     return KV != KV_F32 && D % 32 == 0;
 }
 
+// Two row blocks per wavefront (head tile 32) fit the register file at two
+// wavefronts per SIMD up to head_size 128.
+template <int KV, int D> constexpr bool has_mfma_wide() {
+    return has_mfma<KV, D>() && D <= kMfmaWideMaxHeadSize;
+}
+
 template <int KV, int D>
 static const void *partition_fn(int head_tile, bool mfma) {
     if (mfma) {
-        if constexpr (has_mfma<KV, D>())
-            return head_tile == kMfmaHeads
-                       ? reinterpret_cast<const void *>(&paged_decode_partition_mfma_kernel<KV, D>)
-                       : nullptr;
+        if constexpr (has_mfma<KV, D>()) {
+            if (head_tile == kMfmaHeads)
+                return reinterpret_cast<const void *>(&paged_decode_partition_mfma_kernel<KV, D, 1>);
+            if constexpr (has_mfma_wide<KV, D>())
+                if (head_tile == 2 * kMfmaHeads)
+                    return reinterpret_cast<const void *>(
+                        &paged_decode_partition_mfma_kernel<KV, D, 2>);
+        }
         return nullptr;
     }
     return valu_fn<KV, D>(head_tile);
@@ -45,17 +55,21 @@ static hipError_t launch_merge(const DecodeParams &p, hipStream_t st, hipEvent_t
     const unsigned segs = (unsigned)(p.num_seqs * p.num_kv_heads * p.head_tiles);
     const int heads = p.group < GT ? p.group : GT;
     if (p.merge_per_segment) {
-        // float4 columns per thread: the segment's heads * D/4 over 256 threads
+        // float4 columns per thread: the segment's heads * D/4 over 256
+        // threads, rounded up to a power of two (cols <= kMaxKc * 256, so the
+        // "1" alternatives below are never launched)
         constexpr int kMaxKc = (GT * (D / 4) + kMergeSegThreads - 1) / kMergeSegThreads;
         const int cols = heads * (D / 4);
-        // (cols <= kMaxKc * 256, so the "1" alternatives below are never launched)
         if (cols <= kMergeSegThreads)
             paged_decode_merge_segment_kernel<KV, D, GT, TT, 1><<<segs, kMergeSegThreads, 0, st>>>(p);
         else if (cols <= 2 * kMergeSegThreads)
             paged_decode_merge_segment_kernel<KV, D, GT, TT, (kMaxKc > 1 ? 2 : 1)>
                 <<<segs, kMergeSegThreads, 0, st>>>(p);
-        else
+        else if (cols <= 4 * kMergeSegThreads)
             paged_decode_merge_segment_kernel<KV, D, GT, TT, (kMaxKc > 2 ? 4 : 1)>
+                <<<segs, kMergeSegThreads, 0, st>>>(p);
+        else
+            paged_decode_merge_segment_kernel<KV, D, GT, TT, (kMaxKc > 4 ? 8 : 1)>
                 <<<segs, kMergeSegThreads, 0, st>>>(p);
         return hipGetLastError();
     }
@@ -74,11 +88,22 @@ static hipError_t launch_for_head_size(const DecodeParams &p, int head_tile, boo
     const size_t lds = (size_t)(p.num_seqs + 1) * sizeof(int);
     if (mfma) {
         if constexpr (has_mfma<KV, D>()) {
-            if (head_tile != kMfmaHeads) return hipErrorInvalidValue;
-            paged_decode_partition_mfma_kernel<KV, D>
-                <<<(unsigned)(p.num_waves / kMfmaWavesPerGroup), 64 * kMfmaWavesPerGroup, lds, st>>>(
-                    p, p.seq_lens, p.block_tables);
-            return launch_merge<KV, D, kMfmaHeads, MfmaGeometry<D>::kTile>(p, st, after_partition);
+            const unsigned mgrid = (unsigned)(p.num_waves / kMfmaWavesPerGroup);
+            if (head_tile == kMfmaHeads) {
+                paged_decode_partition_mfma_kernel<KV, D, 1>
+                    <<<mgrid, 64 * kMfmaWavesPerGroup, lds, st>>>(p, p.seq_lens, p.block_tables);
+                return launch_merge<KV, D, kMfmaHeads, MfmaGeometry<D>::kTile>(p, st,
+                                                                              after_partition);
+            }
+            if constexpr (has_mfma_wide<KV, D>()) {
+                if (head_tile == 2 * kMfmaHeads) {
+                    paged_decode_partition_mfma_kernel<KV, D, 2>
+                        <<<mgrid, 64 * kMfmaWavesPerGroup, lds, st>>>(p, p.seq_lens,
+                                                                      p.block_tables);
+                    return launch_merge<KV, D, 2 * kMfmaHeads, MfmaGeometry<D>::kTile>(
+                        p, st, after_partition);
+                }
+            }
         }
         return hipErrorInvalidValue;
     }

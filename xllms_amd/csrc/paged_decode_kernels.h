@@ -651,7 +651,6 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p, size_t sba
 // rescaled denominator and float4 numerator), and the splits are combined in
 // LDS the same way.  TT is the tile length (tokens) of the partition kernel
 // that produced the partials: the range arithmetic must match it exactly.
-constexpr int kMergeCols = 32;
 constexpr int kMergeSplit = 8;
 
 template <int KV, int D, int GT, int TT>
@@ -831,7 +830,7 @@ __global__ __launch_bounds__(kMergeSegThreads) void paged_decode_merge_segment_k
         off_o[k] = h * D + (col - h * C4) * 4;
     }
     if (cl < ncols)
-        merge_partials<GT, D, KC, (KC <= 2 ? 8 : 4)>(p, sbase, slot0, split, nsplit, np, off_ml,
+        merge_partials<GT, D, KC, (KC <= 2 ? 8 : 8 / KC)>(p, sbase, slot0, split, nsplit, np, off_ml,
                                                      off_o, m, l, acc);
     if (nsplit > 1) {  // KC == 1 here: ncols < 256
         s_acc[tid] = acc[0];

@@ -1,6 +1,10 @@
 // MFMA tile path of the paged-decode attention (fp16 / bf16 K/V, head_size a
-// multiple of 32, block_size >= 16).  One wavefront serves up to 16 query
-// heads of one kv head; cost per 16-token tile does not depend on the group.
+// multiple of 32, block_size >= 16).  One wavefront serves R row blocks of 16
+// query heads of one kv head (R = 1, or 2 for groups of 17-32 heads at
+// head_size <= 128): every K/V tile it loads is used by all 16R heads.
+// Below, one row block; with R = 2 the QK^T MFMAs run once per block on the
+// same K registers, and each V^T operand read from LDS feeds both blocks' PV
+// MFMAs.
 //
 // Per 16-token tile (one page when block_size = 16), with g = lane/16 and
 // j = lane%16 (v_mfma_f32_16x16x{32,16} operand layouts, checked on gfx950):
@@ -146,10 +150,10 @@ template <int D> struct MfmaState {
     float l;                               // this lane's part of the running sum
 };
 
-template <int KV, int D>
-__device__ __forceinline__ void mfma_tile(const DecodeParams &p, const u32x4 *q, int t0,
-                                          int t_end, bool page_ok, int lane, char *lds,
-                                          const MfmaTileRegs<D> &r, MfmaState<D> &st) {
+template <int KV, int D, int R>
+__device__ __forceinline__ void mfma_tile(const DecodeParams &p, const u32x4 (*q)[MfmaGeometry<D>::kQkSteps],
+                                          int t0, int t_end, bool page_ok, int lane, char *lds,
+                                          const MfmaTileRegs<D> &r, MfmaState<D> (&st)[R]) {
     using G = MfmaGeometry<D>;
     const int j = lane & 15, g = lane >> 4;
 
@@ -164,47 +168,54 @@ __device__ __forceinline__ void mfma_tile(const DecodeParams &p, const u32x4 *q,
         dst[1] = u32x2{r.v[c][2], r.v[c][3]};
     }
 
-    // S = K Q^T for 16 tokens x 16 heads.
-    f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+    // S = K Q^T for 16 tokens x 16 heads, per row block.
+    f32x4 s[R];
 #pragma unroll
-    for (int c = 0; c < G::kQkSteps; c++) s = mfma_qk<KV>(r.k[c], q[c], s);
+    for (int b = 0; b < R; b++) s[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < G::kQkSteps; c++)
+#pragma unroll
+        for (int b = 0; b < R; b++) s[b] = mfma_qk<KV>(r.k[c], q[b][c], s[b]);
 
-    // Online softmax of head j over tokens 4g..4g+3 of this lane.
-    float sc[4];
+    bool ok[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const bool ok = page_ok && (t0 + 4 * g + i < t_end);
-        sc[i] = ok ? s[i] * p.scale_log2 : -INFINITY;
-    }
-    float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(st.m, mx);
-    const float ms = (m_new == -INFINITY) ? 0.0f : m_new;
-    const float alpha = fast_exp2(st.m - ms);
-    float pe[4];
-    float psum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        pe[i] = fast_exp2(sc[i] - ms);
-        psum += pe[i];
-    }
-    st.l = st.l * alpha + psum;
-    st.m = m_new;
+    for (int i = 0; i < 4; i++) ok[i] = page_ok && (t0 + 4 * g + i < t_end);
 
-    // P in the 16-bit type as hi + lo parts (B operand of the PV MFMA).
-    uint32_t hb[4], lb[4];
+    // Online softmax of head j over tokens 4g..4g+3 of this lane; P in the
+    // 16-bit type as hi + lo parts (B operand of the PV MFMA).
+    u32x2 p_hi[R], p_lo[R];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        float hv, lv;
-        hb[i] = round16<KV>(pe[i], hv);
-        lb[i] = round16<KV>(pe[i] - hv, lv);
+    for (int b = 0; b < R; b++) {
+        float sc[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) sc[i] = ok[i] ? s[b][i] * p.scale_log2 : -INFINITY;
+        float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(st[b].m, mx);
+        const float ms = (m_new == -INFINITY) ? 0.0f : m_new;
+        const float alpha = fast_exp2(st[b].m - ms);
+        float pe[4];
+        float psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            pe[i] = fast_exp2(sc[i] - ms);
+            psum += pe[i];
+        }
+        st[b].l = st[b].l * alpha + psum;
+        st[b].m = m_new;
+        uint32_t hb[4], lb[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float hv, lv;
+            hb[i] = round16<KV>(pe[i], hv);
+            lb[i] = round16<KV>(pe[i] - hv, lv);
+        }
+        p_hi[b] = u32x2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
+        p_lo[b] = u32x2{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
+#pragma unroll
+        for (int n = 0; n < G::kDimBlocks; n++) st[b].o[n] *= alpha;
     }
-    const u32x2 p_hi = {hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
-    const u32x2 p_lo = {lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
-
-#pragma unroll
-    for (int n = 0; n < G::kDimBlocks; n++) st.o[n] *= alpha;
 
     // O^T += V^T P for every 16-dim block.
     const char *vrow = lds + (4 * g) * G::kLdsRow + 2 * j;
@@ -216,8 +227,11 @@ __device__ __forceinline__ void mfma_tile(const DecodeParams &p, const u32x4 *q,
         const uint32_t v2 = *(const uint16_t *)(src + 2 * G::kLdsRow);
         const uint32_t v3 = *(const uint16_t *)(src + 3 * G::kLdsRow);
         const u32x2 a = {v0 | (v1 << 16), v2 | (v3 << 16)};
-        st.o[n] = mfma_pv<KV>(a, p_hi, st.o[n]);
-        st.o[n] = mfma_pv<KV>(a, p_lo, st.o[n]);
+#pragma unroll
+        for (int b = 0; b < R; b++) {
+            st[b].o[n] = mfma_pv<KV>(a, p_hi[b], st[b].o[n]);
+            st[b].o[n] = mfma_pv<KV>(a, p_lo[b], st[b].o[n]);
+        }
     }
 }
 
@@ -273,19 +287,24 @@ __device__ __forceinline__ bool next_piece(const DecodeParams &p, const int *__r
     return false;
 }
 
-// Q rows of the piece's (up to) 16 query heads in the MFMA B layout (lane:
-// head j, dims 32c+8g..+7); heads past the group read as zero.
-template <int D>
+// Q rows of the piece's (up to) 16R query heads in the MFMA B layout (row
+// block b, lane: head 16b + j, dims 32c+8g..+7); heads past the group read
+// as zero.
+template <int D, int R>
 __device__ __forceinline__ void mfma_load_q(const DecodeParams &p, const MfmaPiece &pc, int lane,
-                                            u32x4 (&q)[MfmaGeometry<D>::kQkSteps]) {
+                                            u32x4 (&q)[R][MfmaGeometry<D>::kQkSteps]) {
     const int j = lane & 15, g = lane >> 4;
-    const int g0 = pc.ht * kMfmaHeads;
-    const int nh = min(kMfmaHeads, p.group - g0);
+    const int g0 = pc.ht * kMfmaHeads * R;
+    const int nh = min(kMfmaHeads * R, p.group - g0);
     const size_t qrow0 = ((size_t)pc.s * p.num_heads + (size_t)pc.kvh * p.group + g0) * D;
 #pragma unroll
-    for (int c = 0; c < MfmaGeometry<D>::kQkSteps; c++)
-        q[c] = (j < nh) ? load16((const char *)p.q + (qrow0 + (size_t)j * D + 32 * c + 8 * g) * 2)
-                        : u32x4{0, 0, 0, 0};
+    for (int b = 0; b < R; b++)
+#pragma unroll
+        for (int c = 0; c < MfmaGeometry<D>::kQkSteps; c++)
+            q[b][c] = (16 * b + j < nh)
+                          ? load16((const char *)p.q +
+                                   (qrow0 + (size_t)(16 * b + j) * D + 32 * c + 8 * g) * 2)
+                          : u32x4{0, 0, 0, 0};
 }
 
 // Block ids of the piece's tiles first .. first+63, lane i holding tile
@@ -301,7 +320,7 @@ __device__ __forceinline__ int mfma_load_ids(const DecodeParams &p, const int *_
 
 namespace xhip {
 
-// Partition kernel, MFMA tile path (head tile of 16 query heads).
+// Partition kernel, MFMA tile path (head tile of 16R query heads).
 //
 // A wavefront walks the pieces of its stream-K range (usually one or two
 // segments) as one pipeline: while the last tile of a piece is computed, the
@@ -313,14 +332,14 @@ namespace xhip {
 // average at config 2).  Q is loaded when its piece begins: requesting the
 // next piece's Q a piece early as well gained ~1% at configs 2-4 but cost 5%
 // (cascade) to 10% (plain decode) at config 5 (measured, same box).
-template <int KV, int D>
+template <int KV, int D, int R>
 __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partition_mfma_kernel(
     const DecodeParams p, const int *__restrict__ lens, const int *__restrict__ tables) {
     // lens / tables are p.seq_lens / p.block_tables again: as restrict
     // kernel arguments their wavefront-uniform reads become scalar loads,
     // which do not wait behind the K/V loads in flight.
     using G = MfmaGeometry<D>;
-    constexpr int GT = kMfmaHeads;
+    constexpr int GT = kMfmaHeads * R;
     extern __shared__ int pre[];  // num_seqs + 1 tile prefixes
     __shared__ __attribute__((aligned(16))) char vtile[kMfmaWavesPerGroup][G::kLdsTile];
 
@@ -357,8 +376,8 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
     // A range inside one segment's start-up units holds no tile (only when
     // tpw <= seg_cost); the segment's tiles belong to the next wavefront.
     if (!next_piece<16>(p, lens, pre, cur, pc)) return;
-    u32x4 q[G::kQkSteps];
-    mfma_load_q<D>(p, pc, lane, q);
+    u32x4 q[R][G::kQkSteps];
+    mfma_load_q<D, R>(p, pc, lane, q);
     int ids = mfma_load_ids(p, tables, pc, 0, lane);
     MfmaTileRegs<D> ra, rb;
     int blk_a = __builtin_amdgcn_readlane(ids, 0);
@@ -383,11 +402,14 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
         const bool cached_n = has_next && pn.s < p.cached_seqs;
         const int *bt = tables + (size_t)pc.s * p.max_blocks;
 
-        MfmaState<D> st;
+        MfmaState<D> st[R];
 #pragma unroll
-        for (int n = 0; n < G::kDimBlocks; n++) st.o[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        st.m = -INFINITY;
-        st.l = 0.0f;
+        for (int b = 0; b < R; b++) {
+#pragma unroll
+            for (int n = 0; n < G::kDimBlocks; n++) st[b].o[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            st[b].m = -INFINITY;
+            st[b].l = 0.0f;
+        }
         const int ntiles = (pc.t_end - pc.t_begin + 15) >> 4;
         for (int i = 0; i < ntiles; i++) {
             if (i > 0 && (i & 63) == 0) ids = mfma_load_ids(p, tables, pc, i, lane);
@@ -405,50 +427,53 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
                               in_piece ? t0 + 16 : pn.t_begin,
                               in_piece ? pc.t_end : (has_next ? pn.t_end : 0), blk_b, lane,
                               in_piece ? cached : cached_n, rb);
-            mfma_tile<KV, D>(p, q, t0, pc.t_end, blk_a >= 0, lane, lds, ra, st);
+            mfma_tile<KV, D, R>(p, q, t0, pc.t_end, blk_a >= 0, lane, lds, ra, st);
             ra = rb;
             blk_a = blk_b;
         }
 
-        float l = st.l;
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
         const int g0 = pc.ht * GT;
         const int nh = min(GT, p.group - g0);
         const size_t qrow0 = ((size_t)pc.s * p.num_heads + (size_t)pc.kvh * p.group + g0) * D;
-        if (j < nh) {
+#pragma unroll
+        for (int b = 0; b < R; b++) {
+            float l = st[b].l;
+            l += __shfl_xor(l, 16);
+            l += __shfl_xor(l, 32);
+            const int hj = 16 * b + j;  // head of this lane in the tile
+            if (hj >= nh) continue;
             if (pc.whole && p.out_f32) {
                 const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-                float *dst = p.out_f32 + qrow0 + (size_t)j * D + 4 * gq;
+                float *dst = p.out_f32 + qrow0 + (size_t)hj * D + 4 * gq;
 #pragma unroll
-                for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st.o[n] * inv;
-                if (gq == 0) p.out_lse[qrow0 / D + j] = l > 0.0f ? st.m + log2f(l) : -INFINITY;
+                for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st[b].o[n] * inv;
+                if (gq == 0) p.out_lse[qrow0 / D + hj] = l > 0.0f ? st[b].m + log2f(l) : -INFINITY;
             } else if (pc.whole) {
                 const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-                char *dst = (char *)p.out + (qrow0 + (size_t)j * D + 4 * gq) * 2;
+                char *dst = (char *)p.out + (qrow0 + (size_t)hj * D + 4 * gq) * 2;
 #pragma unroll
                 for (int n = 0; n < G::kDimBlocks; n++) {
                     float f0, f1, f2, f3;
-                    const uint32_t b0 = round16<KV>(st.o[n][0] * inv, f0);
-                    const uint32_t b1 = round16<KV>(st.o[n][1] * inv, f1);
-                    const uint32_t b2 = round16<KV>(st.o[n][2] * inv, f2);
-                    const uint32_t b3 = round16<KV>(st.o[n][3] * inv, f3);
+                    const uint32_t b0 = round16<KV>(st[b].o[n][0] * inv, f0);
+                    const uint32_t b1 = round16<KV>(st[b].o[n][1] * inv, f1);
+                    const uint32_t b2 = round16<KV>(st[b].o[n][2] * inv, f2);
+                    const uint32_t b3 = round16<KV>(st[b].o[n][3] * inv, f3);
                     *(u32x2 *)(dst + 32 * n) = u32x2{b0 | (b1 << 16), b2 | (b3 << 16)};
                 }
             } else {
-                float *dst = p.ws_o + ((size_t)pc.slot * GT + j) * D + 4 * gq;
+                float *dst = p.ws_o + ((size_t)pc.slot * GT + hj) * D + 4 * gq;
 #pragma unroll
-                for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st.o[n];
+                for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st[b].o[n];
                 if (gq == 0) {
-                    p.ws_ml[((size_t)pc.slot * GT + j) * 2] = st.m;
-                    p.ws_ml[((size_t)pc.slot * GT + j) * 2 + 1] = l;
+                    p.ws_ml[((size_t)pc.slot * GT + hj) * 2] = st[b].m;
+                    p.ws_ml[((size_t)pc.slot * GT + hj) * 2 + 1] = l;
                 }
             }
         }
         if (!has_next) break;
         pc = pn;
         ids = ids_n;
-        mfma_load_q<D>(p, pc, lane, q);
+        mfma_load_q<D, R>(p, pc, lane, q);
     }
 }
 

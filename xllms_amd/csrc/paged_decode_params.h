@@ -30,7 +30,9 @@ enum KvType : int { KV_F16 = 1, KV_BF16 = 2, KV_F32 = 3 };
 constexpr int kWavesPerGroup = 4;    // VALU tile path: wavefronts per workgroup
 constexpr int kMfmaWavesPerGroup = 4;  // MFMA tile path
 constexpr int kMaxHeadTile = 8;      // query heads per wavefront, VALU tile path
-constexpr int kMfmaHeads = 16;       // query heads per wavefront, MFMA tile path
+constexpr int kMfmaHeads = 16;       // query heads per MFMA row block (R blocks per wavefront)
+constexpr int kMfmaWideMaxHeadSize = 128;  // largest head_size with R = 2
+constexpr int kMergeCols = 32;       // float4 columns per workgroup of the chunked merge
 constexpr int kLoadsPerTile = 4;     // 16-byte K (and V) loads per lane per tile
 constexpr int kMaxSeqsPerLaunch = 8192;  // the per-workgroup prefix scan lives in LDS
 

@@ -188,8 +188,8 @@ def paged_attention_cascade(out, query, key_cache, value_cache, block_tables, se
                             kv_block_stride: int | None = None, kv_head_stride: int | None = None,
                             kv_dtype: int | None = None, stream=None, check: bool = True) -> int:
     """Prefix-aware decode (nxt_paged_attention_cascade): same result as
-    paged_attention, reading each shared prefix page once per 16 rows of the
-    sequences that share it.  prefix_group: int32 [num_seqs] (-1 = none),
+    paged_attention, reading each shared prefix page once per 32 query rows
+    (16 for fp32 or head_size > 128) of the sequences that share it.  prefix_group: int32 [num_seqs] (-1 = none),
     prefix_blocks: int32 [max_groups] shared leading pages per group."""
     lib = _lib.backend()
     num_seqs, num_heads, head_size = query.shape
