@@ -55,22 +55,20 @@ static hipError_t launch_merge(const DecodeParams &p, hipStream_t st, hipEvent_t
     const unsigned segs = (unsigned)(p.num_seqs * p.num_kv_heads * p.head_tiles);
     const int heads = p.group < GT ? p.group : GT;
     if (p.merge_per_segment) {
-        // float4 columns per thread: the segment's heads * D/4 over 256
-        // threads, rounded up to a power of two (cols <= kMaxKc * 256, so the
-        // "1" alternatives below are never launched)
-        constexpr int kMaxKc = (GT * (D / 4) + kMergeSegThreads - 1) / kMergeSegThreads;
+        // one thread per float4 column of the segment (heads * D/4), at
+        // least 256; the wider instantiations exist only where a segment
+        // can have that many columns
+        constexpr int kMaxCols = GT * (D / 4);
+        constexpr int kNt512 = kMaxCols > 256 ? 512 : kMergeSegThreads;
+        constexpr int kNt1024 = kMaxCols > 512 ? 1024 : kMergeSegThreads;
         const int cols = heads * (D / 4);
         if (cols <= kMergeSegThreads)
-            paged_decode_merge_segment_kernel<KV, D, GT, TT, 1><<<segs, kMergeSegThreads, 0, st>>>(p);
-        else if (cols <= 2 * kMergeSegThreads)
-            paged_decode_merge_segment_kernel<KV, D, GT, TT, (kMaxKc > 1 ? 2 : 1)>
+            paged_decode_merge_segment_kernel<KV, D, GT, TT, kMergeSegThreads>
                 <<<segs, kMergeSegThreads, 0, st>>>(p);
-        else if (cols <= 4 * kMergeSegThreads)
-            paged_decode_merge_segment_kernel<KV, D, GT, TT, (kMaxKc > 2 ? 4 : 1)>
-                <<<segs, kMergeSegThreads, 0, st>>>(p);
+        else if (cols <= 512)
+            paged_decode_merge_segment_kernel<KV, D, GT, TT, kNt512><<<segs, kNt512, 0, st>>>(p);
         else
-            paged_decode_merge_segment_kernel<KV, D, GT, TT, (kMaxKc > 4 ? 8 : 1)>
-                <<<segs, kMergeSegThreads, 0, st>>>(p);
+            paged_decode_merge_segment_kernel<KV, D, GT, TT, kNt1024><<<segs, kNt1024, 0, st>>>(p);
         return hipGetLastError();
     }
     const unsigned chunks = (unsigned)((heads * (D / 4) + kMergeCols - 1) / kMergeCols);

@@ -748,18 +748,17 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
 
 // Merge kernel, one workgroup per segment: for batches with enough segments
 // to fill the GPU (where the (segment, chunk) grid above would launch several
-// thousand short workgroups, each costing ~2 ns of dispatch).  The 256
-// threads cover the segment's ncols float4 columns: with ncols >= 256 each
-// thread owns the KC columns t, t + 256, ... (KC = ceil(ncols / 256), a
-// power of two chosen at launch); with fewer, the S = 256 / pow2(ncols)
-// threads of a column split its partials (every S-th one) and combine in LDS.
-// Each thread runs the online log-sum-exp merge over its columns together,
-// a batch of partials' loads in flight at a time.
-constexpr int kMergeSegThreads = 256;
+// thousand short workgroups, each costing ~2 ns of dispatch).  NT threads
+// (256, 512 or 1024, chosen at launch as the segment's ncols float4 columns
+// rounded up to a power of two, at least 256) cover the columns, one each;
+// with fewer than 256 columns, the S = 256 / pow2(ncols) threads of a column
+// split its partials (every S-th one) and combine in LDS.  Each thread runs
+// the online log-sum-exp merge over its partials with a batch of their loads
+// in flight at a time.
+constexpr int kMergeSegThreads = 256;  // NT when ncols <= 256
 
-template <int KV, int D, int GT, int TT, int KC>
-__global__ __launch_bounds__(kMergeSegThreads) void paged_decode_merge_segment_kernel(
-    const DecodeParams p) {
+template <int KV, int D, int GT, int TT, int NT>
+__global__ __launch_bounds__(NT) void paged_decode_merge_segment_kernel(const DecodeParams p) {
     constexpr int C4 = D / 4;
     __shared__ f32x4 s_acc[kMergeSegThreads];
     __shared__ float s_m[kMergeSegThreads];
@@ -782,7 +781,7 @@ __global__ __launch_bounds__(kMergeSegThreads) void paged_decode_merge_segment_k
     const size_t qrow0 = ((size_t)s * p.num_heads + (size_t)kvh * p.group + g0) * D;
 
     if (L == 0) {
-        for (int col = tid; col < ncols; col += kMergeSegThreads) {
+        for (int col = tid; col < ncols; col += NT) {
             if (p.out_f32) {
                 *(f32x4 *)(p.out_f32 + qrow0 + (size_t)col * 4) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                 if (col % C4 == 0) p.out_lse[qrow0 / D + col / C4] = -INFINITY;
@@ -807,32 +806,20 @@ __global__ __launch_bounds__(kMergeSegThreads) void paged_decode_merge_segment_k
     const int slot0 = (w_first * tpw >= seg_start) ? 0 : 1;
     const size_t sbase = (size_t)w_first * 2;
 
-    // Column span per split: all 256 threads when ncols >= 256, else pow2(ncols).
-    int span = kMergeSegThreads;
+    // Column span per split: all NT threads when ncols > NT / 2, else pow2(ncols).
+    int span = NT;
     while ((span >> 1) >= ncols) span >>= 1;
-    const int split = tid / span;             // 0 .. S-1
-    const int nsplit = kMergeSegThreads / span;
+    const int split = tid / span;  // 0 .. S-1
+    const int nsplit = NT / span;
     const int cl = tid - split * span;
 
-    float m[KC], l[KC];
-    f32x4 acc[KC];
-    int off_ml[KC], off_o[KC];
-#pragma unroll
-    for (int k = 0; k < KC; k++) {
-        m[k] = -INFINITY;
-        l[k] = 0.0f;
-        acc[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        // a column past ncols (last head tile of a group) reads column cl
-        // again and is never stored
-        const int col = cl + k * kMergeSegThreads < ncols ? cl + k * kMergeSegThreads : cl;
-        const int h = col / C4;
-        off_ml[k] = h * 2;
-        off_o[k] = h * D + (col - h * C4) * 4;
-    }
+    float m[1] = {-INFINITY}, l[1] = {0.0f};
+    f32x4 acc[1] = {{0.0f, 0.0f, 0.0f, 0.0f}};
+    const int h = (cl < ncols ? cl : 0) / C4;
+    const int off_ml[1] = {h * 2}, off_o[1] = {h * D + ((cl < ncols ? cl : 0) - h * C4) * 4};
     if (cl < ncols)
-        merge_partials<GT, D, KC, (KC <= 2 ? 8 : 8 / KC)>(p, sbase, slot0, split, nsplit, np, off_ml,
-                                                     off_o, m, l, acc);
-    if (nsplit > 1) {  // KC == 1 here: ncols < 256
+        merge_partials<GT, D, 1, 8>(p, sbase, slot0, split, nsplit, np, off_ml, off_o, m, l, acc);
+    if (nsplit > 1) {  // NT == 256 here: ncols < 256
         s_acc[tid] = acc[0];
         s_m[tid] = m[0];
         s_l[tid] = l[0];
@@ -849,21 +836,17 @@ __global__ __launch_bounds__(kMergeSegThreads) void paged_decode_merge_segment_k
             m[0] = M;
         }
     }
-#pragma unroll
-    for (int k = 0; k < KC; k++) {
-        const int col = cl + k * kMergeSegThreads;
-        if (col >= ncols) continue;
-        const float inv = l[k] > 0.0f ? 1.0f / l[k] : 0.0f;
-        const size_t base = qrow0 + (size_t)col * 4;  // head-major columns
-        if (p.out_f32) {
-            *(f32x4 *)(p.out_f32 + base) = acc[k] * inv;
-            if (col % C4 == 0)
-                p.out_lse[qrow0 / D + col / C4] = l[k] > 0.0f ? m[k] + log2f(l[k]) : -INFINITY;
-            continue;
-        }
-#pragma unroll
-        for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, acc[k][e] * inv);
+    if (cl >= ncols) return;
+    const float inv = l[0] > 0.0f ? 1.0f / l[0] : 0.0f;
+    const size_t base = qrow0 + (size_t)cl * 4;  // head-major columns
+    if (p.out_f32) {
+        *(f32x4 *)(p.out_f32 + base) = acc[0] * inv;
+        if (cl % C4 == 0)
+            p.out_lse[qrow0 / D + cl / C4] = l[0] > 0.0f ? m[0] + log2f(l[0]) : -INFINITY;
+        return;
     }
+#pragma unroll
+    for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, acc[0][e] * inv);
 }
 
 }  // namespace xhip
