@@ -248,11 +248,19 @@ struct PartialOut {
     int cached_seqs;  // leading sequences whose K/V loads are cacheable
 };
 
+// Prefix fold of a pass (cascade suffix pass): DecodeParams::fold_row.
+struct PrefixFold {
+    const int *row;  // [num_seqs]
+    const float *out;
+    const float *lse;
+    int rows, kr;
+};
+
 int run(void *out, const void *query, const void *key_cache, const void *value_cache,
         const int *block_tables, const int *seq_lens, int num_seqs, int num_heads, int head_size,
         int num_kv_heads, float scale, int max_num_blocks_per_seq, int block_size, int dtype_size,
         int kv_block_stride, int kv_head_stride, nxt_stream_t stream_handle, int kv_dtype,
-        int partition_tokens, const PartialOut *po = nullptr) {
+        int partition_tokens, const PartialOut *po = nullptr, const PrefixFold *fold = nullptr) {
     // ---- argument checks (host only; nothing is read from the device)
     if (kv_dtype != NXT_KV_FP16 && kv_dtype != NXT_KV_BF16 && kv_dtype != NXT_KV_FP32)
         return set_status(NXT_ATTN_E_UNSUPPORTED, "kv_dtype %d is not FP16/BF16/FP32", kv_dtype);
@@ -368,6 +376,13 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
             p.out_f32 = po->out_f32 + (size_t)s0 * num_heads * head_size;
             p.out_lse = po->out_lse + (size_t)s0 * num_heads;
             p.cached_seqs = po->cached_seqs > s0 ? po->cached_seqs - s0 : 0;
+        }
+        if (fold) {
+            p.fold_row = fold->row + s0;
+            p.fold_out = fold->out;
+            p.fold_lse = fold->lse;
+            p.fold_rows = fold->rows;
+            p.fold_kr = fold->kr;
         }
         p.q = (const char *)query + row0;
         p.k = key_cache;
@@ -486,8 +501,7 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
                  o_vq = take((size_t)v_max * KR * head_size * eb),
                  o_sl = take(4 * (size_t)num_seqs), o_sb = take(4 * (size_t)num_seqs * mb),
                  o_po = take(4 * (size_t)v_max * KR * head_size), o_pl = take(4 * (size_t)v_max * KR),
-                 o_so = take(4 * (size_t)num_seqs * num_heads * head_size),
-                 o_sls = take(4 * (size_t)num_seqs * num_heads);
+                 o_pr = take(4 * (size_t)num_seqs);
     int device = 0;
     hipError_t e = hipGetDevice(&device);
     if (e != hipSuccess) return set_status(NXT_ATTN_E_HIP, "hipGetDevice: %s", hipGetErrorString(e));
@@ -529,12 +543,10 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
     c.v_q = w + o_vq;
     c.s_lens = (int *)(w + o_sl);
     c.s_bt = (int *)(w + o_sb);
-    c.p_out = (const float *)(w + o_po);
-    c.p_lse = (const float *)(w + o_pl);
-    c.s_out = (const float *)(w + o_so);
-    c.s_lse = (const float *)(w + o_sls);
+    c.p_row = (int *)(w + o_pr);
     // plan -> prefix pass (R gathered query rows per kv head, cacheable K/V:
-    // the rows of a group read the same pages) -> suffix pass -> combine
+    // the rows of a group read the same pages) -> suffix pass, whose members
+    // start from their prefix rows and which writes the output
     e = xhip::launch_cascade_plan(c, stream);
     if (e != hipSuccess)
         return set_status(NXT_ATTN_E_HIP, "cascade plan launch: %s", hipGetErrorString(e));
@@ -543,15 +555,11 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
              num_kv_heads * rows, head_size, num_kv_heads, scale, max_num_blocks_per_seq,
              block_size, eb, kv_block_stride, kv_head_stride, stream_handle, kv_dtype, 0, &pre);
     if (st != NXT_ATTN_OK) return st;
-    const PartialOut suf{(float *)(w + o_so), (float *)(w + o_sls), 0};
-    st = run(nullptr, query, key_cache, value_cache, c.s_bt, c.s_lens, num_seqs, num_heads,
-             head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size, eb,
-             kv_block_stride, kv_head_stride, stream_handle, kv_dtype, 0, &suf);
-    if (st != NXT_ATTN_OK) return st;
-    e = xhip::launch_cascade_combine(c, stream);
-    if (e != hipSuccess)
-        return set_status(NXT_ATTN_E_HIP, "cascade combine launch: %s", hipGetErrorString(e));
-    return ok();
+    const PrefixFold fold{c.p_row, (const float *)(w + o_po), (const float *)(w + o_pl), rows,
+                          (int)KR};
+    return run(out, query, key_cache, value_cache, c.s_bt, c.s_lens, num_seqs, num_heads,
+               head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size, eb,
+               kv_block_stride, kv_head_stride, stream_handle, kv_dtype, 0, nullptr, &fold);
 }
 
 // KV append (decode: block_tables + positions; prefill: slots).

@@ -1,7 +1,8 @@
-// Prefix-aware (cascade) decode: launch parameters and launchers of the plan,
-// detection and combine kernels (paged_decode_cascade.hip).  The attention
-// itself runs twice through the ordinary partition + merge kernels: once on
-// a prefix batch and once on a suffix batch that these kernels build.
+// Prefix-aware (cascade) decode: launch parameters and launchers of the plan
+// and detection kernels (paged_decode_cascade.hip).  The attention itself
+// runs twice through the ordinary partition + merge kernels: once on a prefix
+// batch, and once on a suffix batch that starts every member's segments from
+// its prefix result (DecodeParams::fold_row) and writes the output.
 #pragma once
 
 #include <hip/hip_runtime_api.h>
@@ -43,17 +44,13 @@ struct CascadeParams {
     void *v_q;                 // [v_max][num_kv_heads * rows][head_size]
     int *s_lens;               // [num_seqs] suffix lengths
     int *s_bt;                 // [num_seqs][max_blocks] suffix block tables
-    // pass outputs (fp32 + log-sum-exp in log2 units)
-    const float *p_out;        // [v_max][num_kv_heads * rows][head_size]
-    const float *p_lse;        // [v_max][num_kv_heads * rows]
-    const float *s_out;        // [num_seqs][num_heads][head_size]
-    const float *s_lse;        // [num_seqs][num_heads]
+    int *p_row;                // [num_seqs] fold base of each member: the row index, in
+                               // the group's prefix-batch rows laid end to end, of its
+                               // first query head (g_vbase * rows + rank * group); -1
 };
 
 // Plan: group membership and the prefix / suffix batches.
 hipError_t launch_cascade_plan(const CascadeParams &c, hipStream_t stream);
-// out = log-sum-exp merge of the prefix-batch and suffix-batch rows.
-hipError_t launch_cascade_combine(const CascadeParams &c, hipStream_t stream);
 
 // Detection of shared prefixes from the block tables (one workgroup,
 // num_seqs <= kCascadeMaxSeqs): sequences whose first page is the same

@@ -1,24 +1,26 @@
-// Prefix-aware (cascade) decode on gfx950: plan, combine and detection
-// kernels.  No counterpart in the reference (its decode reads every
-// sequence's pages, shared or not); see paged_decode_cascade.h.
+// Prefix-aware (cascade) decode on gfx950: plan and detection kernels.  No
+// counterpart in the reference (its decode reads every sequence's pages,
+// shared or not); see paged_decode_cascade.h.
 //
 // A group is a set of sequences whose first P pages are the same physical
 // pages.  Attention over a group's shared prefix is computed once per page
 // for all of its members: the plan gathers the members' query rows, R per kv
 // head, into the sequences of a prefix batch whose block table is the shared
 // prefix, and shifts every member's own block table past the prefix into a
-// suffix batch.  The ordinary partition + merge kernels run on both batches
-// in partial-output mode (fp32 rows plus their log-sum-exp; prefix pages
-// loaded cacheable, since the rows of a group read them close in time), and
-// the combine kernel merges the two rows of every (sequence, head):
-//   M = max(lse_p, lse_s), O = (2^(lse_p-M) O_p + 2^(lse_s-M) O_s) /
-//                              (2^(lse_p-M) + 2^(lse_s-M)).
-// (One run over both batches together was measured slower: every wavefront
-// then streams prefix and suffix tiles back to back at the slower per-tile
-// rate of the two.)  A row of the prefix batch depends only on its own query
-// (the MFMA tile computes every (token, row) score and every (dim, row)
-// output from that row alone), so where a member lands among the rows does
-// not change its result, and rows no member uses are never read.
+// suffix batch.  The ordinary partition + merge kernels run the prefix batch
+// in partial-output mode (fp32 rows plus their log-sum-exp lse_p; prefix
+// pages loaded cacheable, since the rows of a group read them close in
+// time), then the suffix batch with a prefix fold: (lse_p, O_p) is the
+// online softmax state (m = lse_p, l = 1, o = O_p), so a member's suffix
+// segments start from it and the suffix pass writes
+//   O = (2^(lse_p-m) O_p + sum_t 2^(s_t-m) v_t) / (2^(lse_p-m) + sum_t 2^(s_t-m)),
+// the attention over prefix and suffix together.  (One run over both
+// batches together was measured slower: every wavefront then streams prefix
+// and suffix tiles back to back at the slower per-tile rate of the two.)  A
+// row of the prefix batch depends only on its own query (the MFMA tile
+// computes every (token, row) score and every (dim, row) output from that
+// row alone), so where a member lands among the rows does not change its
+// result, and rows no member uses are never read.
 #include <hip/hip_runtime.h>
 #include <limits.h>
 #include <math.h>
@@ -163,51 +165,14 @@ __global__ __launch_bounds__(256) void cascade_plan_gather_kernel(const CascadeP
             const int s = (int)(k / c.max_blocks), b = (int)(k - (long long)s * c.max_blocks);
             int g;
             const int P = c.rank[s] >= 0 ? member_prefix(c, s, &g) : 0;
-            if (b == 0)
+            if (b == 0) {
                 c.s_lens[s] = P > 0 ? clamp_len(c.seq_lens[s], c.max_ctx) - P * c.block_size
                                     : c.seq_lens[s];
+                c.p_row[s] = P > 0 ? c.g_vbase[g] * c.rows + c.rank[s] * c.group : -1;
+            }
             c.s_bt[k] = b + P < c.max_blocks ? c.block_tables[(size_t)s * c.max_blocks + b + P]
                                               : -1;
         }
-    }
-}
-
-template <int KV>
-__global__ __launch_bounds__(256) void cascade_combine_kernel(const CascadeParams c) {
-    const int C4 = c.head_size / 4;
-    const long long n = (long long)c.num_seqs * c.num_heads * C4;
-    const long long stride = (long long)gridDim.x * blockDim.x;
-    const int R = c.rows;
-    const int KR = c.num_kv_heads * R;
-    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-        const int c4 = (int)(i % C4);
-        const long long row = i / C4;  // s * num_heads + head
-        const int s = (int)(row / c.num_heads);
-        const int head = (int)(row - (long long)s * c.num_heads);
-        const float ls = c.s_lse[row];
-        const f32x4 os = *(const f32x4 *)(c.s_out + row * c.head_size + 4 * c4);
-        float lp = -INFINITY;
-        f32x4 op = {0.0f, 0.0f, 0.0f, 0.0f};
-        const int r = c.rank[s];
-        if (r >= 0) {
-            const int g = c.prefix_group[s];
-            const int kvh = head / c.group, gq = head - kvh * c.group;
-            const int rig = r * c.group + gq;
-            const int v = c.g_vbase[g] + rig / R, j = rig % R;
-            const long long prow = (long long)v * KR + kvh * R + j;
-            lp = c.p_lse[prow];
-            op = *(const f32x4 *)(c.p_out + prow * c.head_size + 4 * c4);
-        }
-        const float M = fmaxf(ls, lp);
-        f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (M != -INFINITY) {
-            const float ws = ls == -INFINITY ? 0.0f : exp2f(ls - M);
-            const float wp = lp == -INFINITY ? 0.0f : exp2f(lp - M);
-            o = (os * ws + op * wp) * (1.0f / (ws + wp));
-        }
-        const size_t base = (size_t)row * c.head_size + 4 * c4;
-#pragma unroll
-        for (int e = 0; e < 4; e++) store_elem<KV>(c.out, base + e, o[e]);
     }
 }
 
@@ -316,16 +281,6 @@ hipError_t launch_cascade_plan(const CascadeParams &c, hipStream_t stream) {
                             (c.head_size * c.elem_bytes / 16) +
                         (long long)(c.v_max + c.num_seqs) * c.max_blocks;
     cascade_plan_gather_kernel<<<grid_for(n), 256, 0, stream>>>(c);
-    return hipGetLastError();
-}
-
-hipError_t launch_cascade_combine(const CascadeParams &c, hipStream_t stream) {
-    const unsigned grid = grid_for((long long)c.num_seqs * c.num_heads * (c.head_size / 4));
-    switch (c.kv_dtype) {
-    case KV_F16: cascade_combine_kernel<KV_F16><<<grid, 256, 0, stream>>>(c); break;
-    case KV_BF16: cascade_combine_kernel<KV_BF16><<<grid, 256, 0, stream>>>(c); break;
-    default: cascade_combine_kernel<KV_F32><<<grid, 256, 0, stream>>>(c); break;
-    }
     return hipGetLastError();
 }
 

@@ -372,6 +372,14 @@ __device__ __forceinline__ int tiles_per_wave(int total, int num_waves, int min_
     return t > min_tpw ? t : min_tpw;
 }
 
+// Row of the prefix-fold state of (a sequence's fold base, kv head, query
+// head g of the group); see DecodeParams::fold_row.
+__device__ __forceinline__ size_t fold_state_row(const DecodeParams &p, int base, int kvh, int g) {
+    const int q = base + g;
+    const int v = q / p.fold_rows;
+    return (size_t)v * p.fold_kr + (size_t)kvh * p.fold_rows + (size_t)(q - v * p.fold_rows);
+}
+
 // Split units of a segment of Ts tiles (paged_decode_params.h): its tiles
 // plus the start-up cost; an empty segment costs nothing.
 __device__ __forceinline__ int segment_units(const DecodeParams &p, int Ts) {
@@ -514,6 +522,22 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
 #pragma unroll
             for (int e = 0; e < VEC; e++) st.o[h][e] = 0.0f;
         }
+        if (p.fold_row && t_begin == 0 && row == 0) {  // row 0 lanes carry the prefix state
+            const int base = p.fold_row[s];
+            if (base >= 0) {
+#pragma unroll
+                for (int h = 0; h < GT; h++) {
+                    if (h >= nh) continue;
+                    const size_t r = fold_state_row(p, base, kvh, g0 + h);
+                    st.m[h] = p.fold_lse[r];
+                    st.l[h] = 1.0f;
+                    if (col_ok) {
+#pragma unroll
+                        for (int e = 0; e < VEC; e++) st.o[h][e] = p.fold_out[r * D + col * VEC + e];
+                    }
+                }
+            }
+        }
         const int *bt = p.block_tables + (size_t)s * p.max_blocks;
         const char *kb = (const char *)p.k + (size_t)kvh * (size_t)p.kv_head_stride * EB;
         const char *vb = (const char *)p.v + (size_t)kvh * (size_t)p.kv_head_stride * EB;
@@ -641,6 +665,31 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p, size_t sba
     }
 }
 
+// Output float4 column `col` (head col / (D/4), head-major) of an empty
+// sequence s: zeros (log-sum-exp -inf), or the prefix row under a prefix
+// fold (the sequence's whole context was the shared prefix).
+template <int KV, int D>
+__device__ __forceinline__ void write_empty_column(const DecodeParams &p, int s, int kvh, int g0,
+                                                   size_t qrow0, int col) {
+    constexpr int C4 = D / 4;
+    const size_t base = qrow0 + (size_t)col * 4;
+    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+    float lse = -INFINITY;
+    const int fb = p.fold_row ? p.fold_row[s] : -1;
+    if (fb >= 0) {
+        const size_t r = fold_state_row(p, fb, kvh, g0 + col / C4);
+        o = *(const f32x4 *)(p.fold_out + r * D + (col % C4) * 4);
+        lse = p.fold_lse[r];
+    }
+    if (p.out_f32) {
+        *(f32x4 *)(p.out_f32 + base) = o;
+        if (col % C4 == 0) p.out_lse[qrow0 / D + col / C4] = lse;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, o[e]);
+    }
+}
+
 // Merge kernel: one workgroup per (segment, chunk of kMergeCols output
 // float4 columns), where a segment is (sequence, kv head, head tile) and the
 // columns run over (head h < nh, dims 4c..4c+3).  It writes zeros for an
@@ -681,16 +730,8 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
     const size_t qrow0 = ((size_t)s * p.num_heads + (size_t)kvh * p.group + g0) * D;
 
     if (L == 0) {
-        if (tid < kMergeCols && col0 + tid < ncols) {
-            const size_t base = qrow0 + (size_t)(col0 + tid) * 4;  // head-major columns
-            if (p.out_f32) {
-                *(f32x4 *)(p.out_f32 + base) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                if ((col0 + tid) % C4 == 0) p.out_lse[qrow0 / D + (col0 + tid) / C4] = -INFINITY;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, 0.0f);
-            }
-        }
+        if (tid < kMergeCols && col0 + tid < ncols)
+            write_empty_column<KV, D>(p, s, kvh, g0, qrow0, col0 + tid);
         return;
     }
     const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);
@@ -781,16 +822,7 @@ __global__ __launch_bounds__(NT) void paged_decode_merge_segment_kernel(const De
     const size_t qrow0 = ((size_t)s * p.num_heads + (size_t)kvh * p.group + g0) * D;
 
     if (L == 0) {
-        for (int col = tid; col < ncols; col += NT) {
-            if (p.out_f32) {
-                *(f32x4 *)(p.out_f32 + qrow0 + (size_t)col * 4) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                if (col % C4 == 0) p.out_lse[qrow0 / D + col / C4] = -INFINITY;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    store_elem<KV>(p.out, qrow0 + (size_t)col * 4 + e, 0.0f);
-            }
-        }
+        for (int col = tid; col < ncols; col += NT) write_empty_column<KV, D>(p, s, kvh, g0, qrow0, col);
         return;
     }
     const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);

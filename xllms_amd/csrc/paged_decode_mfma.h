@@ -307,6 +307,52 @@ __device__ __forceinline__ void mfma_load_q(const DecodeParams &p, const MfmaPie
                           : u32x4{0, 0, 0, 0};
 }
 
+// Prefix fold (DecodeParams::fold_row) of a piece that starts its segment:
+// the prefix pass's result for each head, (m = lse, l = 1, O^T = the
+// normalized prefix row), is merged into the piece's state after its last
+// tile, like one more partial.  Its loads are issued when the piece begins
+// (R = 1), so their latency hides behind the piece's tiles; with R = 2 the 32
+// extra registers would not fit, and they are loaded at the end.
+template <int D, int R> struct MfmaFold {
+    f32x4 o[R][MfmaGeometry<D>::kDimBlocks];
+    float m[R];
+    int base;  // the sequence's fold base, < 0: no fold
+};
+
+template <int D, int R>
+__device__ __forceinline__ void mfma_fold_load(const DecodeParams &p, const MfmaPiece &pc,
+                                               int lane, MfmaFold<D, R> &f) {
+    const int j = lane & 15, g = lane >> 4;
+    const int g0 = pc.ht * kMfmaHeads * R;
+    const int nh = min(kMfmaHeads * R, p.group - g0);
+#pragma unroll
+    for (int b = 0; b < R; b++) {
+        // heads past the group read head g0 (valid) and are never written
+        const size_t r = fold_state_row(p, f.base, pc.kvh, g0 + (16 * b + j < nh ? 16 * b + j : 0));
+        f.m[b] = p.fold_lse[r];
+#pragma unroll
+        for (int n = 0; n < MfmaGeometry<D>::kDimBlocks; n++)
+            f.o[b][n] = *(const f32x4 *)(p.fold_out + r * D + 16 * n + 4 * g);
+    }
+}
+
+template <int D, int R>
+__device__ __forceinline__ void mfma_fold_apply(const MfmaFold<D, R> &f, int lane,
+                                                MfmaState<D> (&st)[R]) {
+    const int g = lane >> 4;
+#pragma unroll
+    for (int b = 0; b < R; b++) {
+        const float M = fmaxf(st[b].m, f.m[b]);
+        const float Ms = (M == -INFINITY) ? 0.0f : M;
+        const float a = fast_exp2(st[b].m - Ms), w = fast_exp2(f.m[b] - Ms);
+        st[b].l = st[b].l * a + (g == 0 ? w : 0.0f);  // l is summed over the 4 lane groups
+#pragma unroll
+        for (int n = 0; n < MfmaGeometry<D>::kDimBlocks; n++)
+            st[b].o[n] = st[b].o[n] * a + f.o[b][n] * w;
+        st[b].m = M;
+    }
+}
+
 // Block ids of the piece's tiles first .. first+63, lane i holding tile
 // first+i (clamped to the piece's last tile).
 __device__ __forceinline__ int mfma_load_ids(const DecodeParams &p, const int *__restrict__ tables,
@@ -379,6 +425,8 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
     u32x4 q[R][G::kQkSteps];
     mfma_load_q<D, R>(p, pc, lane, q);
     int ids = mfma_load_ids(p, tables, pc, 0, lane);
+    // fold base of the current piece (requested a piece ahead from here on)
+    int fold_base = (p.fold_row && pc.t_begin == 0) ? p.fold_row[pc.s] : -1;
     MfmaTileRegs<D> ra, rb;
     int blk_a = __builtin_amdgcn_readlane(ids, 0);
     {
@@ -394,6 +442,7 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
         // current one again), so every path through the loop below has the
         // same loads in flight and the compiler's wait counts stay exact.
         const int ids_n = mfma_load_ids(p, tables, pn, 0, lane);
+        const int fold_base_n = (p.fold_row && has_next && pn.t_begin == 0) ? p.fold_row[pn.s] : -1;
         const char *kb = (const char *)p.k + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
         const char *vb = (const char *)p.v + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
         const char *kb_n = (const char *)p.k + (size_t)pn.kvh * (size_t)p.kv_head_stride * 2;
@@ -410,6 +459,9 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
             st[b].m = -INFINITY;
             st[b].l = 0.0f;
         }
+        MfmaFold<D, R> fold;
+        fold.base = fold_base;
+        if (R == 1 && fold.base >= 0) mfma_fold_load<D, R>(p, pc, lane, fold);
         const int ntiles = (pc.t_end - pc.t_begin + 15) >> 4;
         for (int i = 0; i < ntiles; i++) {
             if (i > 0 && (i & 63) == 0) ids = mfma_load_ids(p, tables, pc, i, lane);
@@ -432,6 +484,10 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
             blk_a = blk_b;
         }
 
+        if (fold.base >= 0) {
+            if (R != 1) mfma_fold_load<D, R>(p, pc, lane, fold);
+            mfma_fold_apply<D, R>(fold, lane, st);
+        }
         const int g0 = pc.ht * GT;
         const int nh = min(GT, p.group - g0);
         const size_t qrow0 = ((size_t)pc.s * p.num_heads + (size_t)pc.kvh * p.group + g0) * D;
@@ -473,6 +529,7 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
         if (!has_next) break;
         pc = pn;
         ids = ids_n;
+        fold_base = fold_base_n;
         mfma_load_q<D, R>(p, pc, lane, q);
     }
 }

@@ -70,6 +70,21 @@ struct DecodeParams {
     float *out_lse;
     int cached_seqs;           // sequences [0, cached_seqs) load K/V cacheable (pages read
                                // by several wavefronts close in time); the rest nontemporal
+    // Prefix fold (cascade suffix pass): when fold_row is set, sequence s
+    // with fold_row[s] >= 0 continues the attention of an earlier pass over
+    // its shared prefix.  That pass left, for (kv head h, query head g of
+    // the group), the normalized row fold_out[r * head_size ..] and its
+    // log-sum-exp fold_lse[r] (log2 units) at r = v * fold_kr + h * fold_rows
+    // + j with v, j = divmod(fold_row[s] + g, fold_rows).  Such a state is
+    // the online softmax's (m = lse, l = 1, o = row): the piece that starts a
+    // segment (token 0) begins from it instead of the empty state, and an
+    // empty sequence outputs the prefix row.
+    const int *fold_row;
+    const float *fold_out;
+    const float *fold_lse;
+    int fold_rows;
+    int fold_kr;
 };
+
 
 }  // namespace xhip
