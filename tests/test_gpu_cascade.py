@@ -121,6 +121,21 @@ def test_cascade_without_groups_is_the_plain_decode(cuda):
     assert_close(got, O.run_workload(wl, precision="mt"), wl.kv_dtype, "no groups")
 
 
+def test_cascade_plan_beyond_the_lds_limits(cuda):
+    """More than 1024 groups: the plan runs its global-memory kernel instead
+    of the LDS one (same results); with fewer, the LDS kernel."""
+    rng = np.random.default_rng(14)
+    spec = [(1 + int(rng.integers(0, 3)), [int(x) for x in rng.integers(0, 40, size=2)])
+            for _ in range(1100)]
+    wl, pg, pb = shared_case(spec, singles=[7, 0, 90], H=8, KVH=2, D=64, seed=14)
+    print(f"case seqs={wl.num_seqs} groups={len(pb)}", flush=True)
+    ref = O.run_workload(wl, precision="mt")
+    assert_close(run_cascade(wl, pg, pb), ref, wl.kv_dtype, "cascade, 1100 groups")
+    # the same batch with only the first 1000 groups shared (LDS plan)
+    pg2 = np.where(pg < 1000, pg, -1).astype(np.int32)
+    assert_close(run_cascade(wl, pg2, pb[:1000]), ref, wl.kv_dtype, "cascade, 1000 groups")
+
+
 def test_cascade_repeated_calls_reuse_the_plan_workspace(cuda):
     """Back-to-back cascade calls of different shapes on one stream."""
     cases = [shared_case([(4, [9, 2, 30])], singles=[5], seed=11),

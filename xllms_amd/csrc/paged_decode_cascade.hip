@@ -120,6 +120,62 @@ __global__ __launch_bounds__(kPlanThreads) void cascade_plan_meta_kernel(const C
     for (int v = vt + tid; v < c.v_max; v += kPlanThreads) c.v_group[v] = -1;
 }
 
+// Plan, part 1 with the work arrays in LDS (batches of up to kPlanLdsSeqs
+// sequences and kPlanLdsGroups groups): the same results as
+// cascade_plan_meta_kernel, which keeps them in global memory and so waits
+// for a global round trip at each of its ~10 steps.  Here the inputs are read
+// once and the results stored at the end.
+constexpr int kPlanLdsGroups = 1024;
+constexpr int kPlanLdsSeqs = 4096;
+
+__global__ __launch_bounds__(kPlanThreads) void cascade_plan_meta_lds_kernel(const CascadeParams c) {
+    __shared__ int part[kPlanThreads];
+    __shared__ int l_count[kPlanLdsGroups], l_first[kPlanLdsGroups];
+    __shared__ int l_vbase[kPlanLdsGroups], l_moff[kPlanLdsGroups];
+    __shared__ int l_group[kPlanLdsSeqs], l_rank[kPlanLdsSeqs];
+    const int tid = threadIdx.x;
+    const int B = c.num_seqs, NG = c.max_groups;
+    for (int g = tid; g < NG; g += kPlanThreads) {
+        l_count[g] = 0;
+        l_first[g] = INT_MAX;
+    }
+    __syncthreads();
+    for (int s = tid; s < B; s += kPlanThreads) {
+        int g;
+        member_prefix(c, s, &g);
+        int r = -1;
+        if (g >= 0) {
+            r = atomicAdd(&l_count[g], 1);
+            atomicMin(&l_first[g], s);
+        }
+        l_group[s] = g;
+        l_rank[s] = r;
+        c.rank[s] = r;
+    }
+    __syncthreads();
+    // prefix sequences of every group: ceil(members * group / rows)
+    for (int g = tid; g < NG; g += kPlanThreads) {
+        l_vbase[g] = (l_count[g] * c.group + c.rows - 1) / c.rows;
+        l_moff[g] = l_count[g];
+    }
+    __syncthreads();
+    const int vt = block_exclusive_scan(l_vbase, NG, part);
+    block_exclusive_scan(l_moff, NG, part);
+    for (int g = tid; g < NG; g += kPlanThreads) {
+        c.g_count[g] = l_count[g];
+        c.g_first[g] = l_first[g];
+        c.g_vbase[g] = l_vbase[g];
+        c.g_moff[g] = l_moff[g];
+        const int n = (l_count[g] * c.group + c.rows - 1) / c.rows;
+        for (int k = 0; k < n; k++) c.v_group[l_vbase[g] + k] = g;
+    }
+    for (int s = tid; s < B; s += kPlanThreads) {
+        const int r = l_rank[s];
+        if (r >= 0) c.member_seq[l_moff[l_group[s]] + r] = s;
+    }
+    for (int v = vt + tid; v < c.v_max; v += kPlanThreads) c.v_group[v] = -1;
+}
+
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // Plan, part 2 (grid-stride): the prefix batch (gathered query rows, block
@@ -274,7 +330,10 @@ unsigned grid_for(long long n) {
 }  // namespace
 
 hipError_t launch_cascade_plan(const CascadeParams &c, hipStream_t stream) {
-    cascade_plan_meta_kernel<<<1, kPlanThreads, 0, stream>>>(c);
+    if (c.max_groups <= kPlanLdsGroups && c.num_seqs <= kPlanLdsSeqs)
+        cascade_plan_meta_lds_kernel<<<1, kPlanThreads, 0, stream>>>(c);
+    else
+        cascade_plan_meta_kernel<<<1, kPlanThreads, 0, stream>>>(c);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const long long n = (long long)c.v_max * c.num_kv_heads * c.rows *
