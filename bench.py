@@ -12,9 +12,9 @@ one.
 Prints ONE JSON line:
   value        seqs/s = num_seqs / (GPU time per step), whole job on 1 GPU
   roofline     algorithmic bytes of one launch / average duration of the
-               partition kernel (HIP events on its stream around each launch,
-               over K further steps: the events are kept out of the K timed
-               steps that give `value`), against 8 TB/s;
+               partition kernel (HIP events stamped with each launch's start
+               and end on its stream, over K further steps kept apart from the
+               K timed steps that give `value`), against 8 TB/s;
                `traffic` = HBM bytes per launch from the committed rocprofv3
                PMC summary for this workload (profiles/), else null
   cpu_baseline the oracle (C restatement of the reference CPU attention)
@@ -551,9 +551,9 @@ def main() -> int:
         raise RuntimeError(f"launch failed: {msg}")
     total_ms = ev.elapsed_ms(begin, end)
     # The partition kernel's launch durations: K more steps of the same
-    # calls, the library recording an event on the stream before and after
-    # each partition launch.  Kept out of the timed steps: the two extra
-    # event packets per step lengthen it by ~5 us on MI355X.
+    # calls, the library stamping two events with each partition kernel's
+    # start and end (hipExtLaunchKernel, on the stream it runs on).  Kept out
+    # of the timed steps, which carry no instrumentation.
     if args.cascade:
         kern_ms = np.array([total_ms / args.steps])
     else:

@@ -129,10 +129,11 @@ int nxt_attn_last_status(void);
 const char *nxt_attn_last_error(void);
 
 /* Profiling hook: when set, every later launch from the calling thread
- * records `start_event` on its stream just before the partition kernel and
- * `partition_done_event` right after it (hipEvent_t handles owned by the
- * caller), so the partition kernel can be timed on the stream it runs on.
- * NULL, NULL clears the hook.  Meant for benchmarks and tracing. */
+ * stamps `start_event` and `partition_done_event` (hipEvent_t handles owned
+ * by the caller) with the start and the end of its partition kernel, on the
+ * stream it runs on (hipExtLaunchKernel's kernel events), so the kernel can
+ * be timed without event packets queued around it.  NULL, NULL clears the
+ * hook.  Meant for benchmarks and tracing. */
 void nxt_attn_set_trace_events(void *start_event, void *partition_done_event);
 
 /* Waits for and frees every cached split-K workspace of this process. */

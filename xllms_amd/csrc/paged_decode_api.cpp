@@ -420,23 +420,18 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
             ((long long)nseq * segs >= 2LL * cus || (long long)nseq * segs * chunks > 4LL * cus) ? 1
                                                                                                 : 0;
 
-        if (t_trace_start) {
-            e = hipEventRecord(t_trace_start, stream);
-            if (e != hipSuccess)
-                return set_status(NXT_ATTN_E_HIP, "hipEventRecord: %s", hipGetErrorString(e));
-        }
         switch (kv_dtype) {
         case NXT_KV_FP16:
             e = xhip::launch_decode_f16(p, head_size, tiling.head_tile, mfma, stream,
-                                        t_trace_partition);
+                                        t_trace_start, t_trace_partition);
             break;
         case NXT_KV_BF16:
             e = xhip::launch_decode_bf16(p, head_size, tiling.head_tile, mfma, stream,
-                                         t_trace_partition);
+                                         t_trace_start, t_trace_partition);
             break;
         default:
             e = xhip::launch_decode_f32(p, head_size, tiling.head_tile, mfma, stream,
-                                        t_trace_partition);
+                                        t_trace_start, t_trace_partition);
             break;
         }
         if (e != hipSuccess)

@@ -8,8 +8,8 @@ int partition_occupancy_bf16(int head_size, int head_tile, bool mfma, size_t lds
 }
 
 hipError_t launch_decode_bf16(const DecodeParams &p, int head_size, int head_tile, bool mfma,
-                             hipStream_t stream, hipEvent_t after_partition) {
-    return launch_for_dtype<KV_BF16>(p, head_size, head_tile, mfma, stream, after_partition);
+                             hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
+    return launch_for_dtype<KV_BF16>(p, head_size, head_tile, mfma, stream, ev_start, ev_stop);
 }
 
 }  // namespace xhip

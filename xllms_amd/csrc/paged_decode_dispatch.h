@@ -3,6 +3,8 @@
 // multiples of 32; the VALU path covers every supported shape.
 #pragma once
 
+#include <hip/hip_ext.h>
+
 #include "paged_decode_kernels.h"
 #include "paged_decode_launch.h"
 #include "paged_decode_mfma.h"
@@ -46,12 +48,24 @@ static const void *partition_fn(int head_tile, bool mfma) {
     return valu_fn<KV, D>(head_tile);
 }
 
+// A partition kernel launch.  With trace events it goes through
+// hipExtLaunchKernelGGL, which stamps them from the kernel's own dispatch
+// (its start and its end), not from event packets queued around it, whose
+// latency made the kernel read 2-6 us longer than rocprof's trace.
+template <typename F, typename... Args>
+static hipError_t launch_partition(F kernel, unsigned grid, unsigned block, size_t lds,
+                                   hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop,
+                                   Args... args) {
+    if (ev_start || ev_stop)
+        hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(block), (std::uint32_t)lds, st, ev_start,
+                              ev_stop, 0u, args...);
+    else
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(block), lds, st, args...);
+    return hipGetLastError();
+}
+
 template <int KV, int D, int GT, int TT>
-static hipError_t launch_merge(const DecodeParams &p, hipStream_t st, hipEvent_t after_partition) {
-    if (after_partition) {
-        const hipError_t e = hipEventRecord(after_partition, st);
-        if (e != hipSuccess) return e;
-    }
+static hipError_t launch_merge(const DecodeParams &p, hipStream_t st) {
     const unsigned segs = (unsigned)(p.num_seqs * p.num_kv_heads * p.head_tiles);
     const int heads = p.group < GT ? p.group : GT;
     if (p.merge_per_segment) {
@@ -79,45 +93,58 @@ static hipError_t launch_merge(const DecodeParams &p, hipStream_t st, hipEvent_t
 
 template <int KV, int D>
 static hipError_t launch_for_head_size(const DecodeParams &p, int head_tile, bool mfma,
-                                       hipStream_t st, hipEvent_t after_partition) {
+                                       hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
     constexpr int TT = Geometry<KV, D>::kTileTokens;
     const unsigned grid = (unsigned)(p.num_waves / kWavesPerGroup);
-    const dim3 block(64 * kWavesPerGroup);
     const size_t lds = (size_t)(p.num_seqs + 1) * sizeof(int);
     if (mfma) {
         if constexpr (has_mfma<KV, D>()) {
             const unsigned mgrid = (unsigned)(p.num_waves / kMfmaWavesPerGroup);
             if (head_tile == kMfmaHeads) {
-                paged_decode_partition_mfma_kernel<KV, D, 1>
-                    <<<mgrid, 64 * kMfmaWavesPerGroup, lds, st>>>(p, p.seq_lens, p.block_tables);
-                return launch_merge<KV, D, kMfmaHeads, MfmaGeometry<D>::kTile>(p, st,
-                                                                              after_partition);
+                const hipError_t e = launch_partition(
+                    paged_decode_partition_mfma_kernel<KV, D, 1>, mgrid, 64 * kMfmaWavesPerGroup,
+                    lds, st, ev_start, ev_stop, p, p.seq_lens, p.block_tables);
+                if (e != hipSuccess) return e;
+                return launch_merge<KV, D, kMfmaHeads, MfmaGeometry<D>::kTile>(p, st);
             }
             if constexpr (has_mfma_wide<KV, D>()) {
                 if (head_tile == 2 * kMfmaHeads) {
-                    paged_decode_partition_mfma_kernel<KV, D, 2>
-                        <<<mgrid, 64 * kMfmaWavesPerGroup, lds, st>>>(p, p.seq_lens,
-                                                                      p.block_tables);
-                    return launch_merge<KV, D, 2 * kMfmaHeads, MfmaGeometry<D>::kTile>(
-                        p, st, after_partition);
+                    const hipError_t e = launch_partition(
+                        paged_decode_partition_mfma_kernel<KV, D, 2>, mgrid,
+                        64 * kMfmaWavesPerGroup, lds, st, ev_start, ev_stop, p, p.seq_lens,
+                        p.block_tables);
+                    if (e != hipSuccess) return e;
+                    return launch_merge<KV, D, 2 * kMfmaHeads, MfmaGeometry<D>::kTile>(p, st);
                 }
             }
         }
         return hipErrorInvalidValue;
     }
     switch (head_tile) {
-    case 1:
-        paged_decode_partition_kernel<KV, D, 1><<<grid, block, lds, st>>>(p);
-        return launch_merge<KV, D, 1, TT>(p, st, after_partition);
-    case 2:
-        paged_decode_partition_kernel<KV, D, 2><<<grid, block, lds, st>>>(p);
-        return launch_merge<KV, D, 2, TT>(p, st, after_partition);
-    case 4:
-        paged_decode_partition_kernel<KV, D, 4><<<grid, block, lds, st>>>(p);
-        return launch_merge<KV, D, 4, TT>(p, st, after_partition);
-    case 8:
-        paged_decode_partition_kernel<KV, D, 8><<<grid, block, lds, st>>>(p);
-        return launch_merge<KV, D, 8, TT>(p, st, after_partition);
+    case 1: {
+        const hipError_t e = launch_partition(paged_decode_partition_kernel<KV, D, 1>, grid,
+                                              64 * kWavesPerGroup, lds, st, ev_start, ev_stop, p);
+        if (e != hipSuccess) return e;
+        return launch_merge<KV, D, 1, TT>(p, st);
+    }
+    case 2: {
+        const hipError_t e = launch_partition(paged_decode_partition_kernel<KV, D, 2>, grid,
+                                              64 * kWavesPerGroup, lds, st, ev_start, ev_stop, p);
+        if (e != hipSuccess) return e;
+        return launch_merge<KV, D, 2, TT>(p, st);
+    }
+    case 4: {
+        const hipError_t e = launch_partition(paged_decode_partition_kernel<KV, D, 4>, grid,
+                                              64 * kWavesPerGroup, lds, st, ev_start, ev_stop, p);
+        if (e != hipSuccess) return e;
+        return launch_merge<KV, D, 4, TT>(p, st);
+    }
+    case 8: {
+        const hipError_t e = launch_partition(paged_decode_partition_kernel<KV, D, 8>, grid,
+                                              64 * kWavesPerGroup, lds, st, ev_start, ev_stop, p);
+        if (e != hipSuccess) return e;
+        return launch_merge<KV, D, 8, TT>(p, st);
+    }
     default: return hipErrorInvalidValue;
     }
 }
@@ -148,10 +175,10 @@ static int occupancy_for_dtype(int head_size, int head_tile, bool mfma, size_t l
 
 template <int KV>
 static hipError_t launch_for_dtype(const DecodeParams &p, int head_size, int head_tile, bool mfma,
-                                   hipStream_t st, hipEvent_t after_partition) {
+                                   hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
     switch (head_size) {
 #define XHIP_CASE(d) \
-    case d: return launch_for_head_size<KV, d>(p, head_tile, mfma, st, after_partition);
+    case d: return launch_for_head_size<KV, d>(p, head_tile, mfma, st, ev_start, ev_stop);
         XHIP_FOR_HEAD_SIZES(XHIP_CASE)
 #undef XHIP_CASE
     default: return hipErrorInvalidValue;

@@ -19,15 +19,15 @@ int partition_occupancy_f32(int head_size, int head_tile, bool mfma, size_t lds_
 
 // Launches the partition kernel on num_waves / (wavefronts per workgroup)
 // workgroups, then the merge kernel over every (sequence, kv head, head
-// tile).  A non-null
-// `after_partition` event is recorded on the stream between the two.
-// Returns hipErrorInvalidValue for a head_size / head_tile with no
-// instantiation, else the launch status.
+// tile).  Non-null `ev_start` / `ev_stop` events are stamped with the
+// partition kernel's start and end (hipExtLaunchKernel).  Returns
+// hipErrorInvalidValue for a head_size / head_tile with no instantiation,
+// else the launch status.
 hipError_t launch_decode_f16(const DecodeParams &p, int head_size, int head_tile, bool mfma,
-                             hipStream_t stream, hipEvent_t after_partition);
+                             hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
 hipError_t launch_decode_bf16(const DecodeParams &p, int head_size, int head_tile, bool mfma,
-                              hipStream_t stream, hipEvent_t after_partition);
+                              hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
 hipError_t launch_decode_f32(const DecodeParams &p, int head_size, int head_tile, bool mfma,
-                             hipStream_t stream, hipEvent_t after_partition);
+                             hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
 
 }  // namespace xhip
