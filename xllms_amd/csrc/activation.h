@@ -6,6 +6,8 @@
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
 
+#include "fast_div.h"
+
 namespace xhip {
 
 // Same values as NxtActivationOp in include/xllm_hip_operator_api.h.
@@ -20,29 +22,6 @@ enum ActOp : int {
 
 // constexpr functions are callable from host and device code alike.
 constexpr bool act_is_gated(int op) { return op >= ACT_SILU_AND_MUL && op <= ACT_GELU_TANH_AND_MUL; }
-
-// Unsigned 32-bit division by a run-time constant through a multiply-high
-// (Granlund & Montgomery, "Division by invariant integers using
-// multiplication", PLDI 1994, the round-up variant): for every n < 2^32,
-//   n / d == (umulhi(n, mul) + n) >> shift, the sum taken in 64 bits,
-// with shift = ceil(log2 d) and mul = floor(2^32 (2^shift - d) / d) + 1.
-struct DivMagic {
-    uint32_t mul;
-    uint32_t shift;
-    uint32_t d;
-};
-
-constexpr DivMagic div_magic(uint32_t d) {
-    uint32_t shift = 0;
-    while (shift < 32 && (1ull << shift) < d) shift++;
-    const uint64_t mul = (((1ull << 32) * ((1ull << shift) - d)) / d) + 1;
-    return DivMagic{(uint32_t)mul, shift, d};
-}
-
-constexpr uint32_t div_by(uint32_t n, const DivMagic &m) {
-    const uint32_t hi = (uint32_t)(((uint64_t)n * m.mul) >> 32);
-    return (uint32_t)(((uint64_t)hi + n) >> m.shift);
-}
 
 struct ActivationParams {
     void *out;              // [num_tokens][d]

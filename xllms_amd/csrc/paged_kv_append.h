@@ -4,6 +4,8 @@
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
 
+#include "fast_div.h"
+
 namespace xhip {
 
 struct KvAppendParams {
@@ -28,6 +30,11 @@ struct KvAppendParams {
     int bs_shift;
     int max_blocks;
     int max_ctx;               // max_blocks * block_size
+    // set by launch_kv_append for each of its launches:
+    int tok0;                  // first token of the launch
+    uint32_t chunks;           // 16-byte chunks of K (and of V) in the launch
+    DivMagic row_div;          // division by row_chunks
+    DivMagic head_div;         // division by num_kv_heads
 };
 
 hipError_t launch_kv_append(const KvAppendParams &p, hipStream_t stream);

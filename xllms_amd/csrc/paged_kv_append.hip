@@ -12,9 +12,13 @@
 // slot per token) or from `block_tables` + `positions` (decode: token s of
 // sequence s at position positions[s]).  A negative slot, position or page
 // id skips the token.  In copy mode (`src_slots`) the rows come from another
-// slot of the same caches: the copy-on-write of a partly shared page.  HBM-bound byte copy: each lane moves 16 bytes of K
-// and 16 of V with one load and one store each; a wavefront covers four
-// 256-byte rows.
+// slot of the same caches: the copy-on-write of a partly shared page.
+// HBM-bound byte copy: each lane moves one 16-byte chunk of K and the same
+// chunk of V, with one load and one store each, from 32-bit indices (a
+// multiply-high division by the row's chunks and by the kv heads; a 64-bit
+// grid-stride version with three 64-bit divisions per chunk copied at 66%
+// of the HBM peak).  The new rows are read once: nontemporal loads.
+// Launches hold fewer than 2^31 chunks each (tokens split across launches).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -24,59 +28,70 @@ namespace xhip {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(256) void paged_kv_append_kernel(const KvAppendParams p) {
-    const long long n_chunks = (long long)p.num_tokens * p.num_kv_heads * p.row_chunks;
-    const long long stride = (long long)gridDim.x * blockDim.x;
-    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n_chunks; i += stride) {
-        const int c = (int)(i % p.row_chunks);
-        const long long row = i / p.row_chunks;  // token * num_kv_heads + kv head
-        const int h = (int)(row % p.num_kv_heads);
-        const int tok = (int)(row / p.num_kv_heads);
-        long long slot;
-        if (p.slots) {
-            slot = p.slots[tok];
-        } else {
-            const int pos = p.positions[tok];
-            if (pos < 0 || pos >= p.max_ctx) continue;
-            const int blk = p.block_tables[(size_t)tok * p.max_blocks + (pos >> p.bs_shift)];
-            slot = blk < 0 ? -1 : (long long)blk * p.block_size + (pos & (p.block_size - 1));
-        }
-        if (slot < 0) continue;
-        const long long blk = slot >> p.bs_shift;
-        const long long off = slot & (p.block_size - 1);
-        const size_t dst = (size_t)(blk * p.kv_block_stride_bytes + h * p.kv_head_stride_bytes +
-                                    off * p.row_bytes) + (size_t)c * 16;
-        size_t src;
-        if (p.src_slots) {  // copy inside the cache, page slot to page slot
-            const long long from = p.src_slots[tok];
-            if (from < 0) continue;
-            src = (size_t)((from >> p.bs_shift) * p.kv_block_stride_bytes +
-                           h * p.kv_head_stride_bytes +
-                           (from & (p.block_size - 1)) * p.row_bytes) + (size_t)c * 16;
-        } else if (p.key_rows) {  // each token's rows at their own address
-            const size_t o = (size_t)h * p.row_bytes + (size_t)c * 16;
-            const u32x4 k = *(const u32x4 *)(p.key_rows[tok] + o);
-            const u32x4 v = *(const u32x4 *)(p.value_rows[tok] + o);
-            *(u32x4 *)((char *)p.key_cache + dst) = k;
-            *(u32x4 *)((char *)p.value_cache + dst) = v;
-            continue;
-        } else {
-            src = (size_t)row * p.row_bytes + (size_t)c * 16;
-        }
-        const u32x4 k = *(const u32x4 *)((const char *)p.key + src);
-        const u32x4 v = *(const u32x4 *)((const char *)p.value + src);
-        *(u32x4 *)((char *)p.key_cache + dst) = k;
-        *(u32x4 *)((char *)p.value_cache + dst) = v;
+constexpr int kKvAppendBlock = 64;  // one wavefront per workgroup
+constexpr long long kKvAppendMaxChunks = (1LL << 31) - 1;
+
+__global__ __launch_bounds__(kKvAppendBlock) void paged_kv_append_kernel(const KvAppendParams p) {
+    const uint32_t i = blockIdx.x * kKvAppendBlock + threadIdx.x;
+    if (i >= p.chunks) return;
+    const uint32_t row_l = div_by(i, p.row_div);  // row of the launch: token * kv heads + head
+    const int c = (int)(i - row_l * (uint32_t)p.row_chunks);
+    const uint32_t tok_l = div_by(row_l, p.head_div);
+    const int h = (int)(row_l - tok_l * (uint32_t)p.num_kv_heads);
+    const int tok = p.tok0 + (int)tok_l;
+    long long slot;
+    if (p.slots) {
+        slot = p.slots[tok];
+    } else {
+        const int pos = p.positions[tok];
+        if (pos < 0 || pos >= p.max_ctx) return;
+        const int blk = p.block_tables[(size_t)tok * p.max_blocks + (pos >> p.bs_shift)];
+        slot = blk < 0 ? -1 : (long long)blk * p.block_size + (pos & (p.block_size - 1));
     }
+    if (slot < 0) return;
+    const long long blk = slot >> p.bs_shift;
+    const long long off = slot & (p.block_size - 1);
+    const size_t dst = (size_t)(blk * p.kv_block_stride_bytes + h * p.kv_head_stride_bytes +
+                                off * p.row_bytes) + (size_t)c * 16;
+    u32x4 k, v;
+    if (p.src_slots) {  // copy inside the cache, page slot to page slot
+        const long long from = p.src_slots[tok];
+        if (from < 0) return;
+        const size_t src = (size_t)((from >> p.bs_shift) * p.kv_block_stride_bytes +
+                                    h * p.kv_head_stride_bytes +
+                                    (from & (p.block_size - 1)) * p.row_bytes) + (size_t)c * 16;
+        k = *(const u32x4 *)((const char *)p.key + src);
+        v = *(const u32x4 *)((const char *)p.value + src);
+    } else if (p.key_rows) {  // each token's rows at their own address
+        const size_t o = (size_t)h * p.row_bytes + (size_t)c * 16;
+        k = __builtin_nontemporal_load((const u32x4 *)(p.key_rows[tok] + o));
+        v = __builtin_nontemporal_load((const u32x4 *)(p.value_rows[tok] + o));
+    } else {
+        const size_t src = ((size_t)tok * p.num_kv_heads + h) * p.row_bytes + (size_t)c * 16;
+        k = __builtin_nontemporal_load((const u32x4 *)((const char *)p.key + src));
+        v = __builtin_nontemporal_load((const u32x4 *)((const char *)p.value + src));
+    }
+    *(u32x4 *)((char *)p.key_cache + dst) = k;
+    *(u32x4 *)((char *)p.value_cache + dst) = v;
 }
 
-hipError_t launch_kv_append(const KvAppendParams &p, hipStream_t stream) {
-    const long long n_chunks = (long long)p.num_tokens * p.num_kv_heads * p.row_chunks;
-    if (n_chunks == 0) return hipSuccess;
-    long long blocks = (n_chunks + 255) / 256;
-    if (blocks > 65536) blocks = 65536;  // grid-stride beyond
-    paged_kv_append_kernel<<<(unsigned)blocks, 256, 0, stream>>>(p);
-    return hipGetLastError();
+hipError_t launch_kv_append(const KvAppendParams &params, hipStream_t stream) {
+    KvAppendParams p = params;
+    const long long per_token = (long long)p.num_kv_heads * p.row_chunks;
+    if (p.num_tokens <= 0 || per_token <= 0) return hipSuccess;
+    p.row_div = div_magic((uint32_t)p.row_chunks);
+    p.head_div = div_magic((uint32_t)p.num_kv_heads);
+    const long long tok_per_launch = kKvAppendMaxChunks / per_token;
+    for (long long t0 = 0; t0 < p.num_tokens; t0 += tok_per_launch) {
+        const long long n = p.num_tokens - t0 < tok_per_launch ? p.num_tokens - t0 : tok_per_launch;
+        p.tok0 = (int)t0;
+        p.chunks = (uint32_t)(n * per_token);
+        const long long blocks = ((long long)p.chunks + kKvAppendBlock - 1) / kKvAppendBlock;
+        paged_kv_append_kernel<<<(unsigned)blocks, kKvAppendBlock, 0, stream>>>(p);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 __global__ __launch_bounds__(256) void gather_rows_kernel(char *dst, const char *const *src,
