@@ -497,7 +497,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
     constexpr int NCH = Geo::kChunks;
     constexpr int RL = Geo::kRowLanes;
     constexpr int TT = Geo::kTileTokens;
-    extern __shared__ int pre[];  // num_seqs + 1 tile prefixes
+    extern __shared__ int pre[];  // num_seqs + 1 split-unit prefixes
 
     const int lane = threadIdx.x & 63;
     const int col = lane % RL;
@@ -611,38 +611,29 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-// Online log-sum-exp merge, into (m, l, acc) of KC columns, of a segment's
-// partials j = j0, j0 + step, ... < np (partial j in slot
+// Online log-sum-exp merge, into (m, l, acc) of one float4 column, of a
+// segment's partials j = j0, j0 + step, ... < np (partial j in slot
 // sbase + 2j + (j == 0 ? slot0 : 0)).  The partials go in batches of up to
 // NB whose loads are all issued before any is used, so a thread waits for
 // one memory round trip per batch, not per partial; batch slots past np
-// load and combine nothing.  Column k's (m, l) and float4 of o sit at
-// off_ml[k] and off_o[k] floats into a slot.
-template <int GT, int D, int KC, int NB>
+// load and combine nothing.  The column's (m, l) and float4 of o sit at
+// off_ml and off_o floats into a slot.
+template <int GT, int D, int NB>
 __device__ __forceinline__ void merge_partials(const DecodeParams &p, size_t sbase, int slot0,
-                                               int j0, int step, int np, const int (&off_ml)[KC],
-                                               const int (&off_o)[KC], float (&m)[KC],
-                                               float (&l)[KC], f32x4 (&acc)[KC]) {
+                                               int j0, int step, int np, int off_ml, int off_o,
+                                               float &m, float &l, f32x4 &acc) {
     for (int jb = j0; jb < np; jb += NB * step) {
-        f32x2 mlv[NB][KC];
-        f32x4 ov[NB][KC];
+        f32x2 mlv[NB];
+        f32x4 ov[NB];
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             const int j = jb + b * step;
-#pragma unroll
-            for (int k = 0; k < KC; k++) {  // (defined values for the slots left unread)
-                mlv[b][k] = f32x2{-INFINITY, 0.0f};
-                ov[b][k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            }
+            mlv[b] = f32x2{-INFINITY, 0.0f};  // (defined values for the slots left unread)
+            ov[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             if (j < np) {
                 const size_t slot = sbase + 2 * (size_t)j + (j == 0 ? slot0 : 0);
-                const float *mlb = p.ws_ml + slot * GT * 2;
-                const float *ob = p.ws_o + slot * GT * D;
-#pragma unroll
-                for (int k = 0; k < KC; k++) {
-                    mlv[b][k] = *(const f32x2 *)(mlb + off_ml[k]);
-                    ov[b][k] = *(const f32x4 *)(ob + off_o[k]);
-                }
+                mlv[b] = *(const f32x2 *)(p.ws_ml + slot * GT * 2 + off_ml);
+                ov[b] = *(const f32x4 *)(p.ws_o + slot * GT * D + off_o);
             }
         }
         // keep the scheduler from starting the combine (and waiting on the
@@ -651,16 +642,13 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p, size_t sba
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             if (jb + b * step >= np) break;
-#pragma unroll
-            for (int k = 0; k < KC; k++) {
-                const float mj = mlv[b][k].x;
-                const float M = fmaxf(m[k], mj);
-                const float Ms = (M == -INFINITY) ? 0.0f : M;
-                const float a = fast_exp2(m[k] - Ms), w = fast_exp2(mj - Ms);
-                l[k] = l[k] * a + mlv[b][k].y * w;
-                acc[k] = acc[k] * a + ov[b][k] * w;
-                m[k] = M;
-            }
+            const float mj = mlv[b].x;
+            const float M = fmaxf(m, mj);
+            const float Ms = (M == -INFINITY) ? 0.0f : M;
+            const float a = fast_exp2(m - Ms), w = fast_exp2(mj - Ms);
+            l = l * a + mlv[b].y * w;
+            acc = acc * a + ov[b] * w;
+            m = M;
         }
     }
 }
@@ -754,17 +742,16 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
     const bool active = col < ncols;
     const int h = active ? col / C4 : 0;
     const int c = active ? col - h * C4 : 0;
-    float m[1] = {-INFINITY}, l[1] = {0.0f};
-    f32x4 acc[1] = {{0.0f, 0.0f, 0.0f, 0.0f}};
-    const int off_ml[1] = {h * 2}, off_o[1] = {h * D + c * 4};
-    if (active) merge_partials<GT, D, 1, 8>(p, sbase, slot0, ps, kMergeSplit, np, off_ml, off_o, m, l, acc);
-    s_acc[ps][cl] = acc[0];
-    s_m[ps][cl] = m[0];
-    s_l[ps][cl] = l[0];
+    float m = -INFINITY, l = 0.0f;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (active) merge_partials<GT, D, 8>(p, sbase, slot0, ps, kMergeSplit, np, h * 2, h * D + c * 4, m, l, acc);
+    s_acc[ps][cl] = acc;
+    s_m[ps][cl] = m;
+    s_l[ps][cl] = l;
     __syncthreads();
     if (ps != 0 || !active) return;
-    float mm = m[0], ll = l[0];
-    f32x4 aa = acc[0];
+    float mm = m, ll = l;
+    f32x4 aa = acc;
 #pragma unroll
     for (int k = 1; k < kMergeSplit; k++) {
         const float mk = s_m[k][cl];
@@ -845,40 +832,40 @@ __global__ __launch_bounds__(NT) void paged_decode_merge_segment_kernel(const De
     const int nsplit = NT / span;
     const int cl = tid - split * span;
 
-    float m[1] = {-INFINITY}, l[1] = {0.0f};
-    f32x4 acc[1] = {{0.0f, 0.0f, 0.0f, 0.0f}};
-    const int h = (cl < ncols ? cl : 0) / C4;
-    const int off_ml[1] = {h * 2}, off_o[1] = {h * D + ((cl < ncols ? cl : 0) - h * C4) * 4};
-    if (cl < ncols)
-        merge_partials<GT, D, 1, 8>(p, sbase, slot0, split, nsplit, np, off_ml, off_o, m, l, acc);
+    float m = -INFINITY, l = 0.0f;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (cl < ncols) {
+        const int h = cl / C4;
+        merge_partials<GT, D, 8>(p, sbase, slot0, split, nsplit, np, h * 2, h * D + (cl - h * C4) * 4,
+                                 m, l, acc);
+    }
     if (nsplit > 1) {  // NT == 256 here: ncols < 256
-        s_acc[tid] = acc[0];
-        s_m[tid] = m[0];
-        s_l[tid] = l[0];
+        s_acc[tid] = acc;
+        s_m[tid] = m;
+        s_l[tid] = l;
         __syncthreads();
         if (split != 0) return;
         for (int k = 1; k < nsplit; k++) {
             const int o = k * span + cl;
             const float mk = s_m[o];
-            const float M = fmaxf(m[0], mk);
+            const float M = fmaxf(m, mk);
             const float Ms = (M == -INFINITY) ? 0.0f : M;
-            const float a = fast_exp2(m[0] - Ms), b = fast_exp2(mk - Ms);
-            l[0] = l[0] * a + s_l[o] * b;
-            acc[0] = acc[0] * a + s_acc[o] * b;
-            m[0] = M;
+            const float a = fast_exp2(m - Ms), b = fast_exp2(mk - Ms);
+            l = l * a + s_l[o] * b;
+            acc = acc * a + s_acc[o] * b;
+            m = M;
         }
     }
     if (cl >= ncols) return;
-    const float inv = l[0] > 0.0f ? 1.0f / l[0] : 0.0f;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     const size_t base = qrow0 + (size_t)cl * 4;  // head-major columns
     if (p.out_f32) {
-        *(f32x4 *)(p.out_f32 + base) = acc[0] * inv;
-        if (cl % C4 == 0)
-            p.out_lse[qrow0 / D + cl / C4] = l[0] > 0.0f ? m[0] + log2f(l[0]) : -INFINITY;
+        *(f32x4 *)(p.out_f32 + base) = acc * inv;
+        if (cl % C4 == 0) p.out_lse[qrow0 / D + cl / C4] = l > 0.0f ? m + log2f(l) : -INFINITY;
         return;
     }
 #pragma unroll
-    for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, acc[0][e] * inv);
+    for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, acc[e] * inv);
 }
 
 }  // namespace xhip

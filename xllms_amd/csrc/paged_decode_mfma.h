@@ -386,7 +386,7 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
     // which do not wait behind the K/V loads in flight.
     using G = MfmaGeometry<D>;
     constexpr int GT = kMfmaHeads * R;
-    extern __shared__ int pre[];  // num_seqs + 1 tile prefixes
+    extern __shared__ int pre[];  // num_seqs + 1 split-unit prefixes
     __shared__ __attribute__((aligned(16))) char vtile[kMfmaWavesPerGroup][G::kLdsTile];
 
     const int lane = threadIdx.x & 63;

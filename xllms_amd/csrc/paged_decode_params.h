@@ -45,7 +45,7 @@ struct DecodeParams {
     const int *seq_lens;       // [num_seqs]
     float *ws_o;               // [num_waves*2][head_tile][head_size] fp32 partial outputs
     float *ws_ml;              // [num_waves*2][head_tile][2] (running max, running sum)
-    int *ws_prefix;            // [num_seqs + 1] tiles before each sequence (written by wg 0)
+    int *ws_prefix;            // [num_seqs + 1] split units before each sequence (written by wg 0)
     long long kv_block_stride; // elements
     long long kv_head_stride;  // elements
     int num_seqs;
