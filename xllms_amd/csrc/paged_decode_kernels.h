@@ -380,6 +380,30 @@ __device__ __forceinline__ size_t fold_state_row(const DecodeParams &p, int base
     return (size_t)v * p.fold_kr + (size_t)kvh * p.fold_rows + (size_t)(q - v * p.fold_rows);
 }
 
+// Logical index of workgroup b of a g-workgroup launch such that logical
+// neighbours run on one XCD: the dispatcher deals workgroups to MI355X's 8
+// XCDs round-robin (b on XCD b % 8), so XCD x's workgroups get one
+// contiguous run of logical indices.  Neighbouring stream-K ranges then
+// share an L2 (the cascade's prefix batch reads each shared page from two
+// sequences of equal length, at the same offsets of neighbouring ranges).
+__device__ __forceinline__ int xcd_local_block(int b, int g) {
+    constexpr int kXcds = 8;
+    const int q = g / kXcds, r = g % kXcds;
+    const int x = b % kXcds, i = b / kXcds;
+    return x < r ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
+}
+
+// Logical workgroup of this workgroup for a launch of `total` split units:
+// XCD-local when the batch fills the launch (more than min_tiles_per_wave
+// units per wavefront, so ranges reach the last wavefronts); otherwise
+// (ranges on the lowest logical wavefronts only) the dispatch order, which
+// spreads the busy ones over all XCDs.
+__device__ __forceinline__ int logical_block(const DecodeParams &p, int total) {
+    return (long long)total > (long long)p.num_waves * p.min_tiles_per_wave
+               ? xcd_local_block(blockIdx.x, gridDim.x)
+               : (int)blockIdx.x;
+}
+
 // Split units of a segment of Ts tiles (paged_decode_params.h): its tiles
 // plus the start-up cost; an empty segment costs nothing.
 __device__ __forceinline__ int segment_units(const DecodeParams &p, int Ts) {
@@ -443,9 +467,9 @@ template <int TT, int WPG, typename Fn>
 __device__ __forceinline__ void stream_k_walk(const DecodeParams &p, int *pre, Fn &&fn) {
     batch_prefix<TT, WPG>(p, pre);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int w = blockIdx.x * WPG + wave;
     const int B = p.num_seqs;
     const int total = pre[B];
+    const int w = logical_block(p, total) * WPG + wave;
     const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);
     const long long g_lo = (long long)w * tpw;
     if (g_lo >= total) return;

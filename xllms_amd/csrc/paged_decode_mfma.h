@@ -395,9 +395,9 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
     const int j = lane & 15, gq = lane >> 4;
 
     batch_prefix<16, kMfmaWavesPerGroup>(p, pre);
-    const int w = blockIdx.x * kMfmaWavesPerGroup + wave;
     const int B = p.num_seqs;
     const int total = pre[B];
+    const int w = logical_block(p, total) * kMfmaWavesPerGroup + wave;
     const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);
     const long long g_lo = (long long)w * tpw;
     if (g_lo >= total) return;
