@@ -14,7 +14,6 @@
 #include <cstring>
 #include <string>
 #include <unordered_map>
-#include <unordered_set>
 #include <vector>
 
 #include "paged_kv_append.h"
@@ -108,8 +107,13 @@ struct InstanceState {
     void *key_cache = nullptr;
     void *value_cache = nullptr;
     NxtKvIndex *index = nullptr;
-    std::unordered_map<std::string, int32_t> seqs;       // request id -> sequence
-    std::unordered_map<std::string, NxtDecodeIo> bound;  // request id -> next exec's buffers
+    std::unordered_map<std::string, int32_t> seqs;  // request id -> sequence
+    struct Bound {
+        NxtDecodeIo io;
+        uint64_t exec_stamp;  // the exec that last took it (duplicate check)
+    };
+    std::unordered_map<std::string, Bound> bound;  // request id -> next exec's buffers
+    uint64_t exec_stamp = 0;
     // staging of one exec
     HostBuf<int32_t> h_slots, h_src, h_dst, h_bt, h_lens, h_group, h_pblocks, h_seqs;
     HostBuf<const char *> h_kptr, h_vptr, h_qptr;
@@ -358,7 +362,7 @@ XMI_EXPORT int nxt_model_instance_bind(NxtModelInstance *instance, const char *r
     }
     NxtDecodeIo c = *io;
     c.struct_size = sizeof(NxtDecodeIo);
-    st->bound[request_id] = c;
+    st->bound[request_id] = InstanceState::Bound{c, 0};
     return 0;
 }
 
@@ -372,21 +376,22 @@ XMI_EXPORT int nxt_model_instance_exec(NxtModelInstance *instance, NxtInferReque
     if ((int)request_count > s.max_batch)
         return fail("exec: %u requests > max_batch_size %d", request_count, s.max_batch);
 
-    // every request bound, each once
+    // every request bound, each once (a bound entry carries the stamp of the
+    // exec that took it)
     std::vector<Item> items;
     items.reserve(request_count);
-    std::unordered_set<std::string> ids;
-    ids.reserve(request_count * 2);
+    const uint64_t stamp = ++st->exec_stamp;
     for (uint32_t i = 0; i < request_count; ++i) {
         if (!requests[i] || !requests[i]->request_id) return fail("exec: request %u has no id", i);
         const std::string id = requests[i]->request_id;
         auto b = st->bound.find(id);
         if (b == st->bound.end()) return fail("exec: request %s has no bound buffers", id.c_str());
-        if (!ids.insert(id).second)
+        if (b->second.exec_stamp == stamp)
             return fail("exec: request %s twice in one batch", id.c_str());
+        b->second.exec_stamp = stamp;
         auto q = st->seqs.find(id);
-        items.push_back({id, b->second, q == st->seqs.end() ? -1 : q->second});
-        if (items.back().seq < 0 && b->second.num_tokens == 0)
+        items.push_back({id, b->second.io, q == st->seqs.end() ? -1 : q->second});
+        if (items.back().seq < 0 && b->second.io.num_tokens == 0)
             return fail("exec: new request %s without tokens", id.c_str());
     }
     if (hipSetDevice(st->device) != hipSuccess) return fail("exec: hipSetDevice failed");
