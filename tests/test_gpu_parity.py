@@ -128,13 +128,13 @@ def test_merge_per_segment_paths(cuda, shape):
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("head_size", [32, 64, 96, 128, 256])
-@pytest.mark.parametrize("heads", [(34, 2), (24, 1), (64, 2)])
-def test_mfma_groups_of_17_to_32(cuda, dtype, head_size, heads):
-    """Groups of 17-32 query heads on the MFMA path: one wavefront carries two
-    16-head row blocks over every K/V tile (head_size <= 128; two wavefronts
-    of one block above), with a partly filled second block for 17 and 24
-    heads; automatic plans and explicit partitions (partials of 32 heads
-    merged)."""
+@pytest.mark.parametrize("heads", [(34, 2), (24, 1), (64, 2), (64, 1), (80, 2)])
+def test_mfma_groups_of_17_to_64(cuda, dtype, head_size, heads):
+    """Groups of 17-64 query heads on the MFMA path: one wavefront carries two
+    16-head row blocks over every K/V tile (head_size <= 128; one block per
+    wavefront above), with a partly filled last block for 17, 24 and 40
+    heads, and two or more head tiles for 40 and 64; automatic plans and
+    explicit partitions (partials of 32 heads merged)."""
     H, KVH = heads
     wl = W.small_case(num_seqs=5, H=H, KVH=KVH, D=head_size, kv_dtype=DT[dtype],
                       seed=H * head_size + KVH, lens=[0, 1, 40, 700, 1500])
@@ -373,6 +373,8 @@ def test_unsupported_shapes_leave_output_untouched(cuda):
     assert call(bs=12) == PA.NXT_ATTN_E_UNSUPPORTED
     assert call(kbs=wl.kv_block_stride + 3) == PA.NXT_ATTN_E_UNSUPPORTED
     assert call(num_seqs=-1) == PA.NXT_ATTN_E_INVALID
+    assert call(num_heads=256, num_kv_heads=2) == PA.NXT_ATTN_E_UNSUPPORTED  # group 128 > 64
+    assert call(num_heads=128, num_kv_heads=2, dtype_size=4) == PA.NXT_ATTN_E_UNSUPPORTED  # fp32: > 32
     torch.cuda.synchronize()
     assert torch.equal(dw.out.view(torch.int16), sentinel.view(torch.int16))
     assert call() == PA.NXT_ATTN_OK

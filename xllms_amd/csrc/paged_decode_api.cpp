@@ -160,8 +160,14 @@ struct HeadTiling {
     int head_tiles;  // wavefronts per (seq, kv head, partition)
 };
 
+// Largest GQA group of a tile path: the MFMA path splits any group into
+// head tiles (segments of their own); the VALU path's tiles stop at 32.
+int max_group(bool mfma) {
+    return mfma ? xhip::kMfmaMaxGroup : xhip::kMaxHeadTile * xhip::kWavesPerGroup;
+}
+
 bool head_tiling(int group, bool mfma, int head_size, HeadTiling *t) {
-    if (group <= 0 || group > xhip::kMaxHeadTile * xhip::kWavesPerGroup) return false;
+    if (group <= 0 || group > max_group(mfma)) return false;
     if (mfma) {
         // groups of 17-32 heads: one wavefront with two row blocks reads each
         // K/V tile once for all of them (head_size <= 128), else two
@@ -295,8 +301,7 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
     const bool mfma = use_mfma(kv_dtype, head_size, block_size);
     HeadTiling tiling;
     if (!head_tiling(group, mfma, head_size, &tiling))
-        return set_status(NXT_ATTN_E_UNSUPPORTED, "GQA group %d > %d", group,
-                          xhip::kMaxHeadTile * xhip::kWavesPerGroup);
+        return set_status(NXT_ATTN_E_UNSUPPORTED, "GQA group %d > %d", group, max_group(mfma));
     if (num_seqs == 0) return ok();
     const void *out_any = po ? (const void *)po->out_f32 : out;
     if (!out_any || !query || !key_cache || !value_cache || !block_tables || !seq_lens ||
@@ -465,12 +470,14 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
         max_num_blocks_per_seq <= 0 || !is_pow2(block_size))
         return set_status(NXT_ATTN_E_INVALID, "bad cascade arguments");
     const int group = num_heads / num_kv_heads;
-    // Query rows per kv head of a prefix-batch sequence: 32 where the MFMA
-    // path serves 32 heads per wavefront (each shared page then feeds twice
-    // as many members per read), else a multiple of the 16-head tile.
+    // Query rows per kv head of a prefix-batch sequence: 64 (two 32-head
+    // tiles, neighbouring segments of one sequence, which read the same
+    // shared pages at the same offsets on one XCD) where the MFMA path serves
+    // 32 heads per wavefront, else a multiple of the 16-head tile.
+    constexpr int kCascadeWideRows = 4 * xhip::kCascadeRows;
     const bool wide = use_mfma(kv_dtype, head_size, block_size) &&
-                      head_size <= xhip::kMfmaWideMaxHeadSize && group <= 2 * xhip::kCascadeRows;
-    const int rows = wide ? 2 * xhip::kCascadeRows
+                      head_size <= xhip::kMfmaWideMaxHeadSize && group <= kCascadeWideRows;
+    const int rows = wide ? kCascadeWideRows
                           : (group + xhip::kCascadeRows - 1) / xhip::kCascadeRows *
                                 xhip::kCascadeRows;
     const long long v_max = ((long long)num_seqs * group + rows - 1) / rows + max_groups;

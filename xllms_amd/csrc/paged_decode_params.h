@@ -32,6 +32,7 @@ constexpr int kMfmaWavesPerGroup = 4;  // MFMA tile path
 constexpr int kMaxHeadTile = 8;      // query heads per wavefront, VALU tile path
 constexpr int kMfmaHeads = 16;       // query heads per MFMA row block (R blocks per wavefront)
 constexpr int kMfmaWideMaxHeadSize = 128;  // largest head_size with R = 2
+constexpr int kMfmaMaxGroup = 64;    // largest GQA group on the MFMA path (head tiles of 16 or 32)
 constexpr int kMergeCols = 32;       // float4 columns per workgroup of the chunked merge
 constexpr int kLoadsPerTile = 4;     // 16-byte K (and V) loads per lane per tile
 constexpr int kMaxSeqsPerLaunch = 8192;  // the per-workgroup prefix scan lives in LDS
