@@ -159,8 +159,31 @@ __global__ __launch_bounds__(kPlanThreads) void cascade_plan_meta_lds_kernel(con
         l_moff[g] = l_count[g];
     }
     __syncthreads();
-    const int vt = block_exclusive_scan(l_vbase, NG, part);
-    block_exclusive_scan(l_moff, NG, part);
+    int vt;
+    if (NG <= 64) {
+        // one wavefront scans both arrays with shuffles (no workgroup barriers)
+        if (tid < 64) {
+            const int a = tid < NG ? l_vbase[tid] : 0, b = tid < NG ? l_moff[tid] : 0;
+            int sa = a, sb = b;
+            for (int off = 1; off < 64; off <<= 1) {
+                const int ua = __shfl_up(sa, off), ub = __shfl_up(sb, off);
+                if (tid >= off) {
+                    sa += ua;
+                    sb += ub;
+                }
+            }
+            if (tid < NG) {
+                l_vbase[tid] = sa - a;
+                l_moff[tid] = sb - b;
+            }
+            if (tid == 63) part[0] = sa;
+        }
+        __syncthreads();
+        vt = part[0];
+    } else {
+        vt = block_exclusive_scan(l_vbase, NG, part);
+        block_exclusive_scan(l_moff, NG, part);
+    }
     for (int g = tid; g < NG; g += kPlanThreads) {
         c.g_count[g] = l_count[g];
         c.g_first[g] = l_first[g];
