@@ -252,6 +252,7 @@ struct PartialOut {
     float *out_f32;
     float *out_lse;
     int cached_seqs;  // leading sequences whose K/V loads are cacheable
+    int skip_empty;   // rows of empty sequences are never read: leave them unwritten
 };
 
 // Prefix fold of a pass (cascade suffix pass): DecodeParams::fold_row.
@@ -381,6 +382,7 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
             p.out_f32 = po->out_f32 + (size_t)s0 * num_heads * head_size;
             p.out_lse = po->out_lse + (size_t)s0 * num_heads;
             p.cached_seqs = po->cached_seqs > s0 ? po->cached_seqs - s0 : 0;
+            p.skip_empty = po->skip_empty;
         }
         if (fold) {
             p.fold_row = fold->row + s0;
@@ -552,7 +554,9 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
     e = xhip::launch_cascade_plan(c, stream);
     if (e != hipSuccess)
         return set_status(NXT_ATTN_E_HIP, "cascade plan launch: %s", hipGetErrorString(e));
-    const PartialOut pre{(float *)(w + o_po), (float *)(w + o_pl), (int)v_max};
+    // (the prefix batch's empty sequences are the reserved ones no group
+    // uses: nothing reads their rows)
+    const PartialOut pre{(float *)(w + o_po), (float *)(w + o_pl), (int)v_max, 1};
     st = run(nullptr, c.v_q, key_cache, value_cache, c.v_bt, c.v_lens, (int)v_max,
              num_kv_heads * rows, head_size, num_kv_heads, scale, max_num_blocks_per_seq,
              block_size, eb, kv_block_stride, kv_head_stride, stream_handle, kv_dtype, 0, &pre);

@@ -742,7 +742,7 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
     const size_t qrow0 = ((size_t)s * p.num_heads + (size_t)kvh * p.group + g0) * D;
 
     if (L == 0) {
-        if (tid < kMergeCols && col0 + tid < ncols)
+        if (tid < kMergeCols && col0 + tid < ncols && !p.skip_empty)
             write_empty_column<KV, D>(p, s, kvh, g0, qrow0, col0 + tid);
         return;
     }
@@ -833,7 +833,8 @@ __global__ __launch_bounds__(NT) void paged_decode_merge_segment_kernel(const De
     const size_t qrow0 = ((size_t)s * p.num_heads + (size_t)kvh * p.group + g0) * D;
 
     if (L == 0) {
-        for (int col = tid; col < ncols; col += NT) write_empty_column<KV, D>(p, s, kvh, g0, qrow0, col);
+        if (!p.skip_empty)
+            for (int col = tid; col < ncols; col += NT) write_empty_column<KV, D>(p, s, kvh, g0, qrow0, col);
         return;
     }
     const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);

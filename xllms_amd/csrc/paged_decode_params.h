@@ -71,6 +71,8 @@ struct DecodeParams {
     float *out_lse;
     int cached_seqs;           // sequences [0, cached_seqs) load K/V cacheable (pages read
                                // by several wavefronts close in time); the rest nontemporal
+    int skip_empty;            // 1: the rows of empty sequences are left unwritten (their
+                               // reader never reads them)
     // Prefix fold (cascade suffix pass): when fold_row is set, sequence s
     // with fold_row[s] >= 0 continues the attention of an earlier pass over
     // its shared prefix.  That pass left, for (kv head h, query head g of
