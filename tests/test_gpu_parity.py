@@ -107,6 +107,15 @@ def test_split_k_every_tile_path(cuda, dtype, head_size):
     (64, 2, 64, "fp32", 64),
     (48, 2, 64, "bf16", 256),
     (64, 2, 128, "fp16", 256),
+    # 64 and 16 columns (64-thread workgroups; four threads per column), and
+    # groups whose last head tile is partly filled (40 heads in tiles of
+    # 32 + 8, 24 in 16 + 8, 12 in 8 + 4): those segments have at most half
+    # the workgroup's columns, and threads split their partials.
+    (16, 8, 128, "fp16", 64),
+    (8, 8, 64, "bf16", 128),
+    (80, 2, 128, "fp16", 128),
+    (48, 2, 256, "fp16", 128),
+    (12, 1, 128, "fp32", 256),
 ])
 def test_merge_per_segment_paths(cuda, shape):
     """Batches with enough segments merge with one workgroup per segment:

@@ -69,16 +69,22 @@ static hipError_t launch_merge(const DecodeParams &p, hipStream_t st) {
     const unsigned segs = (unsigned)(p.num_seqs * p.num_kv_heads * p.head_tiles);
     const int heads = p.group < GT ? p.group : GT;
     if (p.merge_per_segment) {
-        // one thread per float4 column of the segment (heads * D/4), at
-        // least 256; the wider instantiations exist only where a segment
-        // can have that many columns
+        // one thread per float4 column of the segment (heads * D/4), the
+        // count rounded up to a power of two from 64 to 1024; the wider
+        // instantiations exist only where a segment can have that many
+        // columns (fewer than 64 columns: 64 threads split the partials)
         constexpr int kMaxCols = GT * (D / 4);
-        constexpr int kNt512 = kMaxCols > 256 ? 512 : kMergeSegThreads;
-        constexpr int kNt1024 = kMaxCols > 512 ? 1024 : kMergeSegThreads;
+        constexpr int kNt128 = kMaxCols > 64 ? 128 : 64;
+        constexpr int kNt256 = kMaxCols > 128 ? 256 : 64;
+        constexpr int kNt512 = kMaxCols > 256 ? 512 : 64;
+        constexpr int kNt1024 = kMaxCols > 512 ? 1024 : 64;
         const int cols = heads * (D / 4);
-        if (cols <= kMergeSegThreads)
-            paged_decode_merge_segment_kernel<KV, D, GT, TT, kMergeSegThreads>
-                <<<segs, kMergeSegThreads, 0, st>>>(p);
+        if (cols <= 64)
+            paged_decode_merge_segment_kernel<KV, D, GT, TT, 64><<<segs, 64, 0, st>>>(p);
+        else if (cols <= 128)
+            paged_decode_merge_segment_kernel<KV, D, GT, TT, kNt128><<<segs, kNt128, 0, st>>>(p);
+        else if (cols <= 256)
+            paged_decode_merge_segment_kernel<KV, D, GT, TT, kNt256><<<segs, kNt256, 0, st>>>(p);
         else if (cols <= 512)
             paged_decode_merge_segment_kernel<KV, D, GT, TT, kNt512><<<segs, kNt512, 0, st>>>(p);
         else

@@ -801,20 +801,21 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
 // Merge kernel, one workgroup per segment: for batches with enough segments
 // to fill the GPU (where the (segment, chunk) grid above would launch several
 // thousand short workgroups, each costing ~2 ns of dispatch).  NT threads
-// (256, 512 or 1024, chosen at launch as the segment's ncols float4 columns
-// rounded up to a power of two, at least 256) cover the columns, one each;
-// with fewer than 256 columns, the S = 256 / pow2(ncols) threads of a column
-// split its partials (every S-th one) and combine in LDS.  Each thread runs
+// (64 to 1024, chosen at launch as the first head tile's float4 columns
+// rounded up to a power of two, at least 64) cover the columns, one each;
+// where a segment has at most NT / 2 columns (fewer than 64, or the partly
+// filled last head tile of a group), the S = NT / pow2(ncols) threads of a
+// column split its partials (every S-th one) and combine in LDS.  Each thread runs
 // the online log-sum-exp merge over its partials with a batch of their loads
 // in flight at a time.
-constexpr int kMergeSegThreads = 256;  // NT when ncols <= 256
+constexpr int kMergeSegThreads = 64;  // the smallest NT (LDS split below that many columns)
 
 template <int KV, int D, int GT, int TT, int NT>
 __global__ __launch_bounds__(NT) void paged_decode_merge_segment_kernel(const DecodeParams p) {
     constexpr int C4 = D / 4;
-    __shared__ f32x4 s_acc[kMergeSegThreads];
-    __shared__ float s_m[kMergeSegThreads];
-    __shared__ float s_l[kMergeSegThreads];
+    __shared__ f32x4 s_acc[NT];
+    __shared__ float s_m[NT];
+    __shared__ float s_l[NT];
     const int segs = p.num_kv_heads * p.head_tiles;
     const int s = blockIdx.x / segs;
     const int seg = blockIdx.x - s * segs;
@@ -864,7 +865,7 @@ __global__ __launch_bounds__(NT) void paged_decode_merge_segment_kernel(const De
         merge_partials<GT, D, 8>(p, sbase, slot0, split, nsplit, np, h * 2, h * D + (cl - h * C4) * 4,
                                  m, l, acc);
     }
-    if (nsplit > 1) {  // NT == 256 here: ncols < 256
+    if (nsplit > 1) {  // ncols <= NT / 2: fewer than 64 columns, or a partly filled last head tile
         s_acc[tid] = acc;
         s_m[tid] = m;
         s_l[tid] = l;
