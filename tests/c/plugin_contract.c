@@ -38,15 +38,24 @@ static int failures = 0;
         }                                                             \
     } while (0)
 
-/* fp32 -> binary16, round to nearest even (normal range suffices here). */
+/* fp32 -> binary16, round to nearest even, for |f| in [2^-14, 65504] or 0:
+ * the inputs below are multiples of 2^-9 in [-1, 1), all exact in binary16
+ * (anything smaller than the normal range is flushed to a signed zero). */
 static unsigned short to_half(float f) {
     unsigned int x;
     memcpy(&x, &f, 4);
     unsigned short sign = (unsigned short)((x >> 16) & 0x8000u);
     unsigned int ax = x & 0x7FFFFFFFu;
+    if (ax < 0x38800000u) return sign; /* below 2^-14 */
     unsigned int odd = (ax >> 13) & 1u;
     ax += 0xC8000FFFu + odd;
     return sign | (unsigned short)(ax >> 13);
+}
+
+/* A seeded value in [-1, 1) that is a multiple of 2^-9. */
+static float next_value(unsigned int *seed) {
+    *seed = *seed * 1664525u + 1013904223u;
+    return (float)((int)(*seed >> 22) - 512) / 512.0f;
 }
 
 static float from_half(unsigned short h) {
@@ -65,15 +74,10 @@ static int real_decode(RunFn run, NxtBackend *b) {
     unsigned short *q = malloc(q_n * 2), *k = malloc(kv_n * 2), *v = malloc(kv_n * 2),
                    *o = malloc(q_n * 2);
     unsigned int seed = 12345u;
-    for (size_t i = 0; i < q_n; i++) {
-        seed = seed * 1664525u + 1013904223u;
-        q[i] = to_half(((float)(seed >> 8) / 16777216.0f - 0.5f) * 2.0f);
-    }
+    for (size_t i = 0; i < q_n; i++) q[i] = to_half(next_value(&seed));
     for (size_t i = 0; i < kv_n; i++) {
-        seed = seed * 1664525u + 1013904223u;
-        k[i] = to_half(((float)(seed >> 8) / 16777216.0f - 0.5f) * 2.0f);
-        seed = seed * 1664525u + 1013904223u;
-        v[i] = to_half(((float)(seed >> 8) / 16777216.0f - 0.5f) * 2.0f);
+        k[i] = to_half(next_value(&seed));
+        v[i] = to_half(next_value(&seed));
     }
     void *dq, *dk, *dv, *dout, *dbt, *dsl;
     if (hipMalloc(&dq, q_n * 2) || hipMalloc(&dk, kv_n * 2) || hipMalloc(&dv, kv_n * 2) ||

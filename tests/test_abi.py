@@ -107,6 +107,23 @@ def test_plugin_contract_c_harness(contract_binary):
     assert r.returncode == 0, r.stdout
 
 
+@pytest.mark.parametrize("sanitize", [[], ["-fsanitize=thread", "-g"]],
+                         ids=["plain", "tsan"])
+def test_workspace_cache_threads(tmp_path, sanitize):
+    """The per-(device, stream) workspace cache under host threads, on a mock
+    device that models queues of in-flight work (tests/c/workspace_cache_test.cpp):
+    no device use-after-free on growth or release, no workspace shared across
+    the per-thread stream's queues, no interleaved enqueues on one handle."""
+    exe = str(tmp_path / "workspace_cache_test")
+    subprocess.run(["g++", "-std=c++17", "-O1", "-pthread", "-Wall", *sanitize,
+                    f"-I{os.path.join(ROOT, 'xllms_amd', 'csrc')}", "-o", exe,
+                    os.path.join(ROOT, "tests", "c", "workspace_cache_test.cpp")], check=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=300)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0 and "PASSED" in r.stdout
+    assert "WARNING: ThreadSanitizer" not in r.stderr
+
+
 def test_plugin_null_conventions_python_loader():
     b = B.LoadedBackend()
     assert b.init_fn(None) == -1
@@ -168,6 +185,31 @@ def test_void_entry_points_record_status():
     lib.nxt_paged_attention_flash(p, p, p, p, p, p, 0, 8, 128, 2, ctypes.c_float(0.1), 4, 16, 2,
                                   4096, 2048, None)
     assert lib.nxt_attn_last_status() == PA.NXT_ATTN_OK
+
+
+def test_cascade_validation_without_launch():
+    """nxt_paged_attention_cascade refuses NULL or misaligned tensors before
+    its plan kernels (which read the tables) are launched: these calls
+    return without touching a GPU."""
+    lib = _lib.backend()
+    p = 256
+
+    def call(out=p, q=p, k=p, v=p, bt=p, sl=p, pg=p, pb=p, max_groups=2, num_seqs=4):
+        return lib.nxt_paged_attention_cascade(out, q, k, v, bt, sl, pg, pb, max_groups,
+                                               num_seqs, 32, 128, 8, ctypes.c_float(0.1), 8, 16,
+                                               8 * 16 * 128, 16 * 128, PA.NXT_KV_FP16, None)
+
+    for name in ("out", "q", "k", "v", "bt", "sl", "pg", "pb"):
+        assert call(**{name: None}) == PA.NXT_ATTN_E_INVALID, name
+        assert PA.last_status()[0] == PA.NXT_ATTN_E_INVALID
+    assert call(q=p + 8) == PA.NXT_ATTN_E_UNSUPPORTED
+    assert call(k=p + 2) == PA.NXT_ATTN_E_UNSUPPORTED
+    assert call(bt=p + 2) == PA.NXT_ATTN_E_INVALID
+    assert call(pg=p + 1) == PA.NXT_ATTN_E_INVALID
+    assert call(max_groups=-1) == PA.NXT_ATTN_E_INVALID
+    # an empty batch needs no tensors, as for the ordinary entry points
+    assert call(out=None, q=None, k=None, v=None, bt=None, sl=None, pg=None, pb=None,
+                num_seqs=0) == PA.NXT_ATTN_OK
 
 
 def test_kv_append_validation_without_launch():

@@ -49,7 +49,7 @@ def test_head_sizes(cuda, dtype, head_size):
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
 @pytest.mark.parametrize("heads", [(8, 8), (8, 4), (6, 2), (8, 2), (12, 4), (16, 2), (40, 8),
-                                   (32, 2), (64, 4), (64, 2)])
+                                   (32, 2), (64, 4), (64, 2), (17, 1), (20, 1), (48, 2)])
 def test_gqa_groups(cuda, dtype, heads):
     H, KVH = heads
     wl = W.small_case(num_seqs=3, H=H, KVH=KVH, D=128, kv_dtype=DT[dtype], seed=H * 7 + KVH,
@@ -116,6 +116,12 @@ def test_split_k_every_tile_path(cuda, dtype, head_size):
     (80, 2, 128, "fp16", 128),
     (48, 2, 256, "fp16", 128),
     (12, 1, 128, "fp32", 256),
+    # VALU groups of 17-24 heads: three head tiles of 8, the last partly
+    # filled (fp32 at 128 and 64 dims; bf16 at head_size 80, which the MFMA
+    # path does not take)
+    (48, 2, 128, "fp32", 64),
+    (40, 2, 64, "fp32", 128),
+    (17, 1, 80, "bf16", 256),
 ])
 def test_merge_per_segment_paths(cuda, shape):
     """Batches with enough segments merge with one workgroup per segment:
@@ -171,10 +177,11 @@ def test_auto_split_many_short_segments(cuda, dtype):
     assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"auto split {dtype}")
 
 
-def test_back_to_back_launches_reuse_counters(cuda):
-    """The in-kernel merge counters are left at zero by every launch: many
-    launches of different shapes on one stream (one shared workspace), each
-    checked, with repeats of the same shape in between."""
+def test_back_to_back_launches_share_a_workspace(cuda):
+    """Launches of different shapes on one stream share one split-K
+    workspace (grown when a shape needs more): each launch's partials and
+    unit prefix are its own, so every result is checked, with repeats of the
+    same shape in between."""
     cases = [W.small_case(num_seqs=6, H=32, KVH=8, D=128, kv_dtype=W.FP16, seed=90 + i,
                           max_len=2500) for i in range(3)]
     cases.append(W.small_case(num_seqs=3, H=16, KVH=1, D=64, kv_dtype=W.BF16, seed=99,
@@ -345,7 +352,9 @@ def test_config3_long_context(cuda):
 
 @pytest.mark.parametrize("kvh", [8, 4])
 def test_config4_bf16(cuda, kvh):
-    wl = W.config4(num_kv_heads=kvh, num_seqs=32)
+    """Config 4 at its full batch of 128 sequences, GQA 8 and GQA 16."""
+    wl = W.config4(num_kv_heads=kvh)
+    assert wl.num_seqs == 128
     stats = assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"config4 kvh={kvh}")
     print("config4", kvh, stats)
 

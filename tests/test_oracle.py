@@ -87,7 +87,10 @@ def test_paged_oracle_matches_golden():
         assert rel.max() <= 1e-5, (name, rel.max())
 
 
-@pytest.mark.skipif(O.ref_lib() is None, reason="oracle/_ref not built (reference tree absent)")
+# a file check, not a load: collection (also under -m gpu) never dlopens the
+# reference build
+@pytest.mark.skipif(not os.path.exists(O.REF_SO),
+                    reason="oracle/_ref not built (reference tree absent)")
 @pytest.mark.parametrize("seed", range(6))
 def test_restatement_matches_compiled_reference(seed):
     rng = np.random.default_rng(seed)

@@ -14,7 +14,9 @@
  *     that every tensor pointer is device memory (hipPointerGetAttributes), so
  *     a garbage descriptor (tests/test_backend_load.c:116-118 passes a 4-byte
  *     int) is refused with -1 instead of being launched.
- *   - fini() waits for the device and releases the split-K workspaces.
+ *   - fini() waits for the device and releases the split-K workspaces that
+ *     this backend's runs allocated (not those of other backends, model
+ *     instances or direct operator callers in the same process).
  */
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
@@ -22,6 +24,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "workspace.h"
 #include "xllm_hip_backend.h"
 
 #define XHIP_EXPORT __attribute__((visibility("default")))
@@ -107,12 +110,16 @@ static int launch(HipBackendState *st, const NxtPagedAttentionInput *pa, void *o
             }
         }
     }
+    /* the workspaces this run allocates belong to this backend (its fini
+     * frees them, and no other backend's) */
+    const void *prev_owner = xhip_set_workspace_owner(st);
     int rc = nxt_paged_attention_ex(output, pa->query, pa->key_cache, pa->value_cache,
                                     pa->block_tables, pa->seq_lens, pa->num_seqs, pa->num_heads,
                                     pa->head_size, pa->num_kv_heads, pa->scale,
                                     pa->max_num_blocks_per_seq, pa->block_size, pa->dtype_size,
                                     pa->kv_block_stride, pa->kv_head_stride, pa->stream, kv_dtype,
                                     partition_tokens);
+    (void)xhip_set_workspace_owner(prev_owner);
     st->runs++;
     if (rc != NXT_ATTN_OK) {
         st->failures++;
@@ -164,7 +171,8 @@ XHIP_EXPORT int nxt_backend_fini(NxtBackend *backend) {
     if (st) {
         fprintf(stderr, "[hip_backend] unloading device=%d runs=%llu failures=%llu\n",
                 st->device_id, st->runs, st->failures);
-        (void)nxt_attn_release_workspaces();
+        /* after a wait for the device: only what this backend's runs allocated */
+        (void)xhip_release_owner_workspaces(st);
         free(st);
         backend->backend_state = NULL;
     }

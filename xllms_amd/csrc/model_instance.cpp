@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "paged_kv_append.h"
+#include "workspace.h"
 #include "xllm_hip_backend.h"
 #include "xllm_hip_kv_index.h"
 
@@ -217,6 +218,9 @@ void destroy_state(InstanceState *st) {
     st->d_pack.release();
     st->d_q.release();
     st->d_out.release();
+    // the operator layer keeps split-K / cascade workspaces per stream:
+    // free this stream's before the handle goes (it may be reused)
+    if (st->stream) (void)xhip_release_stream_workspaces(st->device, st->stream);
     if (st->stream) (void)hipStreamDestroy(st->stream);
     st->magic = 0;
     delete st;

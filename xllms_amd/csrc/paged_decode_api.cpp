@@ -19,6 +19,8 @@
 #include "paged_decode_launch.h"
 #include "paged_decode_params.h"
 #include "paged_kv_append.h"
+#include "workspace.h"
+#include "workspace_cache.h"
 #include "xllm_hip_operator_api.h"
 
 namespace {
@@ -46,55 +48,49 @@ int ok() {
 }
 
 // ---------------------------------------------------------------- workspace
-struct Workspace {
-    int device;
-    hipStream_t stream;
-    int kind;  // kWsSplitK: split-K partials; kWsCascade: cascade plan and pass outputs
-    void *ptr;
-    size_t bytes;
+// Device calls of the workspace cache (workspace_cache.h).
+struct HipDev {
+    // runs fn with `device` current, restoring the caller's device
+    template <class Fn> static int on_device(int device, Fn &&fn) {
+        int cur = 0;
+        if (hipGetDevice(&cur) != hipSuccess) return 1;
+        if (cur != device && hipSetDevice(device) != hipSuccess) return 1;
+        const hipError_t e = fn();
+        if (cur != device) (void)hipSetDevice(cur);
+        return e == hipSuccess ? 0 : 1;
+    }
+    static int sync_stream(int, void *stream) {
+        return hipStreamSynchronize((hipStream_t)stream) == hipSuccess ? 0 : 1;
+    }
+    static int sync_device(int device) {
+        return on_device(device, [] { return hipDeviceSynchronize(); });
+    }
+    static int alloc(int, void **ptr, size_t bytes) {  // the caller's device is current
+        return hipMalloc(ptr, bytes) == hipSuccess ? 0 : 1;
+    }
+    static int release(int device, void *ptr) {
+        return on_device(device, [ptr] { return hipFree(ptr); });
+    }
+    static bool per_thread(void *stream) { return stream == (void *)hipStreamPerThread; }
 };
 
-constexpr int kWsSplitK = 0;
-constexpr int kWsCascade = 1;
+using WsCache = xhip::WorkspaceCache<HipDev>;
+using xhip::kWsCascade;
+using xhip::kWsSplitK;
 
-std::mutex g_ws_mu;
-std::vector<Workspace> g_ws;
+WsCache g_ws;
+thread_local const void *t_ws_owner = nullptr;
 
-// Returns a workspace of at least `bytes` for (device, stream).  Growing one
-// waits for the stream first, so no kernel still in flight on it can touch
-// the old buffer.
-int get_workspace(int device, hipStream_t stream, size_t bytes, void **out, int kind = kWsSplitK) {
-    std::lock_guard<std::mutex> lock(g_ws_mu);
-    for (Workspace &w : g_ws) {
-        if (w.device != device || w.stream != stream || w.kind != kind) continue;
-        if (w.bytes >= bytes) {
-            *out = w.ptr;
-            return NXT_ATTN_OK;
-        }
-        hipError_t e = hipStreamSynchronize(stream);
-        if (e != hipSuccess)
-            return set_status(NXT_ATTN_E_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
-        (void)hipFree(w.ptr);
-        w.ptr = nullptr;
-        w.bytes = 0;
-        e = hipMalloc(&w.ptr, bytes);
-        if (e != hipSuccess) {
-            w.ptr = nullptr;
-            return set_status(NXT_ATTN_E_NOMEM, "split-K workspace of %zu bytes: %s", bytes,
-                              hipGetErrorString(e));
-        }
-        w.bytes = bytes;
-        *out = w.ptr;
-        return NXT_ATTN_OK;
-    }
-    Workspace w{device, stream, kind, nullptr, 0};
-    hipError_t e = hipMalloc(&w.ptr, bytes);
-    if (e != hipSuccess)
-        return set_status(NXT_ATTN_E_NOMEM, "split-K workspace of %zu bytes: %s", bytes,
-                          hipGetErrorString(e));
-    w.bytes = bytes;
-    g_ws.push_back(w);
-    *out = w.ptr;
+// Takes (device, stream, kind)'s workspace of at least `bytes` for one call;
+// it stays locked to this thread until `lease` is destroyed, after the
+// call's launches are enqueued.
+int get_workspace(int device, hipStream_t stream, size_t bytes, WsCache::Lease *lease,
+                  int kind = kWsSplitK) {
+    const int rc = g_ws.acquire(device, (void *)stream, kind, bytes, t_ws_owner, lease);
+    if (rc == WsCache::kSyncFailed)
+        return set_status(NXT_ATTN_E_HIP, "hipStreamSynchronize before growing the workspace failed");
+    if (rc == WsCache::kNoMemory)
+        return set_status(NXT_ATTN_E_NOMEM, "workspace of %zu bytes: hipMalloc failed", bytes);
     return NXT_ATTN_OK;
 }
 
@@ -182,8 +178,10 @@ bool head_tiling(int group, bool mfma, int head_size, HeadTiling *t) {
         t->head_tiles = 1;
         return true;
     }
+    // ceil, not a power of two: every head tile holds at least one head (a
+    // tile past the group would be a segment with no columns to merge)
     t->head_tile = xhip::kMaxHeadTile;
-    t->head_tiles = pow2_ceil((group + xhip::kMaxHeadTile - 1) / xhip::kMaxHeadTile);
+    t->head_tiles = (group + xhip::kMaxHeadTile - 1) / xhip::kMaxHeadTile;
     return t->head_tiles <= xhip::kWavesPerGroup;
 }
 
@@ -370,9 +368,10 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         const size_t o_bytes = (slots * head_size * sizeof(float) + 255) & ~(size_t)255;
         const size_t ml_bytes = (slots * 2 * sizeof(float) + 255) & ~(size_t)255;
         const size_t pre_bytes = (size_t)(nseq + 1) * sizeof(int);
-        void *ws = nullptr;
-        int st = get_workspace(device, stream, o_bytes + ml_bytes + pre_bytes, &ws);
+        WsCache::Lease lease;  // held until this chunk's launches are enqueued
+        int st = get_workspace(device, stream, o_bytes + ml_bytes + pre_bytes, &lease);
         if (st != NXT_ATTN_OK) return st;
+        void *ws = lease.ptr();
 
         const size_t row0 = (size_t)s0 * num_heads * head_size * eb_total;
         DecodeParams p;
@@ -510,10 +509,11 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
     hipError_t e = hipGetDevice(&device);
     if (e != hipSuccess) return set_status(NXT_ATTN_E_HIP, "hipGetDevice: %s", hipGetErrorString(e));
     hipStream_t stream = (hipStream_t)stream_handle;
-    void *ws = nullptr;
-    int st = get_workspace(device, stream, off, &ws, kWsCascade);
+    // held over the plan and both passes (they read what the plan wrote)
+    WsCache::Lease lease;
+    int st = get_workspace(device, stream, off, &lease, kWsCascade);
     if (st != NXT_ATTN_OK) return st;
-    char *w = (char *)ws;
+    char *w = (char *)lease.ptr();
     xhip::CascadeParams c;
     memset(&c, 0, sizeof(c));
     c.block_tables = block_tables;
@@ -842,8 +842,17 @@ __attribute__((visibility("default"))) int nxt_paged_attention_cascade(
     if (st != NXT_ATTN_OK) return st;
     if (num_seqs < 0) return set_status(NXT_ATTN_E_INVALID, "num_seqs %d < 0", num_seqs);
     if (num_seqs == 0) return ok();
-    if (((uintptr_t)out | (uintptr_t)query) & 15)
+    // the checks run() makes only for a non-empty batch: the cascade plan
+    // reads these arrays before any pass of run() is reached
+    if (!out || !query || !key_cache || !value_cache || !block_tables || !seq_lens)
+        return set_status(NXT_ATTN_E_INVALID, "NULL tensor pointer");
+    if (max_groups > 0 && (!prefix_group || !prefix_blocks))
+        return set_status(NXT_ATTN_E_INVALID, "NULL prefix_group / prefix_blocks");
+    if (((uintptr_t)out | (uintptr_t)query | (uintptr_t)key_cache | (uintptr_t)value_cache) & 15)
         return set_status(NXT_ATTN_E_UNSUPPORTED, "tensors must be 16-byte aligned");
+    if (((uintptr_t)block_tables | (uintptr_t)seq_lens | (uintptr_t)prefix_group |
+         (uintptr_t)prefix_blocks) & 3)
+        return set_status(NXT_ATTN_E_INVALID, "int32 arrays must be 4-byte aligned");
     return cascade_run(out, query, key_cache, value_cache, block_tables, seq_lens, prefix_group,
                        prefix_blocks, max_groups, num_seqs, num_heads, head_size, num_kv_heads,
                        scale, max_num_blocks_per_seq, block_size, kv_block_stride,
@@ -882,20 +891,21 @@ __attribute__((visibility("default"))) void nxt_attn_set_trace_events(void *star
 }
 
 __attribute__((visibility("default"))) int nxt_attn_release_workspaces(void) {
-    std::lock_guard<std::mutex> lock(g_ws_mu);
-    int rc = NXT_ATTN_OK;
-    for (Workspace &w : g_ws) {
-        int cur = 0;
-        if (hipGetDevice(&cur) == hipSuccess && hipSetDevice(w.device) == hipSuccess) {
-            if (hipDeviceSynchronize() != hipSuccess) rc = NXT_ATTN_E_HIP;
-            if (hipFree(w.ptr) != hipSuccess) rc = NXT_ATTN_E_HIP;
-            (void)hipSetDevice(cur);
-        } else {
-            rc = NXT_ATTN_E_HIP;
-        }
-    }
-    g_ws.clear();
-    return rc;
+    return g_ws.release_owner(nullptr, true) == WsCache::kOk ? NXT_ATTN_OK : NXT_ATTN_E_HIP;
+}
+
+const void *xhip_set_workspace_owner(const void *owner) {
+    const void *prev = t_ws_owner;
+    t_ws_owner = owner;
+    return prev;
+}
+
+int xhip_release_owner_workspaces(const void *owner) {
+    return g_ws.release_owner(owner) == WsCache::kOk ? 0 : -1;
+}
+
+int xhip_release_stream_workspaces(int device, void *stream) {
+    return g_ws.release_stream(device, stream) == WsCache::kOk ? 0 : -1;
 }
 
 __attribute__((visibility("default"))) const char *nxt_attn_version(void) {

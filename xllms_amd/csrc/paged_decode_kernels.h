@@ -823,6 +823,9 @@ __global__ __launch_bounds__(NT) void paged_decode_merge_segment_kernel(const De
     const int g0 = (seg - kvh * p.head_tiles) * GT;
     const int nh = min(GT, p.group - g0);
     const int ncols = nh * C4;
+    // a head tile with no heads has nothing to merge (the host never plans
+    // one; the column-span loop below needs ncols >= 1 to end)
+    if (ncols <= 0) return;
     const int tid = threadIdx.x;
     // the three scalars the merge needs, requested together (the empty asm
     // keeps the compiler from sinking the prefix loads past the L == 0 exit,

@@ -53,7 +53,7 @@ struct DecodeParams {
     int num_heads;
     int num_kv_heads;
     int group;                 // num_heads / num_kv_heads
-    int head_tiles;            // ceil(group / head tile), 1, 2 or 4
+    int head_tiles;            // ceil(group / head tile), 1 to 4
     int max_blocks;            // block-table row length
     int block_size;
     int bs_shift;              // log2(block_size)
