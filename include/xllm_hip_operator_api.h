@@ -117,6 +117,26 @@ int nxt_paged_attention_ex(void *out, const void *query, const void *key_cache,
                            int kv_block_stride, int kv_head_stride, nxt_stream_t stream,
                            int kv_dtype, int partition_tokens);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments, checks and result as
+ * nxt_paged_attention_ex, but the split-K partials live in a fixed per-device
+ * scratch array of 66 MiB that the library holds until the process ends,
+ * instead of the library's per-stream workspace: the call makes no hipMalloc
+ * or hipFree.  Every automatic plan (partition_tokens = 0) fits on a 256-CU
+ * MI355X, so results equal nxt_paged_attention_ex's bit for bit; a plan
+ * that needs more scratch (an explicit partition_tokens over a large batch)
+ * returns NXT_ATTN_E_UNSUPPORTED without launching.  Every
+ * call on one device shares that device's scratch: calls that overlap on one
+ * device (other streams or threads) race, so serialize them. */
+int nxt_paged_attention_noalloc(void *out, const void *query, const void *key_cache,
+                                const void *value_cache, const int *block_tables,
+                                const int *seq_lens, int num_seqs, int num_heads,
+                                int head_size, int num_kv_heads, float scale,
+                                int max_num_blocks_per_seq, int block_size, int dtype_size,
+                                int kv_block_stride, int kv_head_stride, nxt_stream_t stream,
+                                int kv_dtype, int partition_tokens);
+
 /* Wavefronts the automatic split-K plan launches for this shape (needs a
  * current HIP device for its CU count and the kernel occupancy), or a
  * negative status. */

@@ -48,6 +48,7 @@ OPERATOR_SYMBOLS = (
     "nxt_paged_attention_v2",
     "nxt_paged_attention_flash",
     "nxt_paged_attention_ex",
+    "nxt_paged_attention_noalloc",
     "nxt_paged_attention_auto_waves",
     "nxt_attn_last_status",
     "nxt_attn_last_error",
@@ -96,6 +97,8 @@ def backend() -> ctypes.CDLL:
             fn.restype = None
         lib.nxt_paged_attention_ex.argtypes = _LEGACY_ARGS + [c_int, c_int]
         lib.nxt_paged_attention_ex.restype = c_int
+        lib.nxt_paged_attention_noalloc.argtypes = _LEGACY_ARGS + [c_int, c_int]
+        lib.nxt_paged_attention_noalloc.restype = c_int
         lib.nxt_paged_attention_auto_waves.argtypes = [c_int] * 7
         lib.nxt_paged_attention_auto_waves.restype = c_int
         lib.nxt_attn_last_status.argtypes = []

@@ -18,6 +18,7 @@
 #include "paged_decode_cascade.h"
 #include "paged_decode_launch.h"
 #include "paged_decode_params.h"
+#include "paged_decode_scratch.h"
 #include "paged_kv_append.h"
 #include "workspace.h"
 #include "workspace_cache.h"
@@ -261,11 +262,19 @@ struct PrefixFold {
     int rows, kr;
 };
 
+// A caller-provided split-K workspace (the allocation-free entry point's
+// fixed device scratch) used instead of the workspace cache.
+struct FixedWs {
+    void *ptr;
+    size_t bytes;
+};
+
 int run(void *out, const void *query, const void *key_cache, const void *value_cache,
         const int *block_tables, const int *seq_lens, int num_seqs, int num_heads, int head_size,
         int num_kv_heads, float scale, int max_num_blocks_per_seq, int block_size, int dtype_size,
         int kv_block_stride, int kv_head_stride, nxt_stream_t stream_handle, int kv_dtype,
-        int partition_tokens, const PartialOut *po = nullptr, const PrefixFold *fold = nullptr) {
+        int partition_tokens, const PartialOut *po = nullptr, const PrefixFold *fold = nullptr,
+        const FixedWs *fixed = nullptr) {
     // ---- argument checks (host only; nothing is read from the device)
     if (kv_dtype != NXT_KV_FP16 && kv_dtype != NXT_KV_BF16 && kv_dtype != NXT_KV_FP32)
         return set_status(NXT_ATTN_E_UNSUPPORTED, "kv_dtype %d is not FP16/BF16/FP32", kv_dtype);
@@ -364,14 +373,32 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         }
 
         const size_t eb_total = (size_t)elem_bytes(kv_dtype);
-        const size_t slots = (size_t)waves * 2 * tiling.head_tile;
-        const size_t o_bytes = (slots * head_size * sizeof(float) + 255) & ~(size_t)255;
-        const size_t ml_bytes = (slots * 2 * sizeof(float) + 255) & ~(size_t)255;
+        // workspace: fp32 partials o, their (m, l), the unit prefix
         const size_t pre_bytes = (size_t)(nseq + 1) * sizeof(int);
+        auto o_size = [&](long long w) {
+            return ((size_t)w * 2 * tiling.head_tile * head_size * sizeof(float) + 255) &
+                   ~(size_t)255;
+        };
+        auto ml_size = [&](long long w) {
+            return ((size_t)w * 2 * tiling.head_tile * 2 * sizeof(float) + 255) & ~(size_t)255;
+        };
+        if (fixed && o_size(waves) + ml_size(waves) + pre_bytes > fixed->bytes)
+            return set_status(NXT_ATTN_E_UNSUPPORTED,
+                              "this plan needs %zu bytes of split-K scratch; the allocation-free "
+                              "entry point has %zu%s",
+                              o_size(waves) + ml_size(waves) + pre_bytes, fixed->bytes,
+                              partition_tokens ? " (raise partition_tokens)" : "");
+        const size_t o_bytes = o_size(waves);
+        const size_t ml_bytes = ml_size(waves);
         WsCache::Lease lease;  // held until this chunk's launches are enqueued
-        int st = get_workspace(device, stream, o_bytes + ml_bytes + pre_bytes, &lease);
-        if (st != NXT_ATTN_OK) return st;
-        void *ws = lease.ptr();
+        void *ws = nullptr;
+        if (fixed) {
+            ws = fixed->ptr;  // launches of one stream run in order: chunks reuse it
+        } else {
+            int st = get_workspace(device, stream, o_bytes + ml_bytes + pre_bytes, &lease);
+            if (st != NXT_ATTN_OK) return st;
+            ws = lease.ptr();
+        }
 
         const size_t row0 = (size_t)s0 * num_heads * head_size * eb_total;
         DecodeParams p;
@@ -752,6 +779,34 @@ __attribute__((visibility("default"))) int nxt_paged_attention_ex(
     return run(out, query, key_cache, value_cache, block_tables, seq_lens, num_seqs, num_heads,
                head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size, dtype_size,
                kv_block_stride, kv_head_stride, stream, kv_dtype, partition_tokens);
+}
+
+__attribute__((visibility("default"))) int nxt_paged_attention_noalloc(
+    void *out, const void *query, const void *key_cache, const void *value_cache,
+    const int *block_tables, const int *seq_lens, int num_seqs, int num_heads, int head_size,
+    int num_kv_heads, float scale, int max_num_blocks_per_seq, int block_size, int dtype_size,
+    int kv_block_stride, int kv_head_stride, nxt_stream_t stream, int kv_dtype,
+    int partition_tokens) {
+    // shape checks before the scratch lookup (pointer checks follow in the
+    // real run, still before any launch)
+    if (num_seqs < 0) return set_status(NXT_ATTN_E_INVALID, "num_seqs %d < 0", num_seqs);
+    const int st = run(out, query, key_cache, value_cache, block_tables, seq_lens, 0, num_heads,
+                       head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size,
+                       dtype_size, kv_block_stride, kv_head_stride, stream, kv_dtype,
+                       partition_tokens);
+    if (st != NXT_ATTN_OK || num_seqs == 0) return st;
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return set_status(NXT_ATTN_E_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    FixedWs fixed{nullptr, 0};
+    e = xhip::noalloc_scratch(device, &fixed.ptr, &fixed.bytes);
+    if (e != hipSuccess)
+        return set_status(NXT_ATTN_E_HIP, "scratch address of device %d: %s", device,
+                          hipGetErrorString(e));
+    return run(out, query, key_cache, value_cache, block_tables, seq_lens, num_seqs, num_heads,
+               head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size, dtype_size,
+               kv_block_stride, kv_head_stride, stream, kv_dtype, partition_tokens, nullptr,
+               nullptr, &fixed);
 }
 
 __attribute__((visibility("default"))) int nxt_paged_attention_auto_waves(
