@@ -17,6 +17,12 @@ Prints ONE JSON line:
                K timed steps that give `value`), against 8 TB/s;
                `traffic` = HBM bytes per launch from the committed rocprofv3
                PMC summary for this workload (profiles/), else null
+               step_frac: algorithmic bytes / whole step time (partition and merge
+               launches, back to back), against 8 TB/s
+  measured_peak the ceilings measured in the same run: the batch's own K/V
+               tiles streamed with the kernel's loads and no arithmetic
+               (xllm_stream_probe), and a plain 1 GiB device copy; the kernel's
+               and the step's rate as fractions of the former
   cpu_baseline the oracle (C restatement of the reference CPU attention)
                on the host cores, all threads; single-thread figure alongside
 """
@@ -88,6 +94,110 @@ def load_traffic(workload_name: str):
     with open(path) as f:
         d = json.load(f)
     return d.get("hbm_bytes_per_launch")
+
+
+def tile_descriptors(wl, distinct: bool = False):
+    """The batch's 16-token K/V tiles in the decode's order (sequence, kv
+    head, tile) as xllm_stream_probe descriptors: byte offset << 5 | valid
+    rows.  distinct: each (physical page, kv head) once, with the most valid
+    rows any sequence reads from it (the compulsory tiles of a shared-prefix
+    batch)."""
+    import numpy as np
+    bs, eb, D = wl.block_size, wl.elem_bytes, wl.head_size
+    if bs != 16:
+        return None
+    seen = {}
+    parts = []
+    for s, L in enumerate(wl.seq_lens):
+        L = int(L)
+        nt = -(-L // 16)
+        if nt == 0:
+            continue
+        blk = wl.block_tables[s, :nt].astype(np.int64)
+        rows = np.minimum(16, L - 16 * np.arange(nt)).astype(np.int64)
+        keep = blk >= 0
+        blk, rows = blk[keep], rows[keep]
+        if distinct:
+            for b, r in zip(blk.tolist(), rows.tolist()):
+                seen[b] = max(seen.get(b, 0), r)
+            continue
+        for h in range(wl.num_kv_heads):
+            off = (blk * wl.kv_block_stride + h * wl.kv_head_stride) * eb
+            parts.append((off << 5) | rows)
+    if distinct:
+        blk = np.array(sorted(seen), dtype=np.int64)
+        rows = np.array([seen[b] for b in blk.tolist()], dtype=np.int64)
+        for h in range(wl.num_kv_heads):
+            off = (blk * wl.kv_block_stride + h * wl.kv_head_stride) * eb
+            parts.append((off << 5) | rows)
+    desc = np.concatenate(parts) if parts else np.zeros(0, dtype=np.int64)
+    kv_bytes = int((desc & 31).sum()) * D * eb * 2
+    return desc, kv_bytes
+
+
+def pattern_peak(wl, kpools, vpools, waves: int, steps: int, distinct: bool = False):
+    """Rate at which this batch's K/V tiles stream with the decode kernel's
+    access pattern and no arithmetic (xllm_stream_probe over the same pools,
+    rotated like the timed steps): GB/s of K/V bytes, or None."""
+    import torch
+    from xllms_amd import _lib
+    tb = 16 * wl.head_size * wl.elem_bytes
+    got = tile_descriptors(wl, distinct)
+    if got is None or tb not in (1024, 2048, 4096):
+        return None
+    desc, kv_bytes = got
+    lib = _lib.stream_probe()
+    d_desc = torch.from_numpy(desc).to("cuda")
+    sink = torch.empty(waves * 64, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch(i):
+        rc = lib.xllm_stream_probe(kpools[i % len(kpools)].data_ptr(),
+                                   vpools[i % len(vpools)].data_ptr(), d_desc.data_ptr(),
+                                   int(desc.size), tb, waves, sink.data_ptr(), stream)
+        if rc != 0:
+            raise RuntimeError("xllm_stream_probe failed")
+
+    for i in range(20):
+        launch(i)
+    ev = HipEvents()
+    a, b = ev.create(), ev.create()
+    torch.cuda.synchronize()
+    ev.record(a, stream)
+    for i in range(steps):
+        launch(i)
+    ev.record(b, stream)
+    torch.cuda.synchronize()
+    ms = ev.elapsed_ms(a, b) / steps
+    ev.destroy_all()
+    return {"gbs": round(kv_bytes / (ms / 1e3) / 1e9, 1), "us": round(ms * 1e3, 2),
+            "kv_bytes": kv_bytes, "tiles": int(desc.size), "waves": waves}
+
+
+def device_copy_peak(mib: int = 1024, steps: int = 10) -> dict:
+    """A plain device-to-device copy (torch copy_, the runtime's copy kernel)
+    of `mib` MiB: bytes read + written per second."""
+    import torch
+    n = mib * 2**20 // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    stream = torch.cuda.current_stream().cuda_stream
+    ev = HipEvents()
+    a, b = ev.create(), ev.create()
+    torch.cuda.synchronize()
+    ev.record(a, stream)
+    for _ in range(steps):
+        dst.copy_(src)
+    ev.record(b, stream)
+    torch.cuda.synchronize()
+    ms = ev.elapsed_ms(a, b) / steps
+    ev.destroy_all()
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"gbs": round(2 * n * 4 / (ms / 1e3) / 1e9, 1), "bytes_moved": 2 * n * 4,
+            "us": round(ms * 1e3, 2)}
 
 
 def partition_kernel_name(wl) -> str:
@@ -435,6 +545,10 @@ def main() -> int:
                     help="instead of the attention, time this MLP activation (reference entry "
                          "point, fp16, Llama-3-8B intermediate size 14336) over --act-tokens")
     ap.add_argument("--act-tokens", type=int, default=8192)
+    ap.add_argument("--copy-peak", action="store_true",
+                    help="instead of the benchmark, measure the ceilings the roofline fraction "
+                         "is read against: a plain 1 GiB device copy and the workload's K/V "
+                         "access pattern streamed with no arithmetic (xllm_stream_probe)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run 5 plain device copies of MIB MiB "
                          "(the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -497,6 +611,19 @@ def main() -> int:
     entry = "nxt_paged_attention" if args.partition == 0 and wl.kv_dtype != W.BF16 else None
     waves = PA.auto_waves(wl.num_seqs, wl.num_heads, wl.head_size, wl.num_kv_heads,
                           wl.max_num_blocks_per_seq, wl.block_size, wl.kv_dtype)
+
+    if args.copy_peak:
+        probe = pattern_peak(wl, kpools, vpools, waves, args.steps, distinct=args.cascade)
+        copy = device_copy_peak()
+        log(f"[bench] access-pattern probe {probe}; device copy {copy}")
+        print(json.dumps({"workload": wl.name, "hbm_spec_gbs": HBM_PEAK_GBS,
+                          "pattern_read": probe, "device_copy": copy,
+                          "note": "pattern_read: this batch's K/V tiles streamed with the "
+                                  "decode kernel's loads (16-byte nontemporal, one tile in "
+                                  "flight, same wavefront count) and no arithmetic; "
+                                  "device_copy: read + write bytes of a 1 GiB copy"}),
+              flush=True)
+        return 0
 
     # Pre-marshalled arguments: the timed loop is one ctypes call per step.
     fn = getattr(lib, entry) if entry else lib.nxt_paged_attention_ex
@@ -610,7 +737,23 @@ def main() -> int:
                "tokens_per_seq": round(tok_per_seq, 1)}
         log(f"[bench] cpu baseline: {cpu}")
 
-    traffic = load_traffic(wl.name)
+    # The ceilings the kernel is read against, measured in this run: the
+    # batch's own K/V access pattern with no arithmetic, and a plain copy.
+    probe = pattern_peak(wl, kpools, vpools, waves, 50, distinct=args.cascade)
+    copy = device_copy_peak()
+    step_gbs = alg_bytes / (ms_per_step / 1e3) / 1e9
+    measured_peak = {
+        "pattern_read_gbs": probe["gbs"] if probe else None,
+        "pattern_read": ("the batch's compulsory K/V tiles" if args.cascade else
+                         "the batch's K/V tiles") + " streamed with the decode kernel's loads and "
+                         "wavefront count, no arithmetic (xllm_stream_probe)",
+        "device_copy_gbs": copy["gbs"],
+        "kernel_frac_of_pattern": round(achieved / probe["gbs"], 4) if probe else None,
+        "step_frac_of_pattern": round(step_gbs / probe["gbs"], 4) if probe else None,
+    }
+    log(f"[bench] measured ceilings: {measured_peak}")
+
+    traffic = load_traffic(wl.name + ("_cascade" if args.cascade else ""))
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -637,10 +780,12 @@ def main() -> int:
         "logical_bytes": logical_bytes,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None if args.cascade else traffic,
+                     "step_frac": round(step_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic,
                      "kernel": ("cascade decode step (plan, prefix and suffix partition + merge, "
                                 "combine)") if args.cascade else partition_kernel_name(wl),
                      "kernel_avg_us": round(kernel_avg_ms * 1e3, 2)},
+        "measured_peak": measured_peak,
         "cpu_baseline": cpu,
         "check": check,
     }

@@ -14,6 +14,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(_HERE, "lib")
 BACKEND_SO = os.path.join(LIB_DIR, "libxllm_hip_backend.so")
 WORKLOAD_SO = os.path.join(LIB_DIR, "libxllm_workload.so")
+STREAM_PROBE_SO = os.path.join(LIB_DIR, "libxllm_stream_probe.so")
 
 _lock = threading.Lock()
 _cache: dict[str, ctypes.CDLL] = {}
@@ -185,5 +186,16 @@ def workload() -> ctypes.CDLL:
         lib.xw_float_to_bf16.restype = ctypes.c_uint16
         lib.xw_num_threads.argtypes = []
         lib.xw_num_threads.restype = c_int
+        lib._xllm_typed = True
+    return lib
+
+
+def stream_probe() -> ctypes.CDLL:
+    """The read-only K/V access-pattern probe (measurement tool of bench.py)."""
+    lib = _load(STREAM_PROBE_SO)
+    if not getattr(lib, "_xllm_typed", False):
+        lib.xllm_stream_probe.argtypes = [c_void_p, c_void_p, c_void_p, ctypes.c_longlong, c_int,
+                                          c_int, c_void_p, c_void_p]
+        lib.xllm_stream_probe.restype = c_int
         lib._xllm_typed = True
     return lib
