@@ -161,11 +161,33 @@ __device__ __forceinline__ void chunk_to_float(u32x4 v, float (&f)[VEC]) {
     }
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 values narrowed to the 16-bit type, round to nearest even (NaN
+// stays NaN), packed low = a, high = b: one v_cvt_pk_{f16,bf16}_f32 on
+// gfx950 (a software bf16 rounding with a NaN test compiled to divergent
+// branches and made the bf16 kernels issue ~25% more instructions).
+template <int KV> __device__ __forceinline__ uint32_t pack16(float a, float b) {
+    const f32x2 v = {a, b};
+    if constexpr (KV == KV_F16)
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+    else
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+// The two fp32 values a packed pair of the 16-bit type holds (exact).
+template <int KV> __device__ __forceinline__ f32x2 unpack16(uint32_t w) {
+    if constexpr (KV == KV_F16) {
+        const f16x2 h = __builtin_bit_cast(f16x2, w);
+        return f32x2{(float)h.x, (float)h.y};
+    } else {
+        return f32x2{__builtin_bit_cast(float, w << 16), __builtin_bit_cast(float, w & 0xFFFF0000u)};
+    }
+}
+
 // fp32 -> bf16 bits, round to nearest even (NaN stays NaN).
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
-    uint32_t u = __builtin_bit_cast(uint32_t, x);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x);
 }
 
 // Narrow VEC fp32 values to one 16-byte chunk of the element type (RNE).
@@ -173,16 +195,10 @@ template <int KV, int VEC> __device__ __forceinline__ u32x4 float_to_chunk(const
     u32x4 r;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        if constexpr (KV == KV_F16) {
-            f16x2 h;
-            h.x = (_Float16)f[2 * i];
-            h.y = (_Float16)f[2 * i + 1];
-            r[i] = __builtin_bit_cast(uint32_t, h);
-        } else if constexpr (KV == KV_BF16) {
-            r[i] = f32_to_bf16_bits(f[2 * i]) | (f32_to_bf16_bits(f[2 * i + 1]) << 16);
-        } else {
+        if constexpr (KV == KV_F32)
             r[i] = __builtin_bit_cast(uint32_t, f[i]);
-        }
+        else
+            r[i] = pack16<KV>(f[2 * i], f[2 * i + 1]);
     }
     return r;
 }
@@ -633,19 +649,53 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
     });
 }
 
-typedef float f32x2 __attribute__((ext_vector_type(2)));
+// The slots of a cut segment's partials: partial 0 in slot s0, partial
+// j >= 1 in slot sb + sstride * j.
+struct PartialSlots {
+    size_t s0, sb;
+    int sstride, np;
+};
+
+// The partials of the segment whose first tile is split unit first_tile
+// (Ts tiles, starting at unit seg_start) under a plan of tpw units per
+// wavefront; false when the partition kernel finished it (it lay in one
+// wavefront's range, or in one workgroup's under wg_fix).
+template <int WPG>
+__device__ __forceinline__ bool segment_partials(const DecodeParams &p, int seg_start,
+                                                 int first_tile, int Ts, int tpw,
+                                                 PartialSlots &ps) {
+    const int w_first = first_tile / tpw;
+    const int w_last = (first_tile + Ts - 1) / tpw;
+    // the segment is w_first's first piece when w_first's range begins in the
+    // segment's start-up units or at its first tile
+    const int slot0 = (w_first * tpw >= seg_start) ? 0 : 1;
+    ps.s0 = (size_t)w_first * 2 + slot0;
+    if (p.wg_fix) {
+        const int wg0 = w_first / WPG, wg1 = w_last / WPG;
+        if (wg0 == wg1) return false;
+        ps.np = wg1 - wg0 + 1;
+        ps.sb = (size_t)wg0 * 2 * WPG;
+        ps.sstride = 2 * WPG;
+    } else {
+        if (w_first == w_last) return false;
+        ps.np = w_last - w_first + 1;
+        ps.sb = (size_t)w_first * 2;
+        ps.sstride = 2;
+    }
+    return true;
+}
 
 // Online log-sum-exp merge, into (m, l, acc) of one float4 column, of a
-// segment's partials j = j0, j0 + step, ... < np (partial j in slot
-// sbase + 2j + (j == 0 ? slot0 : 0)).  The partials go in batches of up to
-// NB whose loads are all issued before any is used, so a thread waits for
-// one memory round trip per batch, not per partial; batch slots past np
-// load and combine nothing.  The column's (m, l) and float4 of o sit at
-// off_ml and off_o floats into a slot.
+// segment's partials j = j0, j0 + step, ... < np (slots as in PartialSlots).
+// The partials go in batches of up to NB whose loads are all issued before
+// any is used, so a thread waits for one memory round trip per batch, not
+// per partial; batch slots past np load and combine nothing.  The column's
+// (m, l) and float4 of o sit at off_ml and off_o floats into a slot.
 template <int GT, int D, int NB>
-__device__ __forceinline__ void merge_partials(const DecodeParams &p, size_t sbase, int slot0,
-                                               int j0, int step, int np, int off_ml, int off_o,
+__device__ __forceinline__ void merge_partials(const DecodeParams &p, const PartialSlots &ps,
+                                               int j0, int step, int off_ml, int off_o,
                                                float &m, float &l, f32x4 &acc) {
+    const int np = ps.np;
     for (int jb = j0; jb < np; jb += NB * step) {
         f32x2 mlv[NB];
         f32x4 ov[NB];
@@ -655,7 +705,7 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p, size_t sba
             mlv[b] = f32x2{-INFINITY, 0.0f};  // (defined values for the slots left unread)
             ov[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             if (j < np) {
-                const size_t slot = sbase + 2 * (size_t)j + (j == 0 ? slot0 : 0);
+                const size_t slot = j == 0 ? ps.s0 : ps.sb + (size_t)ps.sstride * j;
                 mlv[b] = *(const f32x2 *)(p.ws_ml + slot * GT * 2 + off_ml);
                 ov[b] = *(const f32x4 *)(p.ws_o + slot * GT * D + off_o);
             }
@@ -749,31 +799,24 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
     const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);
     const int Ts = (L + TT - 1) / TT;
     const int seg_start = pre_s + seg * segment_units(p, Ts);  // in split units
-    const int first_tile = seg_start + p.seg_cost;
-    const int w_first = first_tile / tpw;
-    const int w_last = (first_tile + Ts - 1) / tpw;
-    if (w_first == w_last) return;
-    const int np = w_last - w_first + 1;
-    // the segment is w_first's first piece when w_first's range begins in the
-    // segment's start-up units or at its first tile
-    const int slot0 = (w_first * tpw >= seg_start) ? 0 : 1;
-    // partial j of the segment lives in slot (w_first + j)*2 + (j == 0 ? slot0 : 0)
-    const size_t sbase = (size_t)w_first * 2;
+    PartialSlots ps;
+    if (!segment_partials<kMfmaWavesPerGroup>(p, seg_start, seg_start + p.seg_cost, Ts, tpw, ps))
+        return;
 
     const int cl = tid % kMergeCols;
-    const int ps = tid / kMergeCols;
+    const int psplit = tid / kMergeCols;
     const int col = col0 + cl;
     const bool active = col < ncols;
     const int h = active ? col / C4 : 0;
     const int c = active ? col - h * C4 : 0;
     float m = -INFINITY, l = 0.0f;
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (active) merge_partials<GT, D, 8>(p, sbase, slot0, ps, kMergeSplit, np, h * 2, h * D + c * 4, m, l, acc);
-    s_acc[ps][cl] = acc;
-    s_m[ps][cl] = m;
-    s_l[ps][cl] = l;
+    if (active) merge_partials<GT, D, 8>(p, ps, psplit, kMergeSplit, h * 2, h * D + c * 4, m, l, acc);
+    s_acc[psplit][cl] = acc;
+    s_m[psplit][cl] = m;
+    s_l[psplit][cl] = l;
     __syncthreads();
-    if (ps != 0 || !active) return;
+    if (psplit != 0 || !active) return;
     float mm = m, ll = l;
     f32x4 aa = acc;
 #pragma unroll
@@ -844,15 +887,9 @@ __global__ __launch_bounds__(NT) void paged_decode_merge_segment_kernel(const De
     const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);
     const int Ts = (L + TT - 1) / TT;
     const int seg_start = pre_s + seg * segment_units(p, Ts);  // in split units
-    const int first_tile = seg_start + p.seg_cost;
-    const int w_first = first_tile / tpw;
-    const int w_last = (first_tile + Ts - 1) / tpw;
-    if (w_first == w_last) return;
-    const int np = w_last - w_first + 1;
-    // the segment is w_first's first piece when w_first's range begins in the
-    // segment's start-up units or at its first tile
-    const int slot0 = (w_first * tpw >= seg_start) ? 0 : 1;
-    const size_t sbase = (size_t)w_first * 2;
+    PartialSlots ps;
+    if (!segment_partials<kMfmaWavesPerGroup>(p, seg_start, seg_start + p.seg_cost, Ts, tpw, ps))
+        return;
 
     // Column span per split: all NT threads when ncols > NT / 2, else pow2(ncols).
     int span = NT;
@@ -865,8 +902,7 @@ __global__ __launch_bounds__(NT) void paged_decode_merge_segment_kernel(const De
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     if (cl < ncols) {
         const int h = cl / C4;
-        merge_partials<GT, D, 8>(p, sbase, slot0, split, nsplit, np, h * 2, h * D + (cl - h * C4) * 4,
-                                 m, l, acc);
+        merge_partials<GT, D, 8>(p, ps, split, nsplit, h * 2, h * D + (cl - h * C4) * 4, m, l, acc);
     }
     if (nsplit > 1) {  // ncols <= NT / 2: fewer than 64 columns, or a partly filled last head tile
         s_acc[tid] = acc;

@@ -69,18 +69,6 @@ template <int KV> __device__ __forceinline__ f32x4 mfma_pv(u32x2 a, u32x2 b, f32
                                                          __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
 }
 
-// Round fp32 to the 16-bit type (RNE); returns the bits and the rounded value.
-template <int KV> __device__ __forceinline__ uint32_t round16(float x, float &rounded) {
-    if constexpr (KV == KV_F16) {
-        const _Float16 h = (_Float16)x;
-        rounded = (float)h;
-        return (uint32_t)__builtin_bit_cast(uint16_t, h);
-    } else {
-        const uint32_t b = f32_to_bf16_bits(x);
-        rounded = __builtin_bit_cast(float, b << 16);
-        return b;
-    }
-}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const char *base) {
     return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7FFFFFFF, 0x00020000);
@@ -204,15 +192,12 @@ __device__ __forceinline__ void mfma_tile(const DecodeParams &p, const u32x4 (*q
         }
         st[b].l = st[b].l * alpha + psum;
         st[b].m = m_new;
-        uint32_t hb[4], lb[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float hv, lv;
-            hb[i] = round16<KV>(pe[i], hv);
-            lb[i] = round16<KV>(pe[i] - hv, lv);
-        }
-        p_hi[b] = u32x2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
-        p_lo[b] = u32x2{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
+        // P = hi + lo in the 16-bit type (lo = the exact fp32 remainder of hi)
+        const uint32_t h01 = pack16<KV>(pe[0], pe[1]), h23 = pack16<KV>(pe[2], pe[3]);
+        const f32x2 r01 = unpack16<KV>(h01), r23 = unpack16<KV>(h23);
+        p_hi[b] = u32x2{h01, h23};
+        p_lo[b] = u32x2{pack16<KV>(pe[0] - r01.x, pe[1] - r01.y),
+                        pack16<KV>(pe[2] - r23.x, pe[3] - r23.y)};
 #pragma unroll
         for (int n = 0; n < G::kDimBlocks; n++) st[b].o[n] *= alpha;
     }
@@ -240,7 +225,7 @@ __device__ __forceinline__ void mfma_tile(const DecodeParams &p, const u32x4 (*q
 // entire segment (the output is written directly); else its partial goes to
 // `slot`.  All fields are wavefront-uniform.
 struct MfmaPiece {
-    int s, kvh, ht, t_begin, t_end, whole, slot;
+    int s, kvh, ht, t_begin, t_end, L, whole, slot;
 };
 
 // Cursor over the pieces of one wavefront's range [g, g_end) of the batch's
@@ -279,6 +264,7 @@ __device__ __forceinline__ bool next_piece(const DecodeParams &p, const int *__r
         pc.ht = seg - pc.kvh * p.head_tiles;
         pc.t_begin = t0 * TT;
         pc.t_end = min(L, t1 * TT);
+        pc.L = L;
         pc.whole = t0 == 0 && t1 == Ts;
         pc.slot = c.w * 2 + (c.first ? 0 : 1);
         c.first = 0;
@@ -366,6 +352,98 @@ __device__ __forceinline__ int mfma_load_ids(const DecodeParams &p, const int *_
 
 namespace xhip {
 
+// Where a finished segment's rows go: its output rows (element type), or in
+// partial-output mode its fp32 rows and log-sum-exp.  st holds unreduced
+// per-lane sums (lane group g of head j); they are reduced here.
+template <int KV, int D, int R>
+__device__ __forceinline__ void mfma_write_rows(const DecodeParams &p, const MfmaPiece &pc,
+                                                int lane, const MfmaState<D> (&st)[R]) {
+    using G = MfmaGeometry<D>;
+    constexpr int GT = kMfmaHeads * R;
+    const int j = lane & 15, gq = lane >> 4;
+    const int g0 = pc.ht * GT;
+    const int nh = min(GT, p.group - g0);
+    const size_t qrow0 = ((size_t)pc.s * p.num_heads + (size_t)pc.kvh * p.group + g0) * D;
+#pragma unroll
+    for (int b = 0; b < R; b++) {
+        float l = st[b].l;
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+        const int hj = 16 * b + j;  // head of this lane in the tile
+        if (hj >= nh) continue;
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        if (p.out_f32) {
+            float *dst = p.out_f32 + qrow0 + (size_t)hj * D + 4 * gq;
+#pragma unroll
+            for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st[b].o[n] * inv;
+            if (gq == 0) p.out_lse[qrow0 / D + hj] = l > 0.0f ? st[b].m + log2f(l) : -INFINITY;
+        } else {
+            char *dst = (char *)p.out + (qrow0 + (size_t)hj * D + 4 * gq) * 2;
+#pragma unroll
+            for (int n = 0; n < G::kDimBlocks; n++) {
+                const f32x4 o = st[b].o[n] * inv;
+                *(u32x2 *)(dst + 32 * n) = u32x2{pack16<KV>(o[0], o[1]), pack16<KV>(o[2], o[3])};
+            }
+        }
+    }
+}
+
+// The fp32 partial (m, l, unnormalized o) of a cut segment's piece, in the
+// piece's slot of the split-K workspace.
+template <int D, int R>
+__device__ __forceinline__ void mfma_write_partial(const DecodeParams &p, const MfmaPiece &pc,
+                                                   int lane, const MfmaState<D> (&st)[R]) {
+    using G = MfmaGeometry<D>;
+    constexpr int GT = kMfmaHeads * R;
+    const int j = lane & 15, gq = lane >> 4;
+    const int nh = min(GT, p.group - pc.ht * GT);
+#pragma unroll
+    for (int b = 0; b < R; b++) {
+        float l = st[b].l;
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+        const int hj = 16 * b + j;
+        if (hj >= nh) continue;
+        float *dst = p.ws_o + ((size_t)pc.slot * GT + hj) * D + 4 * gq;
+#pragma unroll
+        for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st[b].o[n];
+        if (gq == 0) {
+            p.ws_ml[((size_t)pc.slot * GT + hj) * 2] = st[b].m;
+            p.ws_ml[((size_t)pc.slot * GT + hj) * 2 + 1] = l;
+        }
+    }
+}
+
+// LDS slot of one wavefront for the workgroup-level combine (mfma_wg_fixup):
+// a state in the lane layout of MfmaState (per-lane o, m and unreduced l),
+// so two states merge lane by lane.
+template <int D> struct MfmaFixSlot {
+    f32x4 o[MfmaGeometry<D>::kDimBlocks][64];
+    float m[64], l[64];
+    int ends;  // the state reaches the end of its segment
+};
+
+template <int D>
+__device__ __forceinline__ void fix_store(MfmaFixSlot<D> &slot, int lane, const MfmaState<D> &st) {
+#pragma unroll
+    for (int n = 0; n < MfmaGeometry<D>::kDimBlocks; n++) slot.o[n][lane] = st.o[n];
+    slot.m[lane] = st.m;
+    slot.l[lane] = st.l;
+}
+
+// st <- st (+) the state in slot (online log-sum-exp, per lane).
+template <int D>
+__device__ __forceinline__ void fix_absorb(const MfmaFixSlot<D> &slot, int lane, MfmaState<D> &st) {
+    const float mo = slot.m[lane];
+    const float M = fmaxf(st.m, mo);
+    const float Ms = (M == -INFINITY) ? 0.0f : M;
+    const float a = fast_exp2(st.m - Ms), b = fast_exp2(mo - Ms);
+    st.l = st.l * a + slot.l[lane] * b;
+#pragma unroll
+    for (int n = 0; n < MfmaGeometry<D>::kDimBlocks; n++) st.o[n] = st.o[n] * a + slot.o[n][lane] * b;
+    st.m = M;
+}
+
 // Partition kernel, MFMA tile path (head tile of 16R query heads).
 //
 // A wavefront walks the pieces of its stream-K range (usually one or two
@@ -378,6 +456,23 @@ namespace xhip {
 // average at config 2).  Q is loaded when its piece begins: requesting the
 // next piece's Q a piece early as well gained ~1% at configs 2-4 but cost 5%
 // (cascade) to 10% (plain decode) at config 5 (measured, same box).
+//
+// Cut segments (mfma_wg_fixup instantiations).  A piece that is not a whole
+// segment is cut at the start (it continues the previous wavefront's range),
+// at the end (the next wavefront continues it), or both.  Writing each such
+// piece's fp32 partial to memory put ~16-20 MB of stores at config 4b into
+// the wavefronts' critical paths (a cut first piece's stores delay the next
+// piece's loads, which share the memory counter; every wavefront ends with
+// one), measured at 8.6 us of a 76 us kernel.  Instead: a cut first piece
+// followed by more pieces goes to the wavefront's LDS slot; the last piece's
+// state stays in registers; at the end, from the workgroup's last wavefront
+// down to its first, a wavefront whose last piece continues into its right
+// neighbour absorbs that neighbour's slot, then either relays the merged
+// state to its own slot (its piece is a continuation from its left
+// neighbour) or, as the leftmost holder of the segment in the workgroup,
+// writes it: finished rows when the whole segment lay in the workgroup,
+// else one partial.  The first wavefront's cut first piece (its left
+// neighbour is in another workgroup) is written as a partial directly.
 template <int KV, int D, int R>
 __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partition_mfma_kernel(
     const DecodeParams p, const int *__restrict__ lens, const int *__restrict__ tables) {
@@ -385,25 +480,29 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
     // kernel arguments their wavefront-uniform reads become scalar loads,
     // which do not wait behind the K/V loads in flight.
     using G = MfmaGeometry<D>;
-    constexpr int GT = kMfmaHeads * R;
+    constexpr bool FIX = mfma_wg_fixup(kMfmaHeads * R, D);
+    constexpr int NW = kMfmaWavesPerGroup;
     extern __shared__ int pre[];  // num_seqs + 1 split-unit prefixes
-    __shared__ __attribute__((aligned(16))) char vtile[kMfmaWavesPerGroup][G::kLdsTile];
+    __shared__ __attribute__((aligned(16))) char vtile[NW][G::kLdsTile];
+    __shared__ MfmaFixSlot<D> fix[FIX ? NW : 1];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     char *lds = vtile[wave];
-    const int j = lane & 15, gq = lane >> 4;
 
-    batch_prefix<16, kMfmaWavesPerGroup>(p, pre);
+    batch_prefix<16, NW>(p, pre);
     const int B = p.num_seqs;
     const int total = pre[B];
-    const int w = logical_block(p, total) * kMfmaWavesPerGroup + wave;
+    const int w = logical_block(p, total) * NW + wave;
     const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);
     const long long g_lo = (long long)w * tpw;
-    if (g_lo >= total) return;
+
+    MfmaState<D> st[R];   // the state of the piece being computed; after the loop, the last one's
+    MfmaPiece pc;         // the piece being computed; after the loop, the last one
+    bool have_last = false;  // FIX: the last piece is cut at its end (its state is kept)
     RangeCursor cur;
     cur.g = (int)g_lo;
-    cur.g_end = min(total, cur.g + tpw);
+    cur.g_end = g_lo < total ? min(total, cur.g + tpw) : cur.g;
     cur.first = 1;
     cur.w = w;
     {
@@ -418,119 +517,129 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
         cur.s = __builtin_amdgcn_readfirstlane(lo);
     }
 
-    MfmaPiece pc;
     // A range inside one segment's start-up units holds no tile (only when
     // tpw <= seg_cost); the segment's tiles belong to the next wavefront.
-    if (!next_piece<16>(p, lens, pre, cur, pc)) return;
-    u32x4 q[R][G::kQkSteps];
-    mfma_load_q<D, R>(p, pc, lane, q);
-    int ids = mfma_load_ids(p, tables, pc, 0, lane);
-    // fold base of the current piece (requested a piece ahead from here on)
-    int fold_base = (p.fold_row && pc.t_begin == 0) ? p.fold_row[pc.s] : -1;
-    MfmaTileRegs<D> ra, rb;
-    int blk_a = __builtin_amdgcn_readlane(ids, 0);
-    {
-        const char *kb = (const char *)p.k + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
-        const char *vb = (const char *)p.v + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
-        mfma_load_tile<D>(p, kb, vb, pc.t_begin, pc.t_end, blk_a, lane, pc.s < p.cached_seqs, ra);
-    }
-
-    while (true) {
-        MfmaPiece pn = pc;
-        const bool has_next = next_piece<16>(p, lens, pre, cur, pn);
-        // Issued whether or not there is a next piece (pn is then the
-        // current one again), so every path through the loop below has the
-        // same loads in flight and the compiler's wait counts stay exact.
-        const int ids_n = mfma_load_ids(p, tables, pn, 0, lane);
-        const int fold_base_n = (p.fold_row && has_next && pn.t_begin == 0) ? p.fold_row[pn.s] : -1;
-        const char *kb = (const char *)p.k + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
-        const char *vb = (const char *)p.v + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
-        const char *kb_n = (const char *)p.k + (size_t)pn.kvh * (size_t)p.kv_head_stride * 2;
-        const char *vb_n = (const char *)p.v + (size_t)pn.kvh * (size_t)p.kv_head_stride * 2;
-        const bool cached = pc.s < p.cached_seqs;
-        const bool cached_n = has_next && pn.s < p.cached_seqs;
-        const int *bt = tables + (size_t)pc.s * p.max_blocks;
-
-        MfmaState<D> st[R];
-#pragma unroll
-        for (int b = 0; b < R; b++) {
-#pragma unroll
-            for (int n = 0; n < G::kDimBlocks; n++) st[b].o[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            st[b].m = -INFINITY;
-            st[b].l = 0.0f;
-        }
-        MfmaFold<D, R> fold;
-        fold.base = fold_base;
-        if (R == 1 && fold.base >= 0) mfma_fold_load<D, R>(p, pc, lane, fold);
-        const int ntiles = (pc.t_end - pc.t_begin + 15) >> 4;
-        for (int i = 0; i < ntiles; i++) {
-            if (i > 0 && (i & 63) == 0) ids = mfma_load_ids(p, tables, pc, i, lane);
-            const int t0 = pc.t_begin + 16 * i;
-            // The next tile: this piece's, else the next piece's first (all
-            // rows out of range when there is none).
-            const int nl = (i + 1) & 63;
-            const bool in_piece = i + 1 < ntiles;
-            int blk_b;
-            if (in_piece)
-                blk_b = nl != 0 ? __builtin_amdgcn_readlane(ids, nl) : bt[(t0 + 16) >> p.bs_shift];
-            else
-                blk_b = has_next ? __builtin_amdgcn_readlane(ids_n, 0) : -1;
-            mfma_load_tile<D>(p, in_piece ? kb : kb_n, in_piece ? vb : vb_n,
-                              in_piece ? t0 + 16 : pn.t_begin,
-                              in_piece ? pc.t_end : (has_next ? pn.t_end : 0), blk_b, lane,
-                              in_piece ? cached : cached_n, rb);
-            mfma_tile<KV, D, R>(p, q, t0, pc.t_end, blk_a >= 0, lane, lds, ra, st);
-            ra = rb;
-            blk_a = blk_b;
+    if (g_lo < total && next_piece<16>(p, lens, pre, cur, pc)) {
+        u32x4 q[R][G::kQkSteps];
+        mfma_load_q<D, R>(p, pc, lane, q);
+        int ids = mfma_load_ids(p, tables, pc, 0, lane);
+        // fold base of the current piece (requested a piece ahead from here on)
+        int fold_base = (p.fold_row && pc.t_begin == 0) ? p.fold_row[pc.s] : -1;
+        MfmaTileRegs<D> ra, rb;
+        int blk_a = __builtin_amdgcn_readlane(ids, 0);
+        {
+            const char *kb = (const char *)p.k + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
+            const char *vb = (const char *)p.v + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
+            mfma_load_tile<D>(p, kb, vb, pc.t_begin, pc.t_end, blk_a, lane, pc.s < p.cached_seqs,
+                              ra);
         }
 
-        if (fold.base >= 0) {
-            if (R != 1) mfma_fold_load<D, R>(p, pc, lane, fold);
-            mfma_fold_apply<D, R>(fold, lane, st);
-        }
-        const int g0 = pc.ht * GT;
-        const int nh = min(GT, p.group - g0);
-        const size_t qrow0 = ((size_t)pc.s * p.num_heads + (size_t)pc.kvh * p.group + g0) * D;
+        while (true) {
+            MfmaPiece pn = pc;
+            const bool has_next = next_piece<16>(p, lens, pre, cur, pn);
+            // Issued whether or not there is a next piece (pn is then the
+            // current one again), so every path through the loop below has
+            // the same loads in flight and the compiler's wait counts stay
+            // exact.
+            const int ids_n = mfma_load_ids(p, tables, pn, 0, lane);
+            const int fold_base_n =
+                (p.fold_row && has_next && pn.t_begin == 0) ? p.fold_row[pn.s] : -1;
+            const char *kb = (const char *)p.k + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
+            const char *vb = (const char *)p.v + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
+            const char *kb_n = (const char *)p.k + (size_t)pn.kvh * (size_t)p.kv_head_stride * 2;
+            const char *vb_n = (const char *)p.v + (size_t)pn.kvh * (size_t)p.kv_head_stride * 2;
+            const bool cached = pc.s < p.cached_seqs;
+            const bool cached_n = has_next && pn.s < p.cached_seqs;
+            const int *bt = tables + (size_t)pc.s * p.max_blocks;
+
 #pragma unroll
-        for (int b = 0; b < R; b++) {
-            float l = st[b].l;
-            l += __shfl_xor(l, 16);
-            l += __shfl_xor(l, 32);
-            const int hj = 16 * b + j;  // head of this lane in the tile
-            if (hj >= nh) continue;
-            if (pc.whole && p.out_f32) {
-                const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-                float *dst = p.out_f32 + qrow0 + (size_t)hj * D + 4 * gq;
+            for (int b = 0; b < R; b++) {
 #pragma unroll
-                for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st[b].o[n] * inv;
-                if (gq == 0) p.out_lse[qrow0 / D + hj] = l > 0.0f ? st[b].m + log2f(l) : -INFINITY;
-            } else if (pc.whole) {
-                const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-                char *dst = (char *)p.out + (qrow0 + (size_t)hj * D + 4 * gq) * 2;
-#pragma unroll
-                for (int n = 0; n < G::kDimBlocks; n++) {
-                    float f0, f1, f2, f3;
-                    const uint32_t b0 = round16<KV>(st[b].o[n][0] * inv, f0);
-                    const uint32_t b1 = round16<KV>(st[b].o[n][1] * inv, f1);
-                    const uint32_t b2 = round16<KV>(st[b].o[n][2] * inv, f2);
-                    const uint32_t b3 = round16<KV>(st[b].o[n][3] * inv, f3);
-                    *(u32x2 *)(dst + 32 * n) = u32x2{b0 | (b1 << 16), b2 | (b3 << 16)};
+                for (int n = 0; n < G::kDimBlocks; n++) st[b].o[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                st[b].m = -INFINITY;
+                st[b].l = 0.0f;
+            }
+            MfmaFold<D, R> fold;
+            fold.base = fold_base;
+            if (R == 1 && fold.base >= 0) mfma_fold_load<D, R>(p, pc, lane, fold);
+            const int ntiles = (pc.t_end - pc.t_begin + 15) >> 4;
+            for (int i = 0; i < ntiles; i++) {
+                if (i > 0 && (i & 63) == 0) ids = mfma_load_ids(p, tables, pc, i, lane);
+                const int t0 = pc.t_begin + 16 * i;
+                // The next tile: this piece's, else the next piece's first (all
+                // rows out of range when there is none).
+                const int nl = (i + 1) & 63;
+                const bool in_piece = i + 1 < ntiles;
+                int blk_b;
+                if (in_piece)
+                    blk_b = nl != 0 ? __builtin_amdgcn_readlane(ids, nl) : bt[(t0 + 16) >> p.bs_shift];
+                else
+                    blk_b = has_next ? __builtin_amdgcn_readlane(ids_n, 0) : -1;
+                mfma_load_tile<D>(p, in_piece ? kb : kb_n, in_piece ? vb : vb_n,
+                                  in_piece ? t0 + 16 : pn.t_begin,
+                                  in_piece ? pc.t_end : (has_next ? pn.t_end : 0), blk_b, lane,
+                                  in_piece ? cached : cached_n, rb);
+                mfma_tile<KV, D, R>(p, q, t0, pc.t_end, blk_a >= 0, lane, lds, ra, st);
+                ra = rb;
+                blk_a = blk_b;
+            }
+
+            if (fold.base >= 0) {
+                if (R != 1) mfma_fold_load<D, R>(p, pc, lane, fold);
+                mfma_fold_apply<D, R>(fold, lane, st);
+            }
+            if (pc.whole) {
+                mfma_write_rows<KV, D, R>(p, pc, lane, st);
+            } else if constexpr (FIX) {
+                if (has_next) {
+                    // a cut piece with more pieces after it: the wavefront's
+                    // first piece, a continuation that ends its segment here
+                    if (wave > 0) {
+                        fix_store<D>(fix[wave], lane, st[0]);
+                        if (lane == 0) fix[wave].ends = 1;
+                    } else {
+                        mfma_write_partial<D, R>(p, pc, lane, st);
+                    }
+                } else {
+                    have_last = true;  // the sweep below decides where it goes
                 }
             } else {
-                float *dst = p.ws_o + ((size_t)pc.slot * GT + hj) * D + 4 * gq;
-#pragma unroll
-                for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st[b].o[n];
-                if (gq == 0) {
-                    p.ws_ml[((size_t)pc.slot * GT + hj) * 2] = st[b].m;
-                    p.ws_ml[((size_t)pc.slot * GT + hj) * 2 + 1] = l;
+                mfma_write_partial<D, R>(p, pc, lane, st);
+            }
+            if (!has_next) break;
+            pc = pn;
+            ids = ids_n;
+            fold_base = fold_base_n;
+            mfma_load_q<D, R>(p, pc, lane, q);
+        }
+    }
+
+    if constexpr (FIX) {
+        // From the workgroup's last wavefront down to its first (the
+        // wavefronts of a workgroup hold consecutive ranges).
+        __syncthreads();
+        for (int i = NW - 1; i >= 0; i--) {
+            if (wave == i && have_last) {
+                const bool cut_start = pc.t_begin > 0;
+                bool ends = pc.t_end >= pc.L;
+                if (!ends && i < NW - 1) {
+                    // the right neighbour's first piece continues this
+                    // segment: its state is in its slot (stored during its
+                    // range, or relayed by it one step ago)
+                    fix_absorb<D>(fix[i + 1], lane, st[0]);
+                    ends = fix[i + 1].ends != 0;
+                }
+                if (cut_start && i > 0) {
+                    fix_store<D>(fix[i], lane, st[0]);
+                    if (lane == 0) fix[i].ends = ends ? 1 : 0;
+                } else if (!cut_start && ends) {
+                    mfma_write_rows<KV, D, R>(p, pc, lane, st);
+                } else {
+                    mfma_write_partial<D, R>(p, pc, lane, st);
                 }
             }
+            __syncthreads();
         }
-        if (!has_next) break;
-        pc = pn;
-        ids = ids_n;
-        fold_base = fold_base_n;
-        mfma_load_q<D, R>(p, pc, lane, q);
     }
 }
 

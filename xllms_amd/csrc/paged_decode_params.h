@@ -37,6 +37,18 @@ constexpr int kMergeCols = 32;       // float4 columns per workgroup of the chun
 constexpr int kLoadsPerTile = 4;     // 16-byte K (and V) loads per lane per tile
 constexpr int kMaxSeqsPerLaunch = 8192;  // the per-workgroup prefix scan lives in LDS
 
+// Workgroup-level combine of cut segments (MFMA tile path, one row block,
+// head_size <= 128): the kMfmaWavesPerGroup wavefronts of a workgroup own
+// consecutive stream-K ranges, so the pieces of one segment that fall in one
+// workgroup are merged through LDS at the end of the kernel.  Only one fp32
+// partial per (segment, workgroup it spans) reaches memory, in the slot of
+// the leftmost wavefront holding a piece of it, and a segment lying inside
+// one workgroup is written finished.  (Wider tiles would need more LDS than
+// two workgroups per CU leave.)
+constexpr bool mfma_wg_fixup(int rows_per_tile, int head_size) {
+    return rows_per_tile == kMfmaHeads && head_size <= 128;
+}
+
 struct DecodeParams {
     void *out;                 // [num_seqs][num_heads][head_size], element type
     const void *q;             // [num_seqs][num_heads][head_size]
@@ -63,6 +75,10 @@ struct DecodeParams {
     int seg_cost;              // split units a segment costs on top of its tiles
     float scale_log2;          // scale * log2(e)
     int merge_per_segment;     // 1: merge with one workgroup per segment
+    int wg_fix;                // 1: the partition kernel combined each segment's pieces
+                               // inside a workgroup (mfma_wg_fixup): partial j >= 1 of a
+                               // segment is in slot 2 * kMfmaWavesPerGroup * (its
+                               // workgroup), and a segment inside one workgroup is finished
     // Partial-output mode (cascade passes): when out_f32 is set, every
     // (sequence, head) row is written in fp32 to out_f32 (indexed like out)
     // together with its log-sum-exp in log2 units, m + log2(l), to
