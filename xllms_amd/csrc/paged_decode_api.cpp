@@ -442,7 +442,7 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         p.scale_log2 = scale * 1.4426950408889634f;
         // the partition kernel combines cut segments inside its workgroups
         // (same predicate as the kernel instantiation's)
-        p.wg_fix = mfma && xhip::mfma_wg_fixup(tiling.head_tile, head_size) ? 1 : 0;
+        p.wg_fix = mfma && xhip::mfma_wg_fixup(tiling.head_tile, head_size) != 0 ? 1 : 0;
         // One merge workgroup per segment once the segments alone fill two
         // workgroups per CU, or once the (segment, column chunk) grid would
         // launch more than four workgroups per CU (each costs ~2 ns of

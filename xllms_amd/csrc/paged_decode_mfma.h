@@ -444,6 +444,43 @@ __device__ __forceinline__ void fix_absorb(const MfmaFixSlot<D> &slot, int lane,
     st.m = M;
 }
 
+// The workgroup's relay slot of the mode-2 combine: one state of R row
+// blocks in the lane layout, and per wavefront whether it relayed its state
+// there (and whether that state reaches the end of its segment).
+template <int D, int R> struct MfmaRelaySlot {
+    f32x4 o[R][MfmaGeometry<D>::kDimBlocks][64];
+    float m[R][64], l[R][64];
+    int relayed[kMfmaWavesPerGroup];
+    int ends[kMfmaWavesPerGroup];
+};
+
+// st <- st (+) the fp32 partial in workspace slot `slot` (its l is the
+// reduced sum: lane group 0 takes it).  Rows past the group were never
+// written; they are left alone.
+template <int D, int R>
+__device__ __forceinline__ void absorb_partial(const DecodeParams &p, int slot, int ht, int lane,
+                                               MfmaState<D> (&st)[R]) {
+    constexpr int GT = kMfmaHeads * R;
+    const int j = lane & 15, gq = lane >> 4;
+    const int nh = min(GT, p.group - ht * GT);
+#pragma unroll
+    for (int b = 0; b < R; b++) {
+        const int hj = 16 * b + j;
+        if (hj >= nh) continue;
+        const float *src = p.ws_o + ((size_t)slot * GT + hj) * D + 4 * gq;
+        const float mo = p.ws_ml[((size_t)slot * GT + hj) * 2];
+        const float lo = gq == 0 ? p.ws_ml[((size_t)slot * GT + hj) * 2 + 1] : 0.0f;
+        const float M = fmaxf(st[b].m, mo);
+        const float Ms = (M == -INFINITY) ? 0.0f : M;
+        const float a = fast_exp2(st[b].m - Ms), w = fast_exp2(mo - Ms);
+        st[b].l = st[b].l * a + lo * w;
+#pragma unroll
+        for (int n = 0; n < MfmaGeometry<D>::kDimBlocks; n++)
+            st[b].o[n] = st[b].o[n] * a + *(const f32x4 *)(src + 16 * n) * w;
+        st[b].m = M;
+    }
+}
+
 // Partition kernel, MFMA tile path (head tile of 16R query heads).
 //
 // A wavefront walks the pieces of its stream-K range (usually one or two
@@ -473,22 +510,32 @@ __device__ __forceinline__ void fix_absorb(const MfmaFixSlot<D> &slot, int lane,
 // writes it: finished rows when the whole segment lay in the workgroup,
 // else one partial.  The first wavefront's cut first piece (its left
 // neighbour is in another workgroup) is written as a partial directly.
+// Mode 2 (two row blocks) keeps one relay slot per workgroup: cut first
+// pieces followed by more pieces are written as partials by every
+// wavefront, and a left neighbour absorbs such a partial from memory (the
+// workgroup barrier orders it) instead of from the relay slot.
+// Two wavefronts per SIMD (the plan's occupancy) up to head_size 128: at
+// most 256 registers each.  Larger heads need more and run one per SIMD.
 template <int KV, int D, int R>
-__global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partition_mfma_kernel(
+__global__ __launch_bounds__(64 * kMfmaWavesPerGroup, D <= 128 ? 2 : 1) void paged_decode_partition_mfma_kernel(
     const DecodeParams p, const int *__restrict__ lens, const int *__restrict__ tables) {
     // lens / tables are p.seq_lens / p.block_tables again: as restrict
     // kernel arguments their wavefront-uniform reads become scalar loads,
     // which do not wait behind the K/V loads in flight.
     using G = MfmaGeometry<D>;
-    constexpr bool FIX = mfma_wg_fixup(kMfmaHeads * R, D);
+    constexpr int FIX = mfma_wg_fixup(kMfmaHeads * R, D);
     constexpr int NW = kMfmaWavesPerGroup;
     extern __shared__ int pre[];  // num_seqs + 1 split-unit prefixes
     __shared__ __attribute__((aligned(16))) char vtile[NW][G::kLdsTile];
-    __shared__ MfmaFixSlot<D> fix[FIX ? NW : 1];
+    __shared__ MfmaFixSlot<D> fix[FIX == 1 ? NW : 1];
+    __shared__ MfmaRelaySlot<D, R> relay;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     char *lds = vtile[wave];
+    if constexpr (FIX == 2) {
+        if (lane == 0) relay.relayed[wave] = 0;  // ordered by batch_prefix's barriers
+    }
 
     batch_prefix<16, NW>(p, pre);
     const int B = p.num_seqs;
@@ -499,7 +546,7 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
 
     MfmaState<D> st[R];   // the state of the piece being computed; after the loop, the last one's
     MfmaPiece pc;         // the piece being computed; after the loop, the last one
-    bool have_last = false;  // FIX: the last piece is cut at its end (its state is kept)
+    bool have_last = false;  // FIX: the last piece is cut (its state is kept for the sweep)
     RangeCursor cur;
     cur.g = (int)g_lo;
     cur.g_end = g_lo < total ? min(total, cur.g + tpw) : cur.g;
@@ -590,7 +637,7 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
             }
             if (pc.whole) {
                 mfma_write_rows<KV, D, R>(p, pc, lane, st);
-            } else if constexpr (FIX) {
+            } else if constexpr (FIX == 1) {
                 if (has_next) {
                     // a cut piece with more pieces after it: the wavefront's
                     // first piece, a continuation that ends its segment here
@@ -603,6 +650,11 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
                 } else {
                     have_last = true;  // the sweep below decides where it goes
                 }
+            } else if constexpr (FIX == 2) {
+                if (has_next)
+                    mfma_write_partial<D, R>(p, pc, lane, st);
+                else
+                    have_last = true;
             } else {
                 mfma_write_partial<D, R>(p, pc, lane, st);
             }
@@ -614,7 +666,58 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup) void paged_decode_partitio
         }
     }
 
-    if constexpr (FIX) {
+    if constexpr (FIX == 2) {
+        // As below, with the one relay slot.
+        __syncthreads();
+        for (int i = NW - 1; i >= 0; i--) {
+            if (wave == i && have_last) {
+                const bool cut_start = pc.t_begin > 0;
+                bool ends = pc.t_end >= pc.L;
+                if (!ends && i < NW - 1) {
+                    if (relay.relayed[i + 1]) {
+#pragma unroll
+                        for (int b = 0; b < R; b++) {
+                            const float mo = relay.m[b][lane];
+                            const float M = fmaxf(st[b].m, mo);
+                            const float Ms = (M == -INFINITY) ? 0.0f : M;
+                            const float a = fast_exp2(st[b].m - Ms), wt = fast_exp2(mo - Ms);
+                            st[b].l = st[b].l * a + relay.l[b][lane] * wt;
+#pragma unroll
+                            for (int n = 0; n < G::kDimBlocks; n++)
+                                st[b].o[n] = st[b].o[n] * a + relay.o[b][n][lane] * wt;
+                            st[b].m = M;
+                        }
+                        ends = relay.ends[i + 1] != 0;
+                    } else {
+                        // the neighbour's first piece, followed by more
+                        // pieces, was written as a partial in its slot 0;
+                        // it ends the segment in that range
+                        absorb_partial<D, R>(p, (w + 1) * 2, pc.ht, lane, st);
+                        ends = true;
+                    }
+                }
+                if (cut_start && i > 0) {
+#pragma unroll
+                    for (int b = 0; b < R; b++) {
+#pragma unroll
+                        for (int n = 0; n < G::kDimBlocks; n++) relay.o[b][n][lane] = st[b].o[n];
+                        relay.m[b][lane] = st[b].m;
+                        relay.l[b][lane] = st[b].l;
+                    }
+                    if (lane == 0) {
+                        relay.relayed[i] = 1;
+                        relay.ends[i] = ends ? 1 : 0;
+                    }
+                } else if (!cut_start && ends) {
+                    mfma_write_rows<KV, D, R>(p, pc, lane, st);
+                } else {
+                    mfma_write_partial<D, R>(p, pc, lane, st);
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if constexpr (FIX == 1) {
         // From the workgroup's last wavefront down to its first (the
         // wavefronts of a workgroup hold consecutive ranges).
         __syncthreads();

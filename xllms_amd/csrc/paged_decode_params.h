@@ -37,16 +37,18 @@ constexpr int kMergeCols = 32;       // float4 columns per workgroup of the chun
 constexpr int kLoadsPerTile = 4;     // 16-byte K (and V) loads per lane per tile
 constexpr int kMaxSeqsPerLaunch = 8192;  // the per-workgroup prefix scan lives in LDS
 
-// Workgroup-level combine of cut segments (MFMA tile path, one row block,
-// head_size <= 128): the kMfmaWavesPerGroup wavefronts of a workgroup own
-// consecutive stream-K ranges, so the pieces of one segment that fall in one
-// workgroup are merged through LDS at the end of the kernel.  Only one fp32
-// partial per (segment, workgroup it spans) reaches memory, in the slot of
-// the leftmost wavefront holding a piece of it, and a segment lying inside
-// one workgroup is written finished.  (Wider tiles would need more LDS than
-// two workgroups per CU leave.)
-constexpr bool mfma_wg_fixup(int rows_per_tile, int head_size) {
-    return rows_per_tile == kMfmaHeads && head_size <= 128;
+// Workgroup-level combine of cut segments (MFMA tile path, head_size <=
+// 128): the kMfmaWavesPerGroup wavefronts of a workgroup own consecutive
+// stream-K ranges, so the pieces of one segment that fall in one workgroup
+// are merged through LDS at the end of the kernel.  Only one fp32 partial
+// per (segment, workgroup it spans) is left for the merge kernel, in the
+// slot of the leftmost wavefront holding a piece of it, and a segment lying
+// inside one workgroup is written finished.  Mode 1 (one row block): every
+// wavefront has an LDS slot.  Mode 2 (two row blocks, whose slots would
+// not leave room for two workgroups per CU): one relay slot per workgroup.
+// 0: no combine (head_size > 128).
+constexpr int mfma_wg_fixup(int rows_per_tile, int head_size) {
+    return head_size > 128 ? 0 : rows_per_tile == kMfmaHeads ? 1 : 2;
 }
 
 struct DecodeParams {
