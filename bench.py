@@ -451,7 +451,10 @@ def bench_serve(args) -> int:
     attention (prefix-aware when the batch shares prefixes) and the output
     scatter, waited for.  The binding calls and the request array (Python)
     are outside the timed region; the native exec call is timed with the host
-    clock.  XLLM_HIP_EXEC_TRACE=1 prints each exec's phase times."""
+    clock.  XLLM_HIP_EXEC_TRACE=1 prints each exec's phase times.  With
+    --per-request the same steps also run as one instance_exec(.., 1) per
+    request, synchronously (the reference scheduler's pattern) and in
+    deferred mode with one flush per step."""
     import numpy as np
     import torch
     from xllms_amd import backend as B
@@ -461,8 +464,11 @@ def bench_serve(args) -> int:
     tdt = W.torch_dtype(kv_dtype)
     nreq, bs = len(prompts), 16
     lens = np.array([len(p) for p in prompts])
-    pages = int(sum(-(-(int(L) + args.warmup + args.steps + 1) // bs) for L in lens))
-    max_blocks = int(-(-(int(lens.max()) + args.warmup + args.steps + 1) // bs))
+    # every timed mode appends one token per request per step
+    phases = 3 if args.per_request else 1
+    grow = phases * (args.warmup + args.steps) + 1
+    pages = int(sum(-(-(int(L) + grow) // bs) for L in lens))
+    max_blocks = int(-(-(int(lens.max()) + grow) // bs))
     dtype_code = {W.FP16: B.NXT_TYPE_FP16, W.BF16: B.NXT_TYPE_BF16_HIP,
                   W.FP32: B.NXT_TYPE_FP32}[kv_dtype]
     m = B.DecodeModel(num_blocks=pages + 64, num_kv_heads=KVH, block_size=bs, head_size=D,
@@ -484,19 +490,60 @@ def bench_serve(args) -> int:
     out = torch.empty_like(q)
     rng = np.random.default_rng(11)
     batch = m.requests(rids)
-    times = []
-    for step in range(args.warmup + args.steps):
+    singles = [m.requests([rid]) for rid in rids]
+
+    def bind_step():
         toks = rng.integers(0, 32000, nreq)
         for i, rid in enumerate(rids):
             m.bind(rid, tokens=[int(toks[i])], key=kv_new[0, i:i + 1], value=kv_new[1, i:i + 1],
                    query=q[i], output=out[i])
-        t0 = time.perf_counter()
-        rc = m.exec_requests(batch)
-        dt = time.perf_counter() - t0
-        if rc != 0:
-            raise RuntimeError(f"exec failed at step {step}")
-        if step >= args.warmup:
-            times.append(dt)
+
+    def run_steps(step_fn):
+        """Median host time of one decode step (the native calls only)."""
+        times = []
+        for step in range(args.warmup + args.steps):
+            bind_step()
+            t0 = time.perf_counter()
+            rc = step_fn()
+            dt = time.perf_counter() - t0
+            if rc != 0:
+                raise RuntimeError(f"exec failed at step {step}")
+            if step >= args.warmup:
+                times.append(dt)
+        return times
+
+    # one exec over the whole batch
+    times = run_steps(lambda: m.exec_requests(batch))
+    per_request = None
+    if args.per_request:
+        # the reference scheduler's pattern: one instance_exec(.., 1) per
+        # request (scheduler.c:477-488), each synchronous ...
+        def sync_step():
+            for one in singles:
+                rc = m.exec_requests(one)
+                if rc != 0:
+                    return rc
+            return 0
+        t_sync = run_steps(sync_step)
+        # ... and the same calls in deferred mode, then one flush per step
+        assert m.set_deferred(True) == 0
+
+        def deferred_step():
+            for one in singles:
+                rc = m.exec_requests(one)
+                if rc != 0:
+                    return rc
+            return m.flush()
+        t_def = run_steps(deferred_step)
+        assert m.set_deferred(False) == 0
+        per_request = {}
+        for key, t in (("synchronous", t_sync), ("deferred", t_def)):
+            md = float(np.median(t))
+            per_request[key] = {"seqs_per_s": round(nreq / md, 1),
+                                "step_us": {"median": round(md * 1e6, 1),
+                                            "min": round(min(t) * 1e6, 1),
+                                            "max": round(max(t) * 1e6, 1)}}
+        log(f"[bench] per-request execs: {per_request}")
     ok = bool(torch.isfinite(out.float()).all())
     exec_count = int(m.model.instances[0].exec_count)
     med = float(np.median(times))
@@ -504,6 +551,11 @@ def bench_serve(args) -> int:
     log(f"[bench] serve {name}: {nreq} requests, prefill {t_prefill:.2f} s; decode exec median "
         f"{med * 1e6:.1f} us (min {min(times) * 1e6:.1f}, max {max(times) * 1e6:.1f}); "
         f"finite outputs: {ok}")
+    if per_request:
+        per_request["deferred_over_whole_batch"] = round(
+            per_request["deferred"]["step_us"]["median"] / (med * 1e6), 3)
+        per_request["synchronous_over_whole_batch"] = round(
+            per_request["synchronous"]["step_us"]["median"] / (med * 1e6), 3)
     print(json.dumps({
         "metric": "decode step through the model instance (instance_exec, whole batch)",
         "value": round(nreq / med, 1), "unit": "seqs/s", "n_gpus": 1, "steps": args.steps,
@@ -514,6 +566,7 @@ def bench_serve(args) -> int:
         "exec_us": {"median": round(med * 1e6, 1), "min": round(min(times) * 1e6, 1),
                     "max": round(max(times) * 1e6, 1)},
         "instance_exec_count": exec_count,
+        **({"per_request": per_request} if per_request else {}),
         "check": {"outputs_finite": ok}}), flush=True)
     return 0 if ok else 1
 
@@ -537,6 +590,10 @@ def main() -> int:
                          "steps), each step one cascade call")
     ap.add_argument("--serve", action="store_true",
                     help="decode steps through the plugin's model instance (configs 2, 4, 5, 6)")
+    ap.add_argument("--per-request", action="store_true",
+                    help="with --serve: also time the reference scheduler's pattern, one "
+                         "instance_exec(.., 1) per request per step, synchronous and in deferred "
+                         "mode (queued, one flush per step)")
     ap.add_argument("--kv-append", action="store_true",
                     help="instead of the attention, time the KV append on the workload's shape: "
                          "every token of the batch written through nxt_paged_kv_write_slots "

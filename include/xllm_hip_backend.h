@@ -293,9 +293,29 @@ int nxt_model_instance_init(NxtModelInstance *instance);
 int nxt_model_instance_fini(NxtModelInstance *instance);
 int nxt_model_instance_exec(NxtModelInstance *instance, NxtInferRequest **requests,
                             uint32_t request_count);
-/* Additive: bind the buffers of the next exec of request_id (copied). */
+/* Additive: bind the buffers of the next exec of request_id (the
+ * descriptor and its token ids are copied). */
 int nxt_model_instance_bind(NxtModelInstance *instance, const char *request_id,
                             const NxtDecodeIo *io);
+
+/* Additive, no counterpart in the reference: deferred execution, for the
+ * reference scheduler's call pattern.  Its poll issues one
+ * instance_exec(instance, &request, 1) per scheduled request
+ * (scheduler.c:477-488), which as synchronous execs is one host-waited
+ * decode launch sequence per request.  With deferred mode on, exec checks
+ * the requests and queues them, returning 0; the queue runs as one
+ * whole-batch exec (the steps above, one wait) when it is flushed:
+ *   - by nxt_model_instance_flush, or an exec with request_count 0;
+ *   - when a queued request is bound again or executed again (its next
+ *     step began), before that bind or exec;
+ *   - when the queue holds max_batch_size requests;
+ *   - when deferred mode is switched off, and by nxt_model_instance_fini.
+ * Outputs of queued requests are ready once the flush that ran them has
+ * returned; its return value is the batch's (0, or -1 as for exec).
+ * set_deferred returns 0, or the flush's status when switching off.  Off
+ * by default: exec then runs and waits as above. */
+int nxt_model_instance_set_deferred(NxtModelInstance *instance, int on);
+int nxt_model_instance_flush(NxtModelInstance *instance);
 
 #ifdef __cplusplus
 }

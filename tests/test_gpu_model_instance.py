@@ -50,11 +50,12 @@ class Client:
         assert rc == 0
         return keep
 
-    def check(self, rids, binds, what):
+    def check(self, rids, binds, what, hist=None):
+        """hist: the histories the outputs were computed over (default: now)."""
         import torch
         torch.cuda.synchronize()
         for rid in rids:
-            self.ref.live[rid] = self.hist[rid]
+            self.ref.live[rid] = (hist or self.hist)[rid]
         q = np.stack([binds[r]["q_bits"] for r in rids])
         want = self.ref.logical_oracle(rids, q)
         got = np.stack([binds[r]["o"].float().cpu().numpy() for r in rids])
@@ -122,4 +123,77 @@ def test_scheduler_style_and_batched_exec(cuda):
     c.bind("late", [3], rng)
     assert m.exec(["late", "late"]) == -1
     assert m.close() == 0
+    torch.cuda.synchronize()
+
+
+def test_deferred_scheduler_pattern(cuda):
+    """Deferred mode (nxt_model_instance_set_deferred): the scheduler's
+    one-request execs are queued and run as one batch when flushed -- by
+    nxt_model_instance_flush, by binding or executing a queued request again
+    (its next step), by a full queue, by switching the mode off and by fini.
+    Every flushed output matches the oracle."""
+    import torch
+    rng = np.random.default_rng(7)
+    H, KVH, D, bs = 32, 8, 128, 16
+    ref = Driver.__new__(Driver)
+    ref.KVH, ref.H, ref.D, ref.bs = KVH, H, D, bs
+    ref.scale = 1.0 / np.sqrt(D)
+    ref.live, ref._rows = {}, {}
+    m = B.DecodeModel(num_blocks=512, num_kv_heads=KVH, block_size=bs, head_size=D,
+                      num_heads=H, max_batch_size=4, max_blocks_per_seq=64)
+    assert m.status == 0
+    c = Client(m, ref, W.FP16)
+    rids = [f"d{i}" for i in range(3)]
+    shared = list(rng.integers(0, 60, 40))
+    assert m.set_deferred(True) == 0
+    # prompts: queued, then an explicit flush runs them as one batch
+    binds = {rid: c.bind(rid, shared + list(rng.integers(0, 60, 10 + 5 * i)), rng)
+             for i, rid in enumerate(rids)}
+    for rid in rids:
+        assert m.exec([rid]) == 0
+    inst = m.model.instances[0]
+    assert inst.exec_count == 0  # nothing ran yet
+    assert m.flush() == 0
+    assert inst.exec_count == 1
+    c.check(rids, binds, "deferred prefill")
+    # a decode step queued request by request; the next step's first bind
+    # flushes it
+    binds = {rid: c.bind(rid, [int(rng.integers(0, 60))], rng) for rid in rids}
+    for rid in rids:
+        assert m.exec([rid]) == 0
+    step_hist = {rid: list(c.hist[rid]) for rid in rids}
+    nxt = c.bind(rids[0], [int(rng.integers(0, 60))], rng)
+    assert inst.exec_count == 2
+    c.check(rids, binds, "flushed by the next bind", hist=step_hist)
+    # executing a queued request again runs the queue first; the second exec
+    # then finds no binding and is refused
+    assert m.exec([rids[0]]) == 0
+    before = inst.exec_count
+    assert m.exec([rids[0]]) == -1
+    assert inst.exec_count == before + 1
+    c.check([rids[0]], {rids[0]: nxt}, "flushed by a second exec")
+    # an unbound request is refused when queued, and nothing runs
+    assert m.exec(["nobody"]) == -1
+    assert m.flush() == 0 and inst.exec_count == before + 1
+    # a full queue (max_batch_size 4) runs at once
+    extra = "d3"
+    binds = {rid: c.bind(rid, [int(rng.integers(0, 60))], rng) for rid in rids}
+    binds[extra] = c.bind(extra, list(rng.integers(60, 99, 33)), rng)
+    before = inst.exec_count
+    for rid in rids + [extra]:
+        assert m.exec([rid]) == 0
+    assert inst.exec_count == before + 1
+    c.check(rids + [extra], binds, "full queue")
+    # switching deferred mode off flushes; fini flushes too
+    binds = {rid: c.bind(rid, [int(rng.integers(0, 60))], rng) for rid in rids}
+    for rid in rids:
+        assert m.exec([rid]) == 0
+    assert m.set_deferred(False) == 0
+    c.check(rids, binds, "flushed by switching off")
+    assert m.set_deferred(True) == 0
+    binds = {rid: c.bind(rid, [int(rng.integers(0, 60))], rng) for rid in rids}
+    for rid in rids:
+        assert m.exec([rid]) == 0
+    assert m.close() == 0
+    c.check(rids, binds, "flushed by fini")
     torch.cuda.synchronize()

@@ -83,7 +83,8 @@ KV_INDEX_SYMBOLS = (
 )
 PLUGIN_SYMBOLS = ("nxt_backend_init", "nxt_backend_run", "nxt_backend_fini", "nxt_backend_run_ex",
                   "nxt_model_init", "nxt_model_fini", "nxt_model_instance_init",
-                  "nxt_model_instance_fini", "nxt_model_instance_exec", "nxt_model_instance_bind")
+                  "nxt_model_instance_fini", "nxt_model_instance_exec", "nxt_model_instance_bind",
+                  "nxt_model_instance_set_deferred", "nxt_model_instance_flush")
 
 _LEGACY_ARGS = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                 c_int, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_int, c_void_p]

@@ -241,8 +241,12 @@ class DecodeModel:
         self.dl.nxt_model_instance_bind.argtypes = [ctypes.POINTER(NxtModelInstance),
                                                     ctypes.c_char_p, ctypes.POINTER(NxtDecodeIo)]
         self.dl.nxt_model_instance_bind.restype = ctypes.c_int
+        self.dl.nxt_model_instance_set_deferred.argtypes = [ctypes.POINTER(NxtModelInstance),
+                                                            ctypes.c_int]
+        self.dl.nxt_model_instance_set_deferred.restype = ctypes.c_int
+        self.dl.nxt_model_instance_flush.argtypes = [ctypes.POINTER(NxtModelInstance)]
+        self.dl.nxt_model_instance_flush.restype = ctypes.c_int
         self._keep = []      # config structures, alive as long as the model
-        self._io_keep = []   # token arrays of bound requests, until their exec
 
         def tensor(tname, dtype_code, shape):
             sh = (ctypes.c_int64 * len(shape))(*shape)
@@ -277,8 +281,7 @@ class DecodeModel:
         import numpy as np
         io = NxtDecodeIo(struct_size=ctypes.sizeof(NxtDecodeIo))
         if tokens is not None and len(tokens):
-            t = np.ascontiguousarray(tokens, dtype=np.int32)
-            self._io_keep.append(t)
+            t = np.ascontiguousarray(tokens, dtype=np.int32)  # copied by the bind
             io.num_tokens = len(t)
             io.token_ids = t.ctypes.data
         ptr = lambda x: None if x is None else x.data_ptr()
@@ -297,17 +300,20 @@ class DecodeModel:
             reqs[i].request_id = rid
             reqs[i].batch_size = 1
             ptrs[i] = ctypes.pointer(reqs[i])
-        return (ids, reqs, ptrs, len(ids))
+        return (ids, reqs, ptrs, len(ids), ctypes.cast(ptrs, ctypes.c_void_p))
 
     def exec_requests(self, prepared) -> int:
-        rc = self.dl.nxt_model_instance_exec(self.instance,
-                                             ctypes.cast(prepared[2], ctypes.c_void_p),
-                                             prepared[3])
-        self._io_keep = []
-        return rc
+        return self.dl.nxt_model_instance_exec(self.instance, prepared[4], prepared[3])
 
     def exec(self, request_ids) -> int:
         return self.exec_requests(self.requests(request_ids))
+
+    def set_deferred(self, on: bool) -> int:
+        """Deferred mode: exec queues requests; a flush runs them as one batch."""
+        return self.dl.nxt_model_instance_set_deferred(self.instance, int(on))
+
+    def flush(self) -> int:
+        return self.dl.nxt_model_instance_flush(self.instance)
 
     def close(self) -> int:
         rc = self.dl.nxt_model_fini(ctypes.byref(self.model))

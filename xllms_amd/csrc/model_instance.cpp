@@ -110,11 +110,18 @@ struct InstanceState {
     NxtKvIndex *index = nullptr;
     std::unordered_map<std::string, int32_t> seqs;  // request id -> sequence
     struct Bound {
-        NxtDecodeIo io;
-        uint64_t exec_stamp;  // the exec that last took it (duplicate check)
+        NxtDecodeIo io;               // token_ids points into `tokens`
+        uint64_t exec_stamp;          // the exec that last took it (duplicate check)
+        std::vector<int32_t> tokens;  // the bound token ids (copied at bind)
+        bool queued = false;          // deferred mode: in `pending`
     };
     std::unordered_map<std::string, Bound> bound;  // request id -> next exec's buffers
     uint64_t exec_stamp = 0;
+    // deferred mode: requests queued by exec (their bound entries marked
+    // queued), run as one batch at the flush
+    bool deferred = false;
+    std::vector<std::string> pending;
+    std::vector<std::string> flushing;  // the batch being run (capacity kept)
     // staging of one exec
     HostBuf<int32_t> h_slots, h_src, h_dst, h_bt, h_lens, h_group, h_pblocks, h_seqs;
     HostBuf<const char *> h_kptr, h_vptr, h_qptr;
@@ -264,6 +271,22 @@ struct Item {
     int32_t seq;  // -1: admitted by this exec
 };
 
+int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<std::string> &ids);
+
+// Runs the queued requests of deferred mode as one exec.
+int flush_pending(NxtModelInstance *instance, InstanceState *st) {
+    if (st->pending.empty()) return 0;
+    st->flushing.swap(st->pending);
+    st->pending.clear();
+    for (const std::string &id : st->flushing) {
+        auto b = st->bound.find(id);
+        if (b != st->bound.end()) b->second.queued = false;
+    }
+    const int rc = exec_ids(instance, st, st->flushing);
+    st->flushing.clear();
+    return rc;
+}
+
 }  // namespace
 
 XMI_EXPORT int nxt_model_init(NxtModel *model) {
@@ -345,6 +368,7 @@ XMI_EXPORT int nxt_model_instance_init(NxtModelInstance *instance) {
 XMI_EXPORT int nxt_model_instance_fini(NxtModelInstance *instance) {
     if (!instance) return -1;
     InstanceState *st = state_of(instance);
+    if (st) (void)flush_pending(instance, st);  // queued requests still run
     destroy_state(st);
     instance->instance_state = nullptr;
     return 0;
@@ -364,9 +388,21 @@ XMI_EXPORT int nxt_model_instance_bind(NxtModelInstance *instance, const char *r
         if (((uintptr_t)p & 15) || !is_device(p))
             return fail("bind %s: buffers must be 16-byte aligned device memory", request_id);
     }
-    NxtDecodeIo c = *io;
-    c.struct_size = sizeof(NxtDecodeIo);
-    st->bound[request_id] = InstanceState::Bound{c, 0};
+    if (st->deferred) {
+        auto q = st->bound.find(request_id);
+        if (q != st->bound.end() && q->second.queued) {
+            // its queued exec consumes the current binding first
+            const int rc = flush_pending(instance, st);
+            if (rc != 0) return rc;
+        }
+    }
+    InstanceState::Bound &b = st->bound[request_id];
+    b.tokens.assign(io->token_ids, io->token_ids + io->num_tokens);
+    b.io = *io;
+    b.io.struct_size = sizeof(NxtDecodeIo);
+    b.io.token_ids = b.tokens.empty() ? nullptr : b.tokens.data();
+    b.exec_stamp = 0;
+    b.queued = false;
     return 0;
 }
 
@@ -374,7 +410,59 @@ XMI_EXPORT int nxt_model_instance_exec(NxtModelInstance *instance, NxtInferReque
                                        uint32_t request_count) {
     InstanceState *st = state_of(instance);
     if (!st || (request_count && !requests)) return -1;
+    for (uint32_t i = 0; i < request_count; ++i)
+        if (!requests[i] || !requests[i]->request_id) return fail("exec: request %u has no id", i);
+    if (!st->deferred) {
+        std::vector<std::string> ids;
+        ids.reserve(request_count);
+        for (uint32_t i = 0; i < request_count; ++i) ids.emplace_back(requests[i]->request_id);
+        return exec_ids(instance, st, ids);
+    }
+    if (request_count == 0) return flush_pending(instance, st);
+    for (uint32_t i = 0; i < request_count; ++i) {
+        const char *id = requests[i]->request_id;
+        auto b = st->bound.find(id);
+        if (b != st->bound.end() && b->second.queued) {
+            // its next step: run the queued batch first (which consumes the
+            // binding, so this exec then finds none)
+            const int rc = flush_pending(instance, st);
+            if (rc != 0) return rc;
+            b = st->bound.find(id);
+        }
+        if (b == st->bound.end()) return fail("exec: request %s has no bound buffers", id);
+        b->second.queued = true;
+        st->pending.emplace_back(id);
+        if ((int)st->pending.size() >= st->spec.max_batch) {
+            const int rc = flush_pending(instance, st);
+            if (rc != 0) return rc;
+        }
+    }
+    return 0;
+}
+
+XMI_EXPORT int nxt_model_instance_flush(NxtModelInstance *instance) {
+    InstanceState *st = state_of(instance);
+    if (!st) return -1;
+    return flush_pending(instance, st);
+}
+
+XMI_EXPORT int nxt_model_instance_set_deferred(NxtModelInstance *instance, int on) {
+    InstanceState *st = state_of(instance);
+    if (!st) return -1;
+    if (on) {
+        st->deferred = true;
+        return 0;
+    }
+    st->deferred = false;
+    return flush_pending(instance, st);
+}
+
+namespace {
+
+// One exec of the requests `ids` (in order): the whole-batch decode step.
+int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<std::string> &ids) {
     const ModelSpec &s = st->spec;
+    const uint32_t request_count = (uint32_t)ids.size();
     const auto t0 = std::chrono::steady_clock::now();
     PhaseTrace tr(t0);
     if ((int)request_count > s.max_batch)
@@ -386,8 +474,7 @@ XMI_EXPORT int nxt_model_instance_exec(NxtModelInstance *instance, NxtInferReque
     items.reserve(request_count);
     const uint64_t stamp = ++st->exec_stamp;
     for (uint32_t i = 0; i < request_count; ++i) {
-        if (!requests[i] || !requests[i]->request_id) return fail("exec: request %u has no id", i);
-        const std::string id = requests[i]->request_id;
+        const std::string &id = ids[i];
         auto b = st->bound.find(id);
         if (b == st->bound.end()) return fail("exec: request %s has no bound buffers", id.c_str());
         if (b->second.exec_stamp == stamp)
@@ -579,3 +666,5 @@ XMI_EXPORT int nxt_model_instance_exec(NxtModelInstance *instance, NxtInferReque
         std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     return rc;
 }
+
+}  // namespace
