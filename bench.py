@@ -805,8 +805,9 @@ def main() -> int:
                          "the batch's K/V tiles") + " streamed with the decode kernel's loads and "
                          "wavefront count, no arithmetic (xllm_stream_probe)",
         "device_copy_gbs": copy["gbs"],
-        "kernel_frac_of_pattern": round(achieved / probe["gbs"], 4) if probe else None,
-        "step_frac_of_pattern": round(step_gbs / probe["gbs"], 4) if probe else None,
+        # time ratios: the probe streams the same tiles the kernel reads
+        "kernel_frac_of_pattern": round(probe["us"] / (kernel_avg_ms * 1e3), 4) if probe else None,
+        "step_frac_of_pattern": round(probe["us"] / (ms_per_step * 1e3), 4) if probe else None,
     }
     log(f"[bench] measured ceilings: {measured_peak}")
 

@@ -25,15 +25,20 @@
  *   - Unsupported shapes never compute a wrong size silently: the call does
  *     nothing on the device and records an error, readable through
  *     nxt_attn_last_status()/nxt_attn_last_error() on the calling thread.
- * Supported: head_size in {32,64,80,96,112,128,192,256}; G = 1..32 with
- * num_heads % num_kv_heads == 0; block_size a power of two in [1, 1024];
+ * Supported: head_size in {32,64,80,96,112,128,192,256}; num_heads %
+ * num_kv_heads == 0 with G <= 64 for fp16/bf16 at head_size % 32 == 0 and
+ * block_size >= 16, else G <= 32; block_size a power of two in [1, 1024];
  * max_num_blocks_per_seq*block_size <= 2^28; 16-byte aligned tensors and
  * strides (every real KV cache layout).
  *
  * Calls are asynchronous on `stream` (NULL = the default stream) and never
  * synchronise, except the rare call that must grow the split-K workspace of
- * that stream, which first waits for the stream.  Calls on different streams
- * are independent (one workspace per (device, stream)).
+ * that stream, which first waits for the stream.  Threads: the library keeps
+ * one workspace per (device, stream queue); a call holds it from lookup until
+ * its launches are enqueued, so calls from several host threads on one
+ * stream handle are enqueued one after the other, calls on different streams
+ * are independent, and hipStreamPerThread gets one workspace per thread.
+ * Do not destroy a stream while calls on it are pending.
  */
 #ifndef XLLM_HIP_OPERATOR_API_H_
 #define XLLM_HIP_OPERATOR_API_H_
