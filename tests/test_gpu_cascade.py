@@ -87,7 +87,8 @@ def test_cascade_config5_matches_oracle(cuda):
 @pytest.mark.parametrize("dtype,D,H,KVH", [("fp16", 128, 32, 8), ("bf16", 128, 64, 8),
                                           ("fp16", 64, 8, 8), ("bf16", 256, 16, 1),
                                           ("fp16", 80, 16, 4), ("fp32", 64, 12, 12),
-                                          ("fp32", 128, 32, 8), ("fp16", 96, 64, 2)])
+                                          ("fp32", 128, 32, 8), ("fp16", 96, 64, 2),
+                                          ("bf16", 32, 48, 1)])
 def test_cascade_groups_match_oracle(cuda, dtype, D, H, KVH):
     """Groups of 1..21 members (prefix rows spanning several 16- or 32-row
     prefix sequences), members with an empty suffix, unshared sequences

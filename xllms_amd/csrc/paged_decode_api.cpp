@@ -269,6 +269,31 @@ struct FixedWs {
     size_t bytes;
 };
 
+// The fields of a launch's DecodeParams that come straight from its batch.
+void fill_batch(DecodeParams &p, const void *query, const void *key_cache, const void *value_cache,
+                const int *block_tables, const int *seq_lens, int nseq, int num_heads,
+                int num_kv_heads, int head_tiles, int max_num_blocks_per_seq, int block_size,
+                int kv_block_stride, int kv_head_stride, float scale) {
+    const long long max_ctx = (long long)max_num_blocks_per_seq * block_size;
+    p.q = query;
+    p.k = key_cache;
+    p.v = value_cache;
+    p.block_tables = block_tables;
+    p.seq_lens = seq_lens;
+    p.kv_block_stride = kv_block_stride;
+    p.kv_head_stride = kv_head_stride;
+    p.num_seqs = nseq;
+    p.num_heads = num_heads;
+    p.num_kv_heads = num_kv_heads;
+    p.group = num_heads / num_kv_heads;
+    p.head_tiles = head_tiles;
+    p.max_blocks = max_num_blocks_per_seq;
+    p.block_size = block_size;
+    p.bs_shift = ilog2(block_size);
+    p.max_ctx = (int)max_ctx;
+    p.scale_log2 = scale * 1.4426950408889634f;
+}
+
 int run(void *out, const void *query, const void *key_cache, const void *value_cache,
         const int *block_tables, const int *seq_lens, int num_seqs, int num_heads, int head_size,
         int num_kv_heads, float scale, int max_num_blocks_per_seq, int block_size, int dtype_size,
@@ -417,29 +442,16 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
             p.fold_rows = fold->rows;
             p.fold_kr = fold->kr;
         }
-        p.q = (const char *)query + row0;
-        p.k = key_cache;
-        p.v = value_cache;
-        p.block_tables = block_tables + (size_t)s0 * max_num_blocks_per_seq;
-        p.seq_lens = seq_lens + s0;
+        fill_batch(p, (const char *)query + row0, key_cache, value_cache,
+                   block_tables + (size_t)s0 * max_num_blocks_per_seq, seq_lens + s0, nseq,
+                   num_heads, num_kv_heads, tiling.head_tiles, max_num_blocks_per_seq, block_size,
+                   kv_block_stride, kv_head_stride, scale);
         p.ws_o = (float *)ws;
         p.ws_ml = (float *)((char *)ws + o_bytes);
         p.ws_prefix = (int *)((char *)ws + o_bytes + ml_bytes);
-        p.kv_block_stride = kv_block_stride;
-        p.kv_head_stride = kv_head_stride;
-        p.num_seqs = nseq;
-        p.num_heads = num_heads;
-        p.num_kv_heads = num_kv_heads;
-        p.group = group;
-        p.head_tiles = tiling.head_tiles;
-        p.max_blocks = max_num_blocks_per_seq;
-        p.block_size = block_size;
-        p.bs_shift = ilog2(block_size);
-        p.max_ctx = (int)max_ctx;
         p.num_waves = (int)waves;
         p.min_tiles_per_wave = min_tpw;
         p.seg_cost = seg_cost;
-        p.scale_log2 = scale * 1.4426950408889634f;
         // the partition kernel combines cut segments inside its workgroups
         // (same predicate as the kernel instantiation's)
         p.wg_fix = mfma && xhip::mfma_wg_fixup(tiling.head_tile, head_size) != 0 ? 1 : 0;
@@ -519,6 +531,35 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
                           "cascade prefix batch of %lld sequences (limit %d): fewer sequences "
                           "or groups per call",
                           v_max, xhip::kMaxSeqsPerLaunch);
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return set_status(NXT_ATTN_E_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    hipStream_t stream = (hipStream_t)stream_handle;
+
+    // The MFMA path with 32-row prefix tiles runs both batches in one
+    // partition launch of `fw` wavefronts and one merge
+    // (paged_decode_cascade_attn.h); otherwise the two batches go through
+    // run() one after the other, the suffix batch folding in the prefix rows.
+    HeadTiling stile{};
+    long long fw = 0;
+    if (wide && supported_head_size(head_size) &&
+        head_tiling(group, true, head_size, &stile)) {
+        const long long tiles = ((long long)max_num_blocks_per_seq * block_size + 15) / 16 + kSegmentCost;
+        const bool fits = v_max * (long long)num_kv_heads * (rows / 32) * tiles < kMaxLaunchTiles &&
+                          (long long)num_seqs * num_kv_heads * stile.head_tiles * tiles <
+                              kMaxLaunchTiles;
+        const size_t lds = (size_t)(v_max + num_seqs + 2) * sizeof(int);
+        const int rs = stile.head_tile / xhip::kMfmaHeads;
+        const int occ = !fits ? 0
+                        : kv_dtype == NXT_KV_FP16 ? xhip::cascade_attn_occupancy_f16(head_size, rs, lds)
+                                                  : xhip::cascade_attn_occupancy_bf16(head_size, rs, lds);
+        if (occ > 0) {
+            int per_cu = occ * xhip::kMfmaWavesPerGroup;
+            if (per_cu > kMfmaWavesPerCu) per_cu = kMfmaWavesPerCu;
+            fw = (long long)cu_count(device) * per_cu;
+            if (fw < 2 * xhip::kMfmaWavesPerGroup) fw = 2 * xhip::kMfmaWavesPerGroup;
+        }
+    }
     // workspace layout (each piece 256-byte aligned)
     size_t off = 0;
     auto take = [&](size_t bytes) {
@@ -535,10 +576,17 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
                  o_sl = take(4 * (size_t)num_seqs), o_sb = take(4 * (size_t)num_seqs * mb),
                  o_po = take(4 * (size_t)v_max * KR * head_size), o_pl = take(4 * (size_t)v_max * KR),
                  o_pr = take(4 * (size_t)num_seqs);
-    int device = 0;
-    hipError_t e = hipGetDevice(&device);
-    if (e != hipSuccess) return set_status(NXT_ATTN_E_HIP, "hipGetDevice: %s", hipGetErrorString(e));
-    hipStream_t stream = (hipStream_t)stream_handle;
+    // one launch over both batches: each batch's split-K workspace (partials
+    // for up to every wavefront, unit prefix), and the suffix batch's rows
+    const size_t gts = (size_t)stile.head_tile;
+    const size_t o_xo = fw ? take(4 * 2 * (size_t)fw * 32 * head_size) : 0,
+                 o_xm = fw ? take(4 * 2 * (size_t)fw * 32 * 2) : 0,
+                 o_xp = fw ? take(4 * ((size_t)v_max + 2)) : 0,
+                 o_yo = fw ? take(4 * 2 * (size_t)fw * gts * head_size) : 0,
+                 o_ym = fw ? take(4 * 2 * (size_t)fw * gts * 2) : 0,
+                 o_yp = fw ? take(4 * ((size_t)num_seqs + 1)) : 0,
+                 o_so = fw ? take(4 * (size_t)num_seqs * num_heads * head_size) : 0,
+                 o_sl2 = fw ? take(4 * (size_t)num_seqs * num_heads) : 0;
     // held over the plan and both passes (they read what the plan wrote)
     WsCache::Lease lease;
     int st = get_workspace(device, stream, off, &lease, kWsCascade);
@@ -584,6 +632,44 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
     e = xhip::launch_cascade_plan(c, stream);
     if (e != hipSuccess)
         return set_status(NXT_ATTN_E_HIP, "cascade plan launch: %s", hipGetErrorString(e));
+    if (fw) {
+        DecodeParams pp, ps;
+        memset(&pp, 0, sizeof(pp));
+        memset(&ps, 0, sizeof(ps));
+        fill_batch(pp, c.v_q, key_cache, value_cache, c.v_bt, c.v_lens, (int)v_max, (int)KR,
+                   num_kv_heads, rows / 32, max_num_blocks_per_seq, block_size, kv_block_stride,
+                   kv_head_stride, scale);
+        fill_batch(ps, query, key_cache, value_cache, c.s_bt, c.s_lens, num_seqs, num_heads,
+                   num_kv_heads, stile.head_tiles, max_num_blocks_per_seq, block_size,
+                   kv_block_stride, kv_head_stride, scale);
+        for (DecodeParams *q : {&pp, &ps}) {
+            q->num_waves = (int)fw;
+            q->min_tiles_per_wave = kMinTilesPerWave;
+            q->seg_cost = kSegmentCost;
+            q->wg_fix = 1;
+            q->skip_empty = 1;  // merged from the other batch, or zeros, by the merge
+        }
+        pp.out_f32 = (float *)(w + o_po);
+        pp.out_lse = (float *)(w + o_pl);
+        pp.cached_seqs = (int)v_max;  // a group's rows read its pages close in time
+        pp.ws_o = (float *)(w + o_xo);
+        pp.ws_ml = (float *)(w + o_xm);
+        pp.ws_prefix = (int *)(w + o_xp);
+        ps.out_f32 = (float *)(w + o_so);
+        ps.out_lse = (float *)(w + o_sl2);
+        ps.ws_o = (float *)(w + o_yo);
+        ps.ws_ml = (float *)(w + o_ym);
+        ps.ws_prefix = (int *)(w + o_yp);
+        const int rs = stile.head_tile / xhip::kMfmaHeads;
+        e = kv_dtype == NXT_KV_FP16
+                ? xhip::launch_cascade_attn_f16(pp, ps, c.p_row, rows, out, head_size, rs, stream,
+                                                t_trace_start, t_trace_partition)
+                : xhip::launch_cascade_attn_bf16(pp, ps, c.p_row, rows, out, head_size, rs, stream,
+                                                 t_trace_start, t_trace_partition);
+        if (e != hipSuccess)
+            return set_status(NXT_ATTN_E_HIP, "cascade attention launch: %s", hipGetErrorString(e));
+        return ok();
+    }
     // (the prefix batch's empty sequences are the reserved ones no group
     // uses: nothing reads their rows)
     const PartialOut pre{(float *)(w + o_po), (float *)(w + o_pl), (int)v_max, 1};

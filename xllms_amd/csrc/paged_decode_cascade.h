@@ -1,12 +1,16 @@
 // Prefix-aware (cascade) decode: launch parameters and launchers of the plan
-// and detection kernels (paged_decode_cascade.hip).  The attention itself
-// runs twice through the ordinary partition + merge kernels: once on a prefix
-// batch, and once on a suffix batch that starts every member's segments from
-// its prefix result (DecodeParams::fold_row) and writes the output.
+// and detection kernels (paged_decode_cascade.hip) and of the attention over
+// the plan's two batches on the MFMA tile path (paged_decode_cascade_attn.h).
+// Other tile paths run the attention through the ordinary partition + merge
+// kernels twice: once on the prefix batch, and once on the suffix batch,
+// which starts every member's segments from its prefix result
+// (DecodeParams::fold_row) and writes the output.
 #pragma once
 
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
+
+#include "paged_decode_params.h"
 
 namespace xhip {
 
@@ -51,6 +55,20 @@ struct CascadeParams {
 
 // Plan: group membership and the prefix / suffix batches.
 hipError_t launch_cascade_plan(const CascadeParams &c, hipStream_t stream);
+
+// Attention of the cascade on the MFMA tile path (paged_decode_cascade_attn.h):
+// the prefix batch pp (32-row head tiles) and the suffix batch ps (head
+// tiles of 16 * rs rows) in one partition launch of ps.num_waves
+// wavefronts (>= 8), then the merge that writes `out` from both.
+// head_size 32, 64, 96 or 128; hipErrorInvalidValue otherwise.
+int cascade_attn_occupancy_f16(int head_size, int rs, size_t lds_bytes);
+int cascade_attn_occupancy_bf16(int head_size, int rs, size_t lds_bytes);
+hipError_t launch_cascade_attn_f16(const DecodeParams &pp, const DecodeParams &ps,
+                                   const int *p_row, int rows, void *out, int head_size, int rs,
+                                   hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
+hipError_t launch_cascade_attn_bf16(const DecodeParams &pp, const DecodeParams &ps,
+                                    const int *p_row, int rows, void *out, int head_size, int rs,
+                                    hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
 
 // Detection of shared prefixes from the block tables (one workgroup,
 // num_seqs <= kCascadeMaxSeqs): sequences whose first page is the same

@@ -7,17 +7,17 @@
 // for all of its members: the plan gathers the members' query rows, R per kv
 // head, into the sequences of a prefix batch whose block table is the shared
 // prefix, and shifts every member's own block table past the prefix into a
-// suffix batch.  The ordinary partition + merge kernels run the prefix batch
-// in partial-output mode (fp32 rows plus their log-sum-exp lse_p; prefix
-// pages loaded cacheable, since the rows of a group read them close in
-// time), then the suffix batch with a prefix fold: (lse_p, O_p) is the
-// online softmax state (m = lse_p, l = 1, o = O_p), so a member's suffix
-// segments start from it and the suffix pass writes
+// suffix batch.  On the MFMA tile path both batches run in one partition
+// launch and one merge combines each member's prefix and suffix states
+// (paged_decode_cascade_attn.h).  Elsewhere the ordinary partition + merge
+// kernels run the prefix batch in partial-output mode (fp32 rows plus their
+// log-sum-exp lse_p; prefix pages loaded cacheable, since the rows of a
+// group read them close in time), then the suffix batch with a prefix fold:
+// (lse_p, O_p) is the online softmax state (m = lse_p, l = 1, o = O_p), so a
+// member's suffix segments start from it and the suffix pass writes
 //   O = (2^(lse_p-m) O_p + sum_t 2^(s_t-m) v_t) / (2^(lse_p-m) + sum_t 2^(s_t-m)),
-// the attention over prefix and suffix together.  (One run over both
-// batches together was measured slower: every wavefront then streams prefix
-// and suffix tiles back to back at the slower per-tile rate of the two.)  A
-// row of the prefix batch depends only on its own query (the MFMA tile
+// the attention over prefix and suffix together.  A row of the prefix batch
+// depends only on its own query (the MFMA tile
 // computes every (token, row) score and every (dim, row) output from that
 // row alone), so where a member lands among the rows does not change its
 // result, and rows no member uses are never read.

@@ -1,0 +1,248 @@
+// Attention of the cascade (prefix-aware) decode on the MFMA tile path, in
+// two launches: both batches of the plan (paged_decode_cascade.h) in one
+// partition launch, then one merge that combines every output row's suffix
+// state with its prefix state.
+//
+// Partition.  The workgroups of one launch are split between the prefix
+// batch (32-row head tiles, R = 2: every shared page is read for 32 (member,
+// head) rows at once) and the suffix batch (the members' own pages, head
+// tiles of the caller's group), each running the ordinary MFMA partition
+// body over its own stream-K plan.  Every workgroup scans the split units of
+// both batches (LDS) and takes the same split: the prefix batch gets a share
+// of the workgroups proportional to its units (kCascadeUnitCost: an R = 2
+// tile costs a wavefront about what an R = 1 tile does, both waiting mostly
+// on their loads; measured on MI355X at config 5, weights 0.8 / 1.0 / 1.25 /
+// 1.5 / 2.0 gave 131.3 / 128.3 / 131.2 / 133.5 / 140.2 us steps).  Run as two
+// launches, the prefix batch (a few thousand short ranges) spent ~30 us
+// mostly in latency while the device's bandwidth went unused; here its
+// ranges stream beside the suffix batch's.  Both bodies run in
+// partial-output mode: finished segments leave fp32 rows and their
+// log-sum-exp, cut segments their partials, and the suffix batch no longer
+// starts from the prefix result (that would make it wait for the prefix
+// batch).
+//
+// Merge.  One workgroup per suffix segment (sequence, kv head, head tile);
+// for every float4 column of its rows the suffix state (finished row, or the
+// partials of its cut segment) and the prefix state of the same query row
+// (the prefix batch's row, or its partials) are combined by the online
+// log-sum-exp rule and written as the output:
+//   O = (2^(lse_p-M) O_p + 2^(lse_s-M) O_s) / (2^(lse_p-M) + 2^(lse_s-M)).
+#pragma once
+
+#include <hip/hip_ext.h>
+
+#include <cstdint>
+
+#include "paged_decode_cascade.h"
+#include "paged_decode_mfma.h"
+
+namespace xhip {
+
+// Weight of a prefix-batch split unit against a suffix-batch unit in the
+// workgroup split, in percent.
+#ifndef XHIP_CASCADE_UNIT_COST
+#define XHIP_CASCADE_UNIT_COST 100
+#endif
+constexpr int kCascadeUnitCost = XHIP_CASCADE_UNIT_COST;
+
+// Workgroups of the prefix body in a launch of G >= 2 workgroups, from the
+// split units of the prefix (tp) and suffix (ts) batches: each batch with
+// units gets at least one.  Integer arithmetic only: every workgroup
+// computes the same split.
+__device__ __forceinline__ int cascade_prefix_groups(int tp, int ts, int G) {
+    if (tp <= 0) return 0;
+    if (ts <= 0) return G;
+    const long long a = (long long)tp * kCascadeUnitCost, b = (long long)ts * 100;
+    const int gp = (int)((a * G + (a + b) / 2) / (a + b));
+    return gp < 1 ? 1 : (gp > G - 1 ? G - 1 : gp);
+}
+
+template <int D, int R1, int R2> union MfmaLdsPair {
+    MfmaLds<D, R1> a;
+    MfmaLds<D, R2> b;
+};
+
+// Partition launch over both batches.  pp / ps are the prefix and suffix
+// batches' plans; their num_waves is the whole launch's (gridDim.x *
+// kMfmaWavesPerGroup).  Workgroup 0 also stores both unit prefixes and the
+// prefix body's workgroup count (pp.ws_prefix[pp.num_seqs + 1]) for the
+// merge.
+template <int KV, int D, int RS>
+__global__ __launch_bounds__(64 * kMfmaWavesPerGroup, 2) void paged_decode_cascade_mfma_kernel(
+    const DecodeParams pp, const DecodeParams ps, const int *__restrict__ plens,
+    const int *__restrict__ ptables, const int *__restrict__ slens,
+    const int *__restrict__ stables) {
+    constexpr int NW = kMfmaWavesPerGroup;
+    extern __shared__ int pre[];  // prefix batch (pp.num_seqs + 1), then suffix batch
+    __shared__ MfmaLdsPair<D, 2, RS> sm;
+    int *pre_p = pre, *pre_s = pre + pp.num_seqs + 1;
+    batch_prefix<16, NW>(pp, pre_p);
+    batch_prefix<16, NW>(ps, pre_s);
+    const int G = gridDim.x;
+    const int gp = cascade_prefix_groups(pre_p[pp.num_seqs], pre_s[ps.num_seqs], G);
+    if (blockIdx.x == 0 && threadIdx.x == 0) pp.ws_prefix[pp.num_seqs + 1] = gp;
+    // neighbouring logical workgroups share an XCD (and its L2): the two
+    // head tiles of a prefix segment read the same pages in neighbouring
+    // ranges
+    const int l = xcd_local_block(blockIdx.x, G);
+    if (l < gp)
+        mfma_partition_body<KV, D, 2>(pp, plens, ptables, pre_p, l, gp * NW, sm.a);
+    else
+        mfma_partition_body<KV, D, RS>(ps, slens, stables, pre_s, l - gp, (G - gp) * NW, sm.b);
+}
+
+// (m, l, acc) <- (m, l, acc) (+) a finished row: the state (lse, 1, row).
+__device__ __forceinline__ void absorb_row(float lse, const f32x4 &row, float &m, float &l,
+                                           f32x4 &acc) {
+    const float M = fmaxf(m, lse);
+    const float Ms = (M == -INFINITY) ? 0.0f : M;
+    const float a = fast_exp2(m - Ms), w = fast_exp2(lse - Ms);
+    l = l * a + w;
+    acc = acc * a + row * w;
+    m = M;
+}
+
+// The state of one float4 column of a segment of batch p: its partials when
+// the partition left the segment cut, else its finished row.  seg is the
+// segment's index within its sequence, hrow the column's head in the
+// segment's tile (GT heads), c the float4 column in the head.
+template <int GT, int D>
+__device__ __forceinline__ void segment_state(const DecodeParams &p, int s, int L, int seg,
+                                              int pre_s, int total, int waves, size_t row, int hrow,
+                                              int c, float &m, float &l, f32x4 &acc) {
+    const int Ts = (L + 15) / 16;
+    const int seg_start = pre_s + seg * segment_units(p, Ts);
+    const int tpw = tiles_per_wave(total, waves, p.min_tiles_per_wave);
+    PartialSlots ps;
+    if (segment_partials<kMfmaWavesPerGroup>(p, seg_start, seg_start + p.seg_cost, Ts, tpw, ps)) {
+        merge_partials<GT, D, 8>(p, ps, 0, 1, hrow * 2, hrow * D + c * 4, m, l, acc);
+    } else {
+        const float lse = p.out_lse[row];
+        const f32x4 o = *(const f32x4 *)(p.out_f32 + row * D + c * 4);
+        absorb_row(lse, o, m, l, acc);
+    }
+}
+
+// Merge over every suffix segment (sequence s, kv head, head tile of GTS
+// heads), NT threads striding over its float4 columns.  p_row[s] is the row,
+// in the prefix batch's rows of a kv head laid end to end (`rows` per
+// prefix-batch sequence), of s's first query head; -1: s has no prefix.
+template <int KV, int D, int GTS, int NT>
+__global__ __launch_bounds__(NT) void paged_decode_cascade_merge_kernel(
+    const DecodeParams pp, const DecodeParams ps, const int *__restrict__ p_row, int rows,
+    void *out) {
+    constexpr int C4 = D / 4;
+    constexpr int NW = kMfmaWavesPerGroup;
+    constexpr int GTP = 2 * kMfmaHeads;
+    const int segs = ps.num_kv_heads * ps.head_tiles;
+    const int s = blockIdx.x / segs;
+    const int seg = blockIdx.x - s * segs;
+    const int kvh = seg / ps.head_tiles;
+    const int g0 = (seg - kvh * ps.head_tiles) * GTS;
+    const int nh = min(GTS, ps.group - g0);
+    const int ncols = nh * C4;
+    // the scalars, requested together
+    const int Ls = seq_len_of(ps, s);
+    const int fb = p_row[s];
+    const int tot_s = ps.ws_prefix[ps.num_seqs];
+    const int pre_s = ps.ws_prefix[s];
+    const int tot_p = pp.ws_prefix[pp.num_seqs];
+    const int gp = pp.ws_prefix[pp.num_seqs + 1];
+    asm volatile("" ::"s"(Ls), "s"(fb), "s"(tot_s), "s"(pre_s), "s"(tot_p), "s"(gp));
+    const int G = ps.num_waves / NW;
+    const size_t srow0 = (size_t)s * ps.num_heads + (size_t)kvh * ps.group + g0;
+    for (int col = threadIdx.x; col < ncols; col += NT) {
+        const int h = col / C4, c = col - h * C4;
+        float m = -INFINITY, l = 0.0f;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (Ls > 0)
+            segment_state<GTS, D>(ps, s, Ls, seg, pre_s, tot_s, (G - gp) * NW, srow0 + h, h, c, m,
+                                  l, acc);
+        if (fb >= 0) {
+            const int q = fb + g0 + h;
+            const int v = q / rows, j = q - v * rows;
+            const int Lv = seq_len_of(pp, v);
+            if (Lv > 0) {
+                const int htp = j / GTP;
+                const size_t prow = (size_t)v * pp.num_heads + (size_t)kvh * rows + j;
+                segment_state<GTP, D>(pp, v, Lv, kvh * pp.head_tiles + htp, pp.ws_prefix[v],
+                                      tot_p, gp * NW, prow, j - htp * GTP, c, m, l, acc);
+            }
+        }
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        const size_t base = (srow0 + h) * D + c * 4;
+#pragma unroll
+        for (int e = 0; e < 4; e++) store_elem<KV>(out, base + e, acc[e] * inv);
+    }
+}
+
+template <int KV, int D, int RS>
+static hipError_t launch_cascade_attn_rs(const DecodeParams &pp, const DecodeParams &ps,
+                                         const int *p_row, int rows, void *out, hipStream_t st,
+                                         hipEvent_t ev_start, hipEvent_t ev_stop) {
+    const unsigned grid = (unsigned)(ps.num_waves / kMfmaWavesPerGroup);
+    const size_t lds = (size_t)(pp.num_seqs + ps.num_seqs + 2) * sizeof(int);
+    auto kernel = paged_decode_cascade_mfma_kernel<KV, D, RS>;
+    if (ev_start || ev_stop)
+        hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWavesPerGroup),
+                              (std::uint32_t)lds, st, ev_start, ev_stop, 0u, pp, ps, pp.seq_lens,
+                              pp.block_tables, ps.seq_lens, ps.block_tables);
+    else
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWavesPerGroup), lds, st, pp, ps,
+                           pp.seq_lens, pp.block_tables, ps.seq_lens, ps.block_tables);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const unsigned segs = (unsigned)(ps.num_seqs * ps.num_kv_heads * ps.head_tiles);
+    paged_decode_cascade_merge_kernel<KV, D, kMfmaHeads * RS, 128>
+        <<<segs, 128, 0, st>>>(pp, ps, p_row, rows, out);
+    return hipGetLastError();
+}
+
+template <int KV, int D>
+static const void *cascade_fn(int rs) {
+    if (rs == 1) return reinterpret_cast<const void *>(&paged_decode_cascade_mfma_kernel<KV, D, 1>);
+    if (rs == 2) return reinterpret_cast<const void *>(&paged_decode_cascade_mfma_kernel<KV, D, 2>);
+    return nullptr;
+}
+
+#define XHIP_FOR_CASCADE_HEAD_SIZES(X) X(32) X(64) X(96) X(128)
+
+template <int KV>
+static int cascade_occupancy_dtype(int head_size, int rs, size_t lds_bytes) {
+    const void *fn = nullptr;
+    switch (head_size) {
+#define XHIP_CASE(d) case d: fn = cascade_fn<KV, d>(rs); break;
+        XHIP_FOR_CASCADE_HEAD_SIZES(XHIP_CASE)
+#undef XHIP_CASE
+    default: break;
+    }
+    if (!fn) return 0;
+    int blocks = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 64 * kMfmaWavesPerGroup,
+                                                     lds_bytes) != hipSuccess)
+        return 0;
+    return blocks;
+}
+
+template <int KV>
+static hipError_t launch_cascade_attn_dtype(const DecodeParams &pp, const DecodeParams &ps,
+                                            const int *p_row, int rows, void *out, int head_size,
+                                            int rs, hipStream_t st, hipEvent_t ev_start,
+                                            hipEvent_t ev_stop) {
+    switch (head_size) {
+#define XHIP_CASE(d)                                                                          \
+    case d:                                                                                   \
+        if (rs == 1)                                                                          \
+            return launch_cascade_attn_rs<KV, d, 1>(pp, ps, p_row, rows, out, st, ev_start,   \
+                                                    ev_stop);                                 \
+        if (rs == 2)                                                                          \
+            return launch_cascade_attn_rs<KV, d, 2>(pp, ps, p_row, rows, out, st, ev_start,   \
+                                                    ev_stop);                                 \
+        return hipErrorInvalidValue;
+        XHIP_FOR_CASCADE_HEAD_SIZES(XHIP_CASE)
+#undef XHIP_CASE
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace xhip

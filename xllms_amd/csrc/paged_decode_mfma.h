@@ -454,6 +454,22 @@ template <int D, int R> struct MfmaRelaySlot {
     int ends[kMfmaWavesPerGroup];
 };
 
+// LDS of one workgroup of the partition kernel: the V tile staging of each
+// wavefront, and the slots of the workgroup-level combine (by mode).
+template <int FIX, int D, int R> struct MfmaSweepLds {
+    int unused;
+};
+template <int D, int R> struct MfmaSweepLds<1, D, R> {
+    MfmaFixSlot<D> fix[kMfmaWavesPerGroup];
+};
+template <int D, int R> struct MfmaSweepLds<2, D, R> {
+    MfmaRelaySlot<D, R> relay;
+};
+template <int D, int R> struct MfmaLds {
+    __attribute__((aligned(16))) char vtile[kMfmaWavesPerGroup][MfmaGeometry<D>::kLdsTile];
+    MfmaSweepLds<mfma_wg_fixup(kMfmaHeads * R, D), D, R> sw;
+};
+
 // st <- st (+) the fp32 partial in workspace slot `slot` (its l is the
 // reduced sum: lane group 0 takes it).  Rows past the group were never
 // written; they are left alone.
@@ -514,34 +530,31 @@ __device__ __forceinline__ void absorb_partial(const DecodeParams &p, int slot, 
 // pieces followed by more pieces are written as partials by every
 // wavefront, and a left neighbour absorbs such a partial from memory (the
 // workgroup barrier orders it) instead of from the relay slot.
-// Two wavefronts per SIMD (the plan's occupancy) up to head_size 128: at
-// most 256 registers each.  Larger heads need more and run one per SIMD.
+//
+// The body runs one workgroup's four ranges: logical workgroup `wg` of a
+// plan of `waves` wavefronts over the batch of p, whose split-unit prefix
+// `pre` is in LDS.
 template <int KV, int D, int R>
-__global__ __launch_bounds__(64 * kMfmaWavesPerGroup, D <= 128 ? 2 : 1) void paged_decode_partition_mfma_kernel(
-    const DecodeParams p, const int *__restrict__ lens, const int *__restrict__ tables) {
-    // lens / tables are p.seq_lens / p.block_tables again: as restrict
-    // kernel arguments their wavefront-uniform reads become scalar loads,
-    // which do not wait behind the K/V loads in flight.
+__device__ __forceinline__ void mfma_partition_body(const DecodeParams &p,
+                                                    const int *__restrict__ lens,
+                                                    const int *__restrict__ tables,
+                                                    const int *pre, int wg, int waves,
+                                                    MfmaLds<D, R> &sm) {
     using G = MfmaGeometry<D>;
     constexpr int FIX = mfma_wg_fixup(kMfmaHeads * R, D);
     constexpr int NW = kMfmaWavesPerGroup;
-    extern __shared__ int pre[];  // num_seqs + 1 split-unit prefixes
-    __shared__ __attribute__((aligned(16))) char vtile[NW][G::kLdsTile];
-    __shared__ MfmaFixSlot<D> fix[FIX == 1 ? NW : 1];
-    __shared__ MfmaRelaySlot<D, R> relay;
-
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    char *lds = vtile[wave];
+    char *lds = sm.vtile[wave];
     if constexpr (FIX == 2) {
-        if (lane == 0) relay.relayed[wave] = 0;  // ordered by batch_prefix's barriers
+        // ordered before any read by the sweep's first barrier
+        if (lane == 0) sm.sw.relay.relayed[wave] = 0;
     }
 
-    batch_prefix<16, NW>(p, pre);
     const int B = p.num_seqs;
     const int total = pre[B];
-    const int w = logical_block(p, total) * NW + wave;
-    const int tpw = tiles_per_wave(total, p.num_waves, p.min_tiles_per_wave);
+    const int w = wg * NW + wave;
+    const int tpw = tiles_per_wave(total, waves, p.min_tiles_per_wave);
     const long long g_lo = (long long)w * tpw;
 
     MfmaState<D> st[R];   // the state of the piece being computed; after the loop, the last one's
@@ -642,8 +655,8 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, D <= 128 ? 2 : 1) void pag
                     // a cut piece with more pieces after it: the wavefront's
                     // first piece, a continuation that ends its segment here
                     if (wave > 0) {
-                        fix_store<D>(fix[wave], lane, st[0]);
-                        if (lane == 0) fix[wave].ends = 1;
+                        fix_store<D>(sm.sw.fix[wave], lane, st[0]);
+                        if (lane == 0) sm.sw.fix[wave].ends = 1;
                     } else {
                         mfma_write_partial<D, R>(p, pc, lane, st);
                     }
@@ -674,20 +687,20 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, D <= 128 ? 2 : 1) void pag
                 const bool cut_start = pc.t_begin > 0;
                 bool ends = pc.t_end >= pc.L;
                 if (!ends && i < NW - 1) {
-                    if (relay.relayed[i + 1]) {
+                    if (sm.sw.relay.relayed[i + 1]) {
 #pragma unroll
                         for (int b = 0; b < R; b++) {
-                            const float mo = relay.m[b][lane];
+                            const float mo = sm.sw.relay.m[b][lane];
                             const float M = fmaxf(st[b].m, mo);
                             const float Ms = (M == -INFINITY) ? 0.0f : M;
                             const float a = fast_exp2(st[b].m - Ms), wt = fast_exp2(mo - Ms);
-                            st[b].l = st[b].l * a + relay.l[b][lane] * wt;
+                            st[b].l = st[b].l * a + sm.sw.relay.l[b][lane] * wt;
 #pragma unroll
                             for (int n = 0; n < G::kDimBlocks; n++)
-                                st[b].o[n] = st[b].o[n] * a + relay.o[b][n][lane] * wt;
+                                st[b].o[n] = st[b].o[n] * a + sm.sw.relay.o[b][n][lane] * wt;
                             st[b].m = M;
                         }
-                        ends = relay.ends[i + 1] != 0;
+                        ends = sm.sw.relay.ends[i + 1] != 0;
                     } else {
                         // the neighbour's first piece, followed by more
                         // pieces, was written as a partial in its slot 0;
@@ -700,13 +713,13 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, D <= 128 ? 2 : 1) void pag
 #pragma unroll
                     for (int b = 0; b < R; b++) {
 #pragma unroll
-                        for (int n = 0; n < G::kDimBlocks; n++) relay.o[b][n][lane] = st[b].o[n];
-                        relay.m[b][lane] = st[b].m;
-                        relay.l[b][lane] = st[b].l;
+                        for (int n = 0; n < G::kDimBlocks; n++) sm.sw.relay.o[b][n][lane] = st[b].o[n];
+                        sm.sw.relay.m[b][lane] = st[b].m;
+                        sm.sw.relay.l[b][lane] = st[b].l;
                     }
                     if (lane == 0) {
-                        relay.relayed[i] = 1;
-                        relay.ends[i] = ends ? 1 : 0;
+                        sm.sw.relay.relayed[i] = 1;
+                        sm.sw.relay.ends[i] = ends ? 1 : 0;
                     }
                 } else if (!cut_start && ends) {
                     mfma_write_rows<KV, D, R>(p, pc, lane, st);
@@ -729,12 +742,12 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, D <= 128 ? 2 : 1) void pag
                     // the right neighbour's first piece continues this
                     // segment: its state is in its slot (stored during its
                     // range, or relayed by it one step ago)
-                    fix_absorb<D>(fix[i + 1], lane, st[0]);
-                    ends = fix[i + 1].ends != 0;
+                    fix_absorb<D>(sm.sw.fix[i + 1], lane, st[0]);
+                    ends = sm.sw.fix[i + 1].ends != 0;
                 }
                 if (cut_start && i > 0) {
-                    fix_store<D>(fix[i], lane, st[0]);
-                    if (lane == 0) fix[i].ends = ends ? 1 : 0;
+                    fix_store<D>(sm.sw.fix[i], lane, st[0]);
+                    if (lane == 0) sm.sw.fix[i].ends = ends ? 1 : 0;
                 } else if (!cut_start && ends) {
                     mfma_write_rows<KV, D, R>(p, pc, lane, st);
                 } else {
@@ -744,6 +757,22 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, D <= 128 ? 2 : 1) void pag
             __syncthreads();
         }
     }
+}
+
+
+// Two wavefronts per SIMD (the plan's occupancy) up to head_size 128: at
+// most 256 registers each.  Larger heads need more and run one per SIMD.
+template <int KV, int D, int R>
+__global__ __launch_bounds__(64 * kMfmaWavesPerGroup, D <= 128 ? 2 : 1) void paged_decode_partition_mfma_kernel(
+    const DecodeParams p, const int *__restrict__ lens, const int *__restrict__ tables) {
+    // lens / tables are p.seq_lens / p.block_tables again: as restrict
+    // kernel arguments their wavefront-uniform reads become scalar loads,
+    // which do not wait behind the K/V loads in flight.
+    extern __shared__ int pre[];  // num_seqs + 1 split-unit prefixes
+    __shared__ MfmaLds<D, R> sm;
+    batch_prefix<16, kMfmaWavesPerGroup>(p, pre);
+    mfma_partition_body<KV, D, R>(p, lens, tables, pre, logical_block(p, pre[p.num_seqs]),
+                                  p.num_waves, sm);
 }
 
 }  // namespace xhip
