@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "paged_kv_append.h"
+#include "paged_decode_rows.h"
 #include "workspace.h"
 #include "xllm_hip_backend.h"
 #include "xllm_hip_kv_index.h"
@@ -126,7 +127,6 @@ struct InstanceState {
     HostBuf<int32_t> h_slots, h_src, h_dst, h_bt, h_lens, h_group, h_pblocks, h_seqs;
     HostBuf<const char *> h_kptr, h_vptr, h_qptr;
     HostBuf<char *> h_optr;
-    DevBuf<char> d_q, d_out;
     HostBuf<char> h_pack;  // every array an exec uploads, 256-byte aligned parts
     DevBuf<char> d_pack;
 
@@ -223,8 +223,6 @@ void destroy_state(InstanceState *st) {
     st->h_optr.release();
     st->h_pack.release();
     st->d_pack.release();
-    st->d_q.release();
-    st->d_out.release();
     // the operator layer keeps split-K / cascade workspaces per stream:
     // free this stream's before the handle goes (it may be reused)
     if (st->stream) (void)xhip_release_stream_workspaces(st->device, st->stream);
@@ -353,9 +351,7 @@ XMI_EXPORT int nxt_model_instance_init(NxtModelInstance *instance) {
                     cache_bytes);
     }
     st->index = nxt_kv_index_create(s.num_blocks, s.block_size, s.max_blocks);
-    const size_t row = (size_t)s.num_heads * s.head_size * s.elem_bytes;
-    if (!st->index || !st->d_q.reserve((size_t)s.max_batch * row) ||
-        !st->d_out.reserve((size_t)s.max_batch * row)) {
+    if (!st->index) {
         destroy_state(st);
         return fail("instance init: out of memory");
     }
@@ -535,7 +531,6 @@ int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<st
 
     tr.mark("index");
     // 2. the attention batch: requests with a query, their tables and groups
-    const size_t qrow = (size_t)s.num_heads * s.head_size * s.elem_bytes;
     st->h_seqs.n = st->h_qptr.n = st->h_optr.n = 0;
     st->h_bt.n = st->h_lens.n = st->h_group.n = st->h_pblocks.n = 0;
     int width = 1, ng = 0;
@@ -582,11 +577,11 @@ int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<st
     if (st->h_pack.n == (size_t)-1) {
         rc = fail("exec: out of host memory");
     } else if (st->h_pack.n > 0) {
-        if (!st->d_pack.reserve(st->h_pack.n)) {
+        if (!st->d_pack.reserve((st->h_pack.n + 15) & ~(size_t)15)) {
             rc = fail("exec: out of device memory");
         } else {
-            e = hipMemcpyAsync(st->d_pack.p, st->h_pack.p, st->h_pack.n, hipMemcpyHostToDevice,
-                               st->stream);
+            e = xhip::launch_stage_copy(st->d_pack.p, st->h_pack.p, (st->h_pack.n + 15) & ~(size_t)15,
+                                        st->stream);
             staged = e == hipSuccess;
         }
     }
@@ -623,33 +618,29 @@ int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<st
     if (e != hipSuccess) rc = fail("exec: K/V write: %s", hipGetErrorString(e));
     const int B = (int)st->h_seqs.n;
     if (rc == 0 && staged && B > 0) {
-        int a = NXT_ATTN_OK;
-        e = xhip::launch_gather_rows(st->d_q.p, (const char *const *)at(o_qptr), (int)qrow, B,
-                                     st->stream);
-        if (e == hipSuccess) {
-            const int kbs = s.num_kv_heads * s.block_size * s.head_size;
-            const int khs = s.block_size * s.head_size;
-            const int *bt = (const int *)at(o_bt), *lens = (const int *)at(o_lens);
-            a = ng > 0 ? nxt_paged_attention_cascade(
-                             st->d_out.p, st->d_q.p, st->key_cache, st->value_cache, bt, lens,
-                             (const int *)at(o_group), (const int *)at(o_pblocks), ng, B,
-                             s.num_heads, s.head_size, s.num_kv_heads, s.scale, width,
-                             s.block_size, kbs, khs, s.kv_dtype, st->stream)
-                       : nxt_paged_attention_ex(st->d_out.p, st->d_q.p, st->key_cache,
-                                                st->value_cache, bt, lens, B, s.num_heads,
-                                                s.head_size, s.num_kv_heads, s.scale, width,
-                                                s.block_size, s.elem_bytes, kbs, khs, st->stream,
-                                                s.kv_dtype, 0);
-            if (a == NXT_ATTN_OK)
-                e = xhip::launch_scatter_rows((char *const *)at(o_optr), st->d_out.p, (int)qrow,
-                                              B, st->stream);
-        }
-        if (e != hipSuccess) rc = fail("exec: attention: %s", hipGetErrorString(e));
+        // the attention reads each request's query rows and writes its output
+        // rows in place, through the staged row pointer tables
+        const int kbs = s.num_kv_heads * s.block_size * s.head_size;
+        const int khs = s.block_size * s.head_size;
+        const int *bt = (const int *)at(o_bt), *lens = (const int *)at(o_lens);
+        const char *const *qr = (const char *const *)at(o_qptr);
+        char *const *orw = (char *const *)at(o_optr);
+        const int a =
+            ng > 0 ? xhip_paged_attention_cascade_rows(
+                         qr, orw, st->key_cache, st->value_cache, bt, lens,
+                         (const int *)at(o_group), (const int *)at(o_pblocks), ng, B, s.num_heads,
+                         s.head_size, s.num_kv_heads, s.scale, width, s.block_size, kbs, khs,
+                         s.kv_dtype, st->stream)
+                   : xhip_paged_attention_rows(qr, orw, st->key_cache, st->value_cache, bt, lens,
+                                               B, s.num_heads, s.head_size, s.num_kv_heads,
+                                               s.scale, width, s.block_size, kbs, khs, s.kv_dtype,
+                                               st->stream);
         if (a != NXT_ATTN_OK) rc = fail("exec: attention: %s", nxt_attn_last_error());
     }
 
     tr.mark("launch");
-    // 4. wait for the device, then end the released requests
+    // 4. wait for the device, then end the released requests (polling
+    //    hipStreamQuery instead took 6-8 us longer per exec)
     e = hipStreamSynchronize(st->stream);
     if (e != hipSuccess && rc == 0) rc = fail("exec: %s", hipGetErrorString(e));
     for (const Item &it : items) {

@@ -18,6 +18,7 @@
 #include "paged_decode_cascade.h"
 #include "paged_decode_launch.h"
 #include "paged_decode_params.h"
+#include "paged_decode_rows.h"
 #include "paged_decode_scratch.h"
 #include "paged_kv_append.h"
 #include "workspace.h"
@@ -269,6 +270,15 @@ struct FixedWs {
     size_t bytes;
 };
 
+// Per-sequence query and output rows (device arrays of num_seqs row
+// pointers, each row block [num_heads][head_size], 16-byte aligned) instead
+// of the contiguous query / out arrays: the model instance's requests keep
+// their own buffers.
+struct RowPtrs {
+    const char *const *q;
+    char *const *o;
+};
+
 // The fields of a launch's DecodeParams that come straight from its batch.
 void fill_batch(DecodeParams &p, const void *query, const void *key_cache, const void *value_cache,
                 const int *block_tables, const int *seq_lens, int nseq, int num_heads,
@@ -299,7 +309,7 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         int num_kv_heads, float scale, int max_num_blocks_per_seq, int block_size, int dtype_size,
         int kv_block_stride, int kv_head_stride, nxt_stream_t stream_handle, int kv_dtype,
         int partition_tokens, const PartialOut *po = nullptr, const PrefixFold *fold = nullptr,
-        const FixedWs *fixed = nullptr) {
+        const FixedWs *fixed = nullptr, const RowPtrs *rows = nullptr) {
     // ---- argument checks (host only; nothing is read from the device)
     if (kv_dtype != NXT_KV_FP16 && kv_dtype != NXT_KV_BF16 && kv_dtype != NXT_KV_FP32)
         return set_status(NXT_ATTN_E_UNSUPPORTED, "kv_dtype %d is not FP16/BF16/FP32", kv_dtype);
@@ -336,14 +346,17 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
     if (!head_tiling(group, mfma, head_size, &tiling))
         return set_status(NXT_ATTN_E_UNSUPPORTED, "GQA group %d > %d", group, max_group(mfma));
     if (num_seqs == 0) return ok();
-    const void *out_any = po ? (const void *)po->out_f32 : out;
-    if (!out_any || !query || !key_cache || !value_cache || !block_tables || !seq_lens ||
+    const void *out_any = po ? (const void *)po->out_f32 : rows ? (const void *)rows->o : out;
+    const void *q_any = rows ? (const void *)rows->q : query;
+    if (!out_any || !q_any || !key_cache || !value_cache || !block_tables || !seq_lens ||
         (po && !po->out_lse))
         return set_status(NXT_ATTN_E_INVALID, "NULL tensor pointer");
     const int eb = elem_bytes(kv_dtype);
-    if (((uintptr_t)out_any | (uintptr_t)query | (uintptr_t)key_cache | (uintptr_t)value_cache) &
-        15)
+    if (((uintptr_t)(po ? out_any : rows ? nullptr : out) | (uintptr_t)(rows ? nullptr : query) |
+         (uintptr_t)key_cache | (uintptr_t)value_cache) & 15)
         return set_status(NXT_ATTN_E_UNSUPPORTED, "tensors must be 16-byte aligned");
+    if (rows && (((uintptr_t)rows->q | (uintptr_t)rows->o) & 7))
+        return set_status(NXT_ATTN_E_INVALID, "row pointer tables must be 8-byte aligned");
     if ((((long long)kv_block_stride * eb) & 15) || (((long long)kv_head_stride * eb) & 15))
         return set_status(NXT_ATTN_E_UNSUPPORTED, "kv strides must be multiples of 16 bytes");
     if ((uintptr_t)block_tables & 3 || (uintptr_t)seq_lens & 3)
@@ -428,7 +441,9 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         const size_t row0 = (size_t)s0 * num_heads * head_size * eb_total;
         DecodeParams p;
         memset(&p, 0, sizeof(p));
-        p.out = out ? (char *)out + row0 : nullptr;
+        p.out = out && !rows ? (char *)out + row0 : nullptr;
+        p.q_rows = rows ? rows->q + s0 : nullptr;
+        p.o_rows = rows ? rows->o + s0 : nullptr;
         if (po) {
             p.out_f32 = po->out_f32 + (size_t)s0 * num_heads * head_size;
             p.out_lse = po->out_lse + (size_t)s0 * num_heads;
@@ -442,7 +457,7 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
             p.fold_rows = fold->rows;
             p.fold_kr = fold->kr;
         }
-        fill_batch(p, (const char *)query + row0, key_cache, value_cache,
+        fill_batch(p, rows ? nullptr : (const char *)query + row0, key_cache, value_cache,
                    block_tables + (size_t)s0 * max_num_blocks_per_seq, seq_lens + s0, nseq,
                    num_heads, num_kv_heads, tiling.head_tiles, max_num_blocks_per_seq, block_size,
                    kv_block_stride, kv_head_stride, scale);
@@ -496,21 +511,22 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
                 const int *prefix_blocks, int max_groups, int num_seqs, int num_heads,
                 int head_size, int num_kv_heads, float scale, int max_num_blocks_per_seq,
                 int block_size, int kv_block_stride, int kv_head_stride, int kv_dtype,
-                nxt_stream_t stream_handle) {
+                nxt_stream_t stream_handle, const RowPtrs *rowp = nullptr) {
     if (max_groups < 0) return set_status(NXT_ATTN_E_INVALID, "max_groups %d < 0", max_groups);
     const int eb = (kv_dtype == NXT_KV_FP16 || kv_dtype == NXT_KV_BF16) ? 2 : 4;
     if (max_groups == 0 || num_seqs <= 0)  // nothing shared: the ordinary decode
         return run(out, query, key_cache, value_cache, block_tables, seq_lens, num_seqs, num_heads,
                    head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size, eb,
-                   kv_block_stride, kv_head_stride, stream_handle, kv_dtype, 0);
+                   kv_block_stride, kv_head_stride, stream_handle, kv_dtype, 0, nullptr, nullptr,
+                   nullptr, rowp);
     if (!prefix_group || !prefix_blocks)
         return set_status(NXT_ATTN_E_INVALID, "NULL prefix_group / prefix_blocks");
     if (num_seqs > xhip::kMaxSeqsPerLaunch || max_groups > num_seqs)
         return set_status(NXT_ATTN_E_UNSUPPORTED,
                           "cascade batch of %d sequences / %d groups (limits %d, num_seqs)",
                           num_seqs, max_groups, xhip::kMaxSeqsPerLaunch);
-    if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads || !out ||
-        max_num_blocks_per_seq <= 0 || !is_pow2(block_size))
+    if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads ||
+        !(rowp ? (const void *)rowp->o : out) || max_num_blocks_per_seq <= 0 || !is_pow2(block_size))
         return set_status(NXT_ATTN_E_INVALID, "bad cascade arguments");
     const int group = num_heads / num_kv_heads;
     // Query rows per kv head of a prefix-batch sequence: 64 (two 32-head
@@ -597,6 +613,7 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
     c.block_tables = block_tables;
     c.seq_lens = seq_lens;
     c.q = query;
+    c.q_rows = rowp ? rowp->q : nullptr;
     c.out = out;
     c.prefix_group = prefix_group;
     c.prefix_blocks = prefix_blocks;
@@ -639,9 +656,12 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
         fill_batch(pp, c.v_q, key_cache, value_cache, c.v_bt, c.v_lens, (int)v_max, (int)KR,
                    num_kv_heads, rows / 32, max_num_blocks_per_seq, block_size, kv_block_stride,
                    kv_head_stride, scale);
-        fill_batch(ps, query, key_cache, value_cache, c.s_bt, c.s_lens, num_seqs, num_heads,
-                   num_kv_heads, stile.head_tiles, max_num_blocks_per_seq, block_size,
+        fill_batch(ps, rowp ? nullptr : query, key_cache, value_cache, c.s_bt, c.s_lens, num_seqs,
+                   num_heads, num_kv_heads, stile.head_tiles, max_num_blocks_per_seq, block_size,
                    kv_block_stride, kv_head_stride, scale);
+        ps.out = rowp ? nullptr : out;  // the merge's output rows
+        ps.q_rows = rowp ? rowp->q : nullptr;
+        ps.o_rows = rowp ? rowp->o : nullptr;
         for (DecodeParams *q : {&pp, &ps}) {
             q->num_waves = (int)fw;
             q->min_tiles_per_wave = kMinTilesPerWave;
@@ -662,9 +682,9 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
         ps.ws_prefix = (int *)(w + o_yp);
         const int rs = stile.head_tile / xhip::kMfmaHeads;
         e = kv_dtype == NXT_KV_FP16
-                ? xhip::launch_cascade_attn_f16(pp, ps, c.p_row, rows, out, head_size, rs, stream,
+                ? xhip::launch_cascade_attn_f16(pp, ps, c.p_row, rows, head_size, rs, stream,
                                                 t_trace_start, t_trace_partition)
-                : xhip::launch_cascade_attn_bf16(pp, ps, c.p_row, rows, out, head_size, rs, stream,
+                : xhip::launch_cascade_attn_bf16(pp, ps, c.p_row, rows, head_size, rs, stream,
                                                  t_trace_start, t_trace_partition);
         if (e != hipSuccess)
             return set_status(NXT_ATTN_E_HIP, "cascade attention launch: %s", hipGetErrorString(e));
@@ -681,7 +701,8 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
                           (int)KR};
     return run(out, query, key_cache, value_cache, c.s_bt, c.s_lens, num_seqs, num_heads,
                head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size, eb,
-               kv_block_stride, kv_head_stride, stream_handle, kv_dtype, 0, nullptr, &fold);
+               kv_block_stride, kv_head_stride, stream_handle, kv_dtype, 0, nullptr, &fold,
+               nullptr, rowp);
 }
 
 // KV append (decode: block_tables + positions; prefill: slots).
@@ -972,12 +993,18 @@ __attribute__((visibility("default"))) int nxt_activation_ex(int op, void *out, 
     return activation_run(op, out, input, num_tokens, d, dtype, stream);
 }
 
-__attribute__((visibility("default"))) int nxt_paged_attention_cascade(
-    void *out, const void *query, const void *key_cache, const void *value_cache,
-    const int *block_tables, const int *seq_lens, const int *prefix_group,
-    const int *prefix_blocks, int max_groups, int num_seqs, int num_heads, int head_size,
-    int num_kv_heads, float scale, int max_num_blocks_per_seq, int block_size,
-    int kv_block_stride, int kv_head_stride, int kv_dtype, nxt_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// nxt_paged_attention_cascade's checks and run, with contiguous query / out
+// or per-sequence rows (rowp).
+int cascade_entry(void *out, const void *query, const RowPtrs *rowp, const void *key_cache,
+                  const void *value_cache, const int *block_tables, const int *seq_lens,
+                  const int *prefix_group, const int *prefix_blocks, int max_groups, int num_seqs,
+                  int num_heads, int head_size, int num_kv_heads, float scale,
+                  int max_num_blocks_per_seq, int block_size, int kv_block_stride,
+                  int kv_head_stride, int kv_dtype, nxt_stream_t stream) {
     // the ordinary path's argument checks, without launching anything
     const int eb = (kv_dtype == NXT_KV_FP16 || kv_dtype == NXT_KV_BF16) ? 2 : 4;
     int st = run(out, query, key_cache, value_cache, block_tables, seq_lens, 0, num_heads,
@@ -988,19 +1015,65 @@ __attribute__((visibility("default"))) int nxt_paged_attention_cascade(
     if (num_seqs == 0) return ok();
     // the checks run() makes only for a non-empty batch: the cascade plan
     // reads these arrays before any pass of run() is reached
-    if (!out || !query || !key_cache || !value_cache || !block_tables || !seq_lens)
+    const void *o_any = rowp ? (const void *)rowp->o : out;
+    const void *q_any = rowp ? (const void *)rowp->q : query;
+    if (!o_any || !q_any || !key_cache || !value_cache || !block_tables || !seq_lens)
         return set_status(NXT_ATTN_E_INVALID, "NULL tensor pointer");
     if (max_groups > 0 && (!prefix_group || !prefix_blocks))
         return set_status(NXT_ATTN_E_INVALID, "NULL prefix_group / prefix_blocks");
-    if (((uintptr_t)out | (uintptr_t)query | (uintptr_t)key_cache | (uintptr_t)value_cache) & 15)
+    if (((uintptr_t)(rowp ? nullptr : out) | (uintptr_t)(rowp ? nullptr : query) |
+         (uintptr_t)key_cache | (uintptr_t)value_cache) & 15)
         return set_status(NXT_ATTN_E_UNSUPPORTED, "tensors must be 16-byte aligned");
+    if (rowp && (((uintptr_t)rowp->q | (uintptr_t)rowp->o) & 7))
+        return set_status(NXT_ATTN_E_INVALID, "row pointer tables must be 8-byte aligned");
     if (((uintptr_t)block_tables | (uintptr_t)seq_lens | (uintptr_t)prefix_group |
          (uintptr_t)prefix_blocks) & 3)
         return set_status(NXT_ATTN_E_INVALID, "int32 arrays must be 4-byte aligned");
     return cascade_run(out, query, key_cache, value_cache, block_tables, seq_lens, prefix_group,
                        prefix_blocks, max_groups, num_seqs, num_heads, head_size, num_kv_heads,
                        scale, max_num_blocks_per_seq, block_size, kv_block_stride,
-                       kv_head_stride, kv_dtype, stream);
+                       kv_head_stride, kv_dtype, stream, rowp);
+}
+
+}  // namespace
+
+extern "C" {
+
+__attribute__((visibility("default"))) int nxt_paged_attention_cascade(
+    void *out, const void *query, const void *key_cache, const void *value_cache,
+    const int *block_tables, const int *seq_lens, const int *prefix_group,
+    const int *prefix_blocks, int max_groups, int num_seqs, int num_heads, int head_size,
+    int num_kv_heads, float scale, int max_num_blocks_per_seq, int block_size,
+    int kv_block_stride, int kv_head_stride, int kv_dtype, nxt_stream_t stream) {
+    return cascade_entry(out, query, nullptr, key_cache, value_cache, block_tables, seq_lens,
+                         prefix_group, prefix_blocks, max_groups, num_seqs, num_heads, head_size,
+                         num_kv_heads, scale, max_num_blocks_per_seq, block_size,
+                         kv_block_stride, kv_head_stride, kv_dtype, stream);
+}
+
+__attribute__((visibility("hidden"))) int xhip_paged_attention_rows(
+    const char *const *q_rows, char *const *o_rows, const void *key_cache,
+    const void *value_cache, const int *block_tables, const int *seq_lens, int num_seqs,
+    int num_heads, int head_size, int num_kv_heads, float scale, int max_num_blocks_per_seq,
+    int block_size, int kv_block_stride, int kv_head_stride, int kv_dtype, nxt_stream_t stream) {
+    const RowPtrs rows{q_rows, o_rows};
+    return run(nullptr, nullptr, key_cache, value_cache, block_tables, seq_lens, num_seqs,
+               num_heads, head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size,
+               elem_bytes(kv_dtype), kv_block_stride, kv_head_stride, stream, kv_dtype, 0,
+               nullptr, nullptr, nullptr, &rows);
+}
+
+__attribute__((visibility("hidden"))) int xhip_paged_attention_cascade_rows(
+    const char *const *q_rows, char *const *o_rows, const void *key_cache,
+    const void *value_cache, const int *block_tables, const int *seq_lens,
+    const int *prefix_group, const int *prefix_blocks, int max_groups, int num_seqs,
+    int num_heads, int head_size, int num_kv_heads, float scale, int max_num_blocks_per_seq,
+    int block_size, int kv_block_stride, int kv_head_stride, int kv_dtype, nxt_stream_t stream) {
+    const RowPtrs rows{q_rows, o_rows};
+    return cascade_entry(nullptr, nullptr, &rows, key_cache, value_cache, block_tables, seq_lens,
+                         prefix_group, prefix_blocks, max_groups, num_seqs, num_heads, head_size,
+                         num_kv_heads, scale, max_num_blocks_per_seq, block_size,
+                         kv_block_stride, kv_head_stride, kv_dtype, stream);
 }
 
 __attribute__((visibility("default"))) int nxt_paged_prefix_groups(

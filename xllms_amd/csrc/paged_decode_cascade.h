@@ -26,6 +26,7 @@ struct CascadeParams {
     const int *block_tables;   // [num_seqs][max_blocks]
     const int *seq_lens;       // [num_seqs]
     const void *q;             // [num_seqs][num_heads][head_size]
+    const char *const *q_rows; // non-null: sequence s's query rows start at q_rows[s] (q unused)
     void *out;                 // [num_seqs][num_heads][head_size], element type
     const int *prefix_group;   // [num_seqs] group id < max_groups, or -1
     const int *prefix_blocks;  // [max_groups] shared full pages of each group
@@ -59,15 +60,16 @@ hipError_t launch_cascade_plan(const CascadeParams &c, hipStream_t stream);
 // Attention of the cascade on the MFMA tile path (paged_decode_cascade_attn.h):
 // the prefix batch pp (32-row head tiles) and the suffix batch ps (head
 // tiles of 16 * rs rows) in one partition launch of ps.num_waves
-// wavefronts (>= 8), then the merge that writes `out` from both.
+// wavefronts (>= 8), then the merge that writes ps's output rows (ps.out or
+// ps.o_rows) from both.
 // head_size 32, 64, 96 or 128; hipErrorInvalidValue otherwise.
 int cascade_attn_occupancy_f16(int head_size, int rs, size_t lds_bytes);
 int cascade_attn_occupancy_bf16(int head_size, int rs, size_t lds_bytes);
 hipError_t launch_cascade_attn_f16(const DecodeParams &pp, const DecodeParams &ps,
-                                   const int *p_row, int rows, void *out, int head_size, int rs,
+                                   const int *p_row, int rows, int head_size, int rs,
                                    hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
 hipError_t launch_cascade_attn_bf16(const DecodeParams &pp, const DecodeParams &ps,
-                                    const int *p_row, int rows, void *out, int head_size, int rs,
+                                    const int *p_row, int rows, int head_size, int rs,
                                     hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
 
 // Detection of shared prefixes from the block tables (one workgroup,

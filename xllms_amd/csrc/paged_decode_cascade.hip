@@ -227,10 +227,11 @@ __global__ __launch_bounds__(256) void cascade_plan_gather_kernel(const CascadeP
             const int r = rig / c.group, gq = rig - r * c.group;
             if (r >= c.g_count[g]) continue;  // no member: never read
             const int s = c.member_seq[c.g_moff[g] + r];
-            const size_t src = ((size_t)s * c.num_heads + (size_t)h * c.group + gq) * row_bytes +
-                               (size_t)ch * 16;
+            const size_t hrow = (size_t)h * c.group + gq;
+            const char *src = c.q_rows ? c.q_rows[s] + hrow * row_bytes
+                                       : (const char *)c.q + ((size_t)s * c.num_heads + hrow) * row_bytes;
             const size_t dst = ((size_t)v * KR + hj) * row_bytes + (size_t)ch * 16;
-            *(u32x4_t *)((char *)c.v_q + dst) = *(const u32x4_t *)((const char *)c.q + src);
+            *(u32x4_t *)((char *)c.v_q + dst) = *(const u32x4_t *)(src + (size_t)ch * 16);
         } else if (i < n1 + n2) {
             const long long k = i - n1;
             const int v = (int)(k / c.max_blocks), b = (int)(k - (long long)v * c.max_blocks);

@@ -124,13 +124,14 @@ __device__ __forceinline__ void segment_state(const DecodeParams &p, int s, int 
 }
 
 // Merge over every suffix segment (sequence s, kv head, head tile of GTS
-// heads), NT threads striding over its float4 columns.  p_row[s] is the row,
+// heads), NT threads striding over its float4 columns, writing the output
+// rows of ps (ps.out or ps.o_rows; its partial-output buffers hold the
+// suffix states).  p_row[s] is the row,
 // in the prefix batch's rows of a kv head laid end to end (`rows` per
 // prefix-batch sequence), of s's first query head; -1: s has no prefix.
 template <int KV, int D, int GTS, int NT>
 __global__ __launch_bounds__(NT) void paged_decode_cascade_merge_kernel(
-    const DecodeParams pp, const DecodeParams ps, const int *__restrict__ p_row, int rows,
-    void *out) {
+    const DecodeParams pp, const DecodeParams ps, const int *__restrict__ p_row, int rows) {
     constexpr int C4 = D / 4;
     constexpr int NW = kMfmaWavesPerGroup;
     constexpr int GTP = 2 * kMfmaHeads;
@@ -170,15 +171,15 @@ __global__ __launch_bounds__(NT) void paged_decode_cascade_merge_kernel(
             }
         }
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        const size_t base = (srow0 + h) * D + c * 4;
+        char *orow = o_row(ps, s, kvh * ps.group + g0 + h, D, 2);
 #pragma unroll
-        for (int e = 0; e < 4; e++) store_elem<KV>(out, base + e, acc[e] * inv);
+        for (int e = 0; e < 4; e++) store_elem<KV>(orow, c * 4 + e, acc[e] * inv);
     }
 }
 
 template <int KV, int D, int RS>
 static hipError_t launch_cascade_attn_rs(const DecodeParams &pp, const DecodeParams &ps,
-                                         const int *p_row, int rows, void *out, hipStream_t st,
+                                         const int *p_row, int rows, hipStream_t st,
                                          hipEvent_t ev_start, hipEvent_t ev_stop) {
     const unsigned grid = (unsigned)(ps.num_waves / kMfmaWavesPerGroup);
     const size_t lds = (size_t)(pp.num_seqs + ps.num_seqs + 2) * sizeof(int);
@@ -194,7 +195,7 @@ static hipError_t launch_cascade_attn_rs(const DecodeParams &pp, const DecodePar
     if (e != hipSuccess) return e;
     const unsigned segs = (unsigned)(ps.num_seqs * ps.num_kv_heads * ps.head_tiles);
     paged_decode_cascade_merge_kernel<KV, D, kMfmaHeads * RS, 128>
-        <<<segs, 128, 0, st>>>(pp, ps, p_row, rows, out);
+        <<<segs, 128, 0, st>>>(pp, ps, p_row, rows);
     return hipGetLastError();
 }
 
@@ -226,17 +227,17 @@ static int cascade_occupancy_dtype(int head_size, int rs, size_t lds_bytes) {
 
 template <int KV>
 static hipError_t launch_cascade_attn_dtype(const DecodeParams &pp, const DecodeParams &ps,
-                                            const int *p_row, int rows, void *out, int head_size,
+                                            const int *p_row, int rows, int head_size,
                                             int rs, hipStream_t st, hipEvent_t ev_start,
                                             hipEvent_t ev_stop) {
     switch (head_size) {
 #define XHIP_CASE(d)                                                                          \
     case d:                                                                                   \
         if (rs == 1)                                                                          \
-            return launch_cascade_attn_rs<KV, d, 1>(pp, ps, p_row, rows, out, st, ev_start,   \
+            return launch_cascade_attn_rs<KV, d, 1>(pp, ps, p_row, rows, st, ev_start,   \
                                                     ev_stop);                                 \
         if (rs == 2)                                                                          \
-            return launch_cascade_attn_rs<KV, d, 2>(pp, ps, p_row, rows, out, st, ev_start,   \
+            return launch_cascade_attn_rs<KV, d, 2>(pp, ps, p_row, rows, st, ev_start,   \
                                                     ev_stop);                                 \
         return hipErrorInvalidValue;
         XHIP_FOR_CASCADE_HEAD_SIZES(XHIP_CASE)

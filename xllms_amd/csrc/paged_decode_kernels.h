@@ -377,6 +377,19 @@ __device__ __forceinline__ void decode_partition(const DecodeParams &p, const in
     }
 }
 
+// Query row of (sequence s, query head h) and output row of the same: from
+// the per-sequence row tables when set, else the contiguous batch arrays.
+// eb: bytes per element.
+__device__ __forceinline__ const char *q_row(const DecodeParams &p, int s, int h, int D, int eb) {
+    return p.q_rows ? p.q_rows[s] + (size_t)h * D * eb
+                    : (const char *)p.q + ((size_t)s * p.num_heads + h) * D * eb;
+}
+
+__device__ __forceinline__ char *o_row(const DecodeParams &p, int s, int h, int D, int eb) {
+    return p.o_rows ? p.o_rows[s] + (size_t)h * D * eb
+                    : (char *)p.out + ((size_t)s * p.num_heads + h) * D * eb;
+}
+
 // Clamped length of sequence s.
 __device__ __forceinline__ int seq_len_of(const DecodeParams &p, int s) {
     const int L = p.seq_lens[s];
@@ -555,7 +568,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
 #pragma unroll
         for (int h = 0; h < GT; h++) {
             st.q[h] = (h < nh && col_ok)
-                          ? load16((const char *)p.q + (qrow0 + (size_t)h * D + col * VEC) * EB)
+                          ? load16(q_row(p, s, kvh * p.group + g0 + h, D, EB) + col * VEC * EB)
                           : u32x4{0, 0, 0, 0};
             st.m[h] = -INFINITY;
             st.l[h] = 0.0f;
@@ -628,7 +641,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
                 float f[VEC];
 #pragma unroll
                 for (int e = 0; e < VEC; e++) f[e] = st.o[h][e] * inv;
-                *(u32x4 *)((char *)p.out + (qrow0 + (size_t)h * D + col * VEC) * EB) =
+                *(u32x4 *)(o_row(p, s, kvh * p.group + g0 + h, D, EB) + col * VEC * EB) =
                     float_to_chunk<KV, VEC>(f);
             }
         } else {
@@ -747,8 +760,9 @@ __device__ __forceinline__ void write_empty_column(const DecodeParams &p, int s,
         *(f32x4 *)(p.out_f32 + base) = o;
         if (col % C4 == 0) p.out_lse[qrow0 / D + col / C4] = lse;
     } else {
+        char *orow = o_row(p, s, kvh * p.group + g0 + col / C4, D, KV == KV_F32 ? 4 : 2);
 #pragma unroll
-        for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, o[e]);
+        for (int e = 0; e < 4; e++) store_elem<KV>(orow, (col % C4) * 4 + e, o[e]);
     }
 }
 
@@ -836,8 +850,9 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
         if (c == 0) p.out_lse[qrow0 / D + h] = ll > 0.0f ? mm + log2f(ll) : -INFINITY;
         return;
     }
+    char *orow = o_row(p, s, kvh * p.group + g0 + h, D, KV == KV_F32 ? 4 : 2);
 #pragma unroll
-    for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, aa[e] * inv);
+    for (int e = 0; e < 4; e++) store_elem<KV>(orow, c * 4 + e, aa[e] * inv);
 }
 
 
@@ -929,8 +944,9 @@ __global__ __launch_bounds__(NT) void paged_decode_merge_segment_kernel(const De
         if (cl % C4 == 0) p.out_lse[qrow0 / D + cl / C4] = l > 0.0f ? m + log2f(l) : -INFINITY;
         return;
     }
+    char *orow = o_row(p, s, kvh * p.group + g0 + cl / C4, D, KV == KV_F32 ? 4 : 2);
 #pragma unroll
-    for (int e = 0; e < 4; e++) store_elem<KV>(p.out, base + e, acc[e] * inv);
+    for (int e = 0; e < 4; e++) store_elem<KV>(orow, (cl % C4) * 4 + e, acc[e] * inv);
 }
 
 }  // namespace xhip

@@ -282,14 +282,13 @@ __device__ __forceinline__ void mfma_load_q(const DecodeParams &p, const MfmaPie
     const int j = lane & 15, g = lane >> 4;
     const int g0 = pc.ht * kMfmaHeads * R;
     const int nh = min(kMfmaHeads * R, p.group - g0);
-    const size_t qrow0 = ((size_t)pc.s * p.num_heads + (size_t)pc.kvh * p.group + g0) * D;
+    const char *q0 = q_row(p, pc.s, pc.kvh * p.group + g0, D, 2);
 #pragma unroll
     for (int b = 0; b < R; b++)
 #pragma unroll
         for (int c = 0; c < MfmaGeometry<D>::kQkSteps; c++)
             q[b][c] = (16 * b + j < nh)
-                          ? load16((const char *)p.q +
-                                   (qrow0 + (size_t)(16 * b + j) * D + 32 * c + 8 * g) * 2)
+                          ? load16(q0 + ((size_t)(16 * b + j) * D + 32 * c + 8 * g) * 2)
                           : u32x4{0, 0, 0, 0};
 }
 
@@ -378,7 +377,7 @@ __device__ __forceinline__ void mfma_write_rows(const DecodeParams &p, const Mfm
             for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st[b].o[n] * inv;
             if (gq == 0) p.out_lse[qrow0 / D + hj] = l > 0.0f ? st[b].m + log2f(l) : -INFINITY;
         } else {
-            char *dst = (char *)p.out + (qrow0 + (size_t)hj * D + 4 * gq) * 2;
+            char *dst = o_row(p, pc.s, pc.kvh * p.group + g0 + hj, D, 2) + 4 * gq * 2;
 #pragma unroll
             for (int n = 0; n < G::kDimBlocks; n++) {
                 const f32x4 o = st[b].o[n] * inv;

@@ -54,6 +54,12 @@ constexpr int mfma_wg_fixup(int rows_per_tile, int head_size) {
 struct DecodeParams {
     void *out;                 // [num_seqs][num_heads][head_size], element type
     const void *q;             // [num_seqs][num_heads][head_size]
+    // Per-sequence rows (the serving path, whose requests keep their own
+    // query and output buffers): when set, sequence s's [num_heads][head_size]
+    // query rows start at q_rows[s] and its output rows at o_rows[s], and
+    // q / out are unused.
+    const char *const *q_rows;
+    char *const *o_rows;
     const void *k;             // paged K cache (element type)
     const void *v;             // paged V cache
     const int *block_tables;   // [num_seqs][max_blocks]

@@ -39,12 +39,8 @@ struct KvAppendParams {
 
 hipError_t launch_kv_append(const KvAppendParams &p, hipStream_t stream);
 
-// Row i (row_bytes, a multiple of 16) of src[i] -> dst + i * row_bytes, and
-// back: the per-request query / output buffers of a batch to and from the
-// contiguous [num_seqs][num_heads][head_size] tensors of the decode kernels.
-hipError_t launch_gather_rows(void *dst, const char *const *src, int row_bytes, int n,
-                              hipStream_t stream);
-hipError_t launch_scatter_rows(char *const *dst, const void *src, int row_bytes, int n,
-                               hipStream_t stream);
+// Copies `bytes` (a multiple of 16; both addresses 16-byte aligned) from
+// host-pinned memory to device memory with a kernel on `stream`.
+hipError_t launch_stage_copy(void *dst, const void *host_src, size_t bytes, hipStream_t stream);
 
 }  // namespace xhip

@@ -94,46 +94,26 @@ hipError_t launch_kv_append(const KvAppendParams &params, hipStream_t stream) {
     return hipSuccess;
 }
 
-__global__ __launch_bounds__(256) void gather_rows_kernel(char *dst, const char *const *src,
-                                                          int chunks, int n) {
-    const long long total = (long long)n * chunks;
+// Staging copy by the device: n16 16-byte chunks from host-pinned memory
+// (read over the host link) into device memory.  The model instance stages
+// each exec's arrays this way instead of with a DMA copy: a small copy went
+// through the DMA engine in ~6.7 us plus its submission, this kernel's reads
+// take one host-link round trip.
+__global__ __launch_bounds__(256) void stage_copy_kernel(const u32x4 *__restrict__ src,
+                                                         u32x4 *__restrict__ dst, long long n16) {
     const long long stride = (long long)gridDim.x * blockDim.x;
-    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-        const int r = (int)(i / chunks), c = (int)(i % chunks);
-        *(u32x4 *)(dst + i * 16) = *(const u32x4 *)(src[r] + (size_t)c * 16);
-    }
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+        dst[i] = src[i];
 }
 
-__global__ __launch_bounds__(256) void scatter_rows_kernel(char *const *dst, const char *src,
-                                                           int chunks, int n) {
-    const long long total = (long long)n * chunks;
-    const long long stride = (long long)gridDim.x * blockDim.x;
-    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-        const int r = (int)(i / chunks), c = (int)(i % chunks);
-        *(u32x4 *)(dst[r] + (size_t)c * 16) = *(const u32x4 *)(src + i * 16);
-    }
-}
-
-static unsigned copy_grid(long long chunks) {
-    long long blocks = (chunks + 255) / 256;
-    return (unsigned)(blocks > 4096 ? 4096 : blocks);
-}
-
-hipError_t launch_gather_rows(void *dst, const char *const *src, int row_bytes, int n,
-                              hipStream_t stream) {
-    if (n <= 0) return hipSuccess;
-    const int chunks = row_bytes / 16;
-    gather_rows_kernel<<<copy_grid((long long)n * chunks), 256, 0, stream>>>((char *)dst, src,
-                                                                              chunks, n);
-    return hipGetLastError();
-}
-
-hipError_t launch_scatter_rows(char *const *dst, const void *src, int row_bytes, int n,
-                               hipStream_t stream) {
-    if (n <= 0) return hipSuccess;
-    const int chunks = row_bytes / 16;
-    scatter_rows_kernel<<<copy_grid((long long)n * chunks), 256, 0, stream>>>(
-        dst, (const char *)src, chunks, n);
+hipError_t launch_stage_copy(void *dst, const void *host_src, size_t bytes, hipStream_t stream) {
+    if (bytes == 0) return hipSuccess;
+    if ((bytes | (uintptr_t)dst | (uintptr_t)host_src) & 15) return hipErrorInvalidValue;
+    const long long n16 = (long long)(bytes / 16);
+    long long blocks = (n16 + 255) / 256;
+    if (blocks > 1024) blocks = 1024;
+    stage_copy_kernel<<<(unsigned)blocks, 256, 0, stream>>>((const u32x4 *)host_src, (u32x4 *)dst,
+                                                             n16);
     return hipGetLastError();
 }
 
