@@ -444,9 +444,9 @@ __device__ __forceinline__ int segment_units(const DecodeParams &p, int Ts) {
 // stores it for the merge kernel.
 template <int TT, int WPG>
 __device__ __forceinline__ void batch_prefix(const DecodeParams &p, int *pre) {
-    __shared__ int part[64 * WPG];
+    __shared__ int part[WPG];
     const int nthr = 64 * WPG;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int B = p.num_seqs;
     const int per = (B + nthr - 1) / nthr;
     const int s0 = tid * per;
@@ -460,16 +460,21 @@ __device__ __forceinline__ void batch_prefix(const DecodeParams &p, int *pre) {
             local += t;
         }
     }
-    part[tid] = local;
-    __syncthreads();
-    // Hillis-Steele inclusive scan of the per-thread sums.
-    for (int off = 1; off < nthr; off <<= 1) {
-        const int v = tid >= off ? part[tid - off] : 0;
-        __syncthreads();
-        part[tid] += v;
-        __syncthreads();
+    // Inclusive scan of the per-thread sums: within each wavefront with
+    // shuffles, then the wavefronts' totals through LDS (one barrier; a
+    // 256-thread Hillis-Steele scan took 16 and made the prologue longer).
+    int incl = local;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_up(incl, off);
+        if (lane >= off) incl += v;
     }
-    int run = part[tid] - local;  // exclusive prefix of this thread's first sequence
+    if (lane == 63) part[wave] = incl;
+    __syncthreads();
+    int base = 0;
+#pragma unroll
+    for (int k = 0; k < WPG - 1; k++) base += k < wave ? part[k] : 0;
+    int run = base + incl - local;  // exclusive prefix of this thread's first sequence
     for (int i = 0; i < per; i++) {
         const int s = s0 + i;
         if (s < B) {
@@ -478,7 +483,7 @@ __device__ __forceinline__ void batch_prefix(const DecodeParams &p, int *pre) {
             run += t;
         }
     }
-    if (tid == nthr - 1) pre[B] = part[nthr - 1];
+    if (tid == nthr - 1) pre[B] = base + incl;
     __syncthreads();
     if (blockIdx.x == 0) {
         for (int s = tid; s <= B; s += nthr) p.ws_prefix[s] = pre[s];
