@@ -669,6 +669,8 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
             q->wg_fix = 1;
             q->skip_empty = 1;  // merged from the other batch, or zeros, by the merge
         }
+        pp.pair_tiles = 1;  // the two 32-row head tiles share each range
+        pp.wg_fix = 0;
         pp.out_f32 = (float *)(w + o_po);
         pp.out_lse = (float *)(w + o_pl);
         pp.cached_seqs = (int)v_max;  // a group's rows read its pages close in time

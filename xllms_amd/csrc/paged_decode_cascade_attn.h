@@ -4,18 +4,22 @@
 // state with its prefix state.
 //
 // Partition.  The workgroups of one launch are split between the prefix
-// batch (32-row head tiles, R = 2: every shared page is read for 32 (member,
-// head) rows at once) and the suffix batch (the members' own pages, head
-// tiles of the caller's group), each running the ordinary MFMA partition
-// body over its own stream-K plan.  Every workgroup scans the split units of
+// batch (two 32-row head tiles per (sequence, kv head), R = 2, paired: the
+// two wavefronts of a pair walk the same stream-K range, one head tile each,
+// so a shared page is loaded for its 64 (member, head) rows by one CU at one
+// time) and the suffix batch (the members' own pages, head tiles of the
+// caller's group), each running the ordinary MFMA partition body over its
+// own stream-K plan.  Every workgroup scans the split units of
 // both batches (LDS) and takes the same split: the prefix batch gets a share
-// of the workgroups proportional to its units (kCascadeUnitCost: an R = 2
-// tile costs a wavefront about what an R = 1 tile does, both waiting mostly
-// on their loads; measured on MI355X at config 5, weights 0.8 / 1.0 / 1.25 /
-// 1.5 / 2.0 gave 131.3 / 128.3 / 131.2 / 133.5 / 140.2 us steps).  Run as two
-// launches, the prefix batch (a few thousand short ranges) spent ~30 us
-// mostly in latency while the device's bandwidth went unused; here its
-// ranges stream beside the suffix batch's.  Both bodies run in
+// of the workgroups proportional to its wavefront-units (a prefix unit
+// occupies a pair of wavefronts) weighted by kCascadeUnitCost.  Measured on
+// MI355X at config 5 (cascade step): weights 0.6 / 0.8 / 1.0 / 1.25 gave
+// 123.8 / 112.1-112.4 / 116.4-116.5 / 120.0 us on one box, 0.7 / 0.8 / 0.9 /
+// 1.0 gave 120.2-120.6 / 122.8-123.0 / 124.9-125.0 / 126.0-126.1 us on
+// another: the best weight differs between boxes, 0.75 is near it on both.
+// Run as two launches, the prefix batch (a few thousand short ranges) spent
+// ~30 us mostly in latency while the device's bandwidth went unused; here
+// its ranges stream beside the suffix batch's.  Both bodies run in
 // partial-output mode: finished segments leave fp32 rows and their
 // log-sum-exp, cut segments their partials, and the suffix batch no longer
 // starts from the prefix result (that would make it wait for the prefix
@@ -41,7 +45,7 @@ namespace xhip {
 // Weight of a prefix-batch split unit against a suffix-batch unit in the
 // workgroup split, in percent.
 #ifndef XHIP_CASCADE_UNIT_COST
-#define XHIP_CASCADE_UNIT_COST 100
+#define XHIP_CASCADE_UNIT_COST 75
 #endif
 constexpr int kCascadeUnitCost = XHIP_CASCADE_UNIT_COST;
 
@@ -52,14 +56,17 @@ constexpr int kCascadeUnitCost = XHIP_CASCADE_UNIT_COST;
 __device__ __forceinline__ int cascade_prefix_groups(int tp, int ts, int G) {
     if (tp <= 0) return 0;
     if (ts <= 0) return G;
-    const long long a = (long long)tp * kCascadeUnitCost, b = (long long)ts * 100;
+    // a prefix unit occupies both wavefronts of a pair
+    const long long a = 2LL * tp * kCascadeUnitCost, b = (long long)ts * 100;
     const int gp = (int)((a * G + (a + b) / 2) / (a + b));
     return gp < 1 ? 1 : (gp > G - 1 ? G - 1 : gp);
 }
 
-template <int D, int R1, int R2> union MfmaLdsPair {
-    MfmaLds<D, R1> a;
-    MfmaLds<D, R2> b;
+// LDS of the two bodies (one runs per workgroup): the prefix body's (paired
+// 32-row tiles, no workgroup combine) and the suffix body's.
+template <int D, int RS> union MfmaLdsPair {
+    MfmaLds<D, 2, 0> a;
+    MfmaLds<D, RS> b;
 };
 
 // Partition launch over both batches.  pp / ps are the prefix and suffix
@@ -74,19 +81,19 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, 2) void paged_decode_casca
     const int *__restrict__ stables) {
     constexpr int NW = kMfmaWavesPerGroup;
     extern __shared__ int pre[];  // prefix batch (pp.num_seqs + 1), then suffix batch
-    __shared__ MfmaLdsPair<D, 2, RS> sm;
+    __shared__ MfmaLdsPair<D, RS> sm;
     int *pre_p = pre, *pre_s = pre + pp.num_seqs + 1;
     batch_prefix<16, NW>(pp, pre_p);
     batch_prefix<16, NW>(ps, pre_s);
     const int G = gridDim.x;
     const int gp = cascade_prefix_groups(pre_p[pp.num_seqs], pre_s[ps.num_seqs], G);
     if (blockIdx.x == 0 && threadIdx.x == 0) pp.ws_prefix[pp.num_seqs + 1] = gp;
-    // neighbouring logical workgroups share an XCD (and its L2): the two
-    // head tiles of a prefix segment read the same pages in neighbouring
-    // ranges
+    // neighbouring logical workgroups share an XCD (and its L2).  (Giving
+    // every XCD its share of prefix workgroups instead measured 0.5-1 us
+    // slower.)
     const int l = xcd_local_block(blockIdx.x, G);
     if (l < gp)
-        mfma_partition_body<KV, D, 2>(pp, plens, ptables, pre_p, l, gp * NW, sm.a);
+        mfma_partition_body<KV, D, 2, true>(pp, plens, ptables, pre_p, l, gp * NW, sm.a);
     else
         mfma_partition_body<KV, D, RS>(ps, slens, stables, pre_s, l - gp, (G - gp) * NW, sm.b);
 }
@@ -105,16 +112,26 @@ __device__ __forceinline__ void absorb_row(float lse, const f32x4 &row, float &m
 // The state of one float4 column of a segment of batch p: its partials when
 // the partition left the segment cut, else its finished row.  seg is the
 // segment's index within its sequence, hrow the column's head in the
-// segment's tile (GT heads), c the float4 column in the head.
+// segment's tile (GT heads), c the float4 column in the head; pair_ht >= 0:
+// p's head tiles are paired (DecodeParams::pair_tiles) and the column is in
+// head tile pair_ht.
 template <int GT, int D>
 __device__ __forceinline__ void segment_state(const DecodeParams &p, int s, int L, int seg,
                                               int pre_s, int total, int waves, size_t row, int hrow,
-                                              int c, float &m, float &l, f32x4 &acc) {
+                                              int c, float &m, float &l, f32x4 &acc,
+                                              int pair_ht = -1) {
     const int Ts = (L + 15) / 16;
     const int seg_start = pre_s + seg * segment_units(p, Ts);
-    const int tpw = tiles_per_wave(total, waves, p.min_tiles_per_wave);
     PartialSlots ps;
-    if (segment_partials<kMfmaWavesPerGroup>(p, seg_start, seg_start + p.seg_cost, Ts, tpw, ps)) {
+    const bool cut =
+        pair_ht >= 0
+            ? segment_partials_paired(seg_start, seg_start + p.seg_cost, Ts,
+                                      tiles_per_wave(total, waves >> 1, p.min_tiles_per_wave),
+                                      pair_ht, ps)
+            : segment_partials<kMfmaWavesPerGroup>(
+                  p, seg_start, seg_start + p.seg_cost, Ts,
+                  tiles_per_wave(total, waves, p.min_tiles_per_wave), ps);
+    if (cut) {
         merge_partials<GT, D, 8>(p, ps, 0, 1, hrow * 2, hrow * D + c * 4, m, l, acc);
     } else {
         const float lse = p.out_lse[row];
@@ -166,8 +183,8 @@ __global__ __launch_bounds__(NT) void paged_decode_cascade_merge_kernel(
             if (Lv > 0) {
                 const int htp = j / GTP;
                 const size_t prow = (size_t)v * pp.num_heads + (size_t)kvh * rows + j;
-                segment_state<GTP, D>(pp, v, Lv, kvh * pp.head_tiles + htp, pp.ws_prefix[v],
-                                      tot_p, gp * NW, prow, j - htp * GTP, c, m, l, acc);
+                segment_state<GTP, D>(pp, v, Lv, kvh, pp.ws_prefix[v], tot_p, gp * NW, prow,
+                                      j - htp * GTP, c, m, l, acc, htp);
             }
         }
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;

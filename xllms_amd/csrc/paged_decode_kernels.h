@@ -433,6 +433,12 @@ __device__ __forceinline__ int logical_block(const DecodeParams &p, int total) {
                : (int)blockIdx.x;
 }
 
+// Stream-K segments of one sequence: one per (kv head, head tile), or per kv
+// head when the head tiles are paired (DecodeParams::pair_tiles).
+__device__ __forceinline__ int seq_segments(const DecodeParams &p) {
+    return p.num_kv_heads * (p.pair_tiles ? 1 : p.head_tiles);
+}
+
 // Split units of a segment of Ts tiles (paged_decode_params.h): its tiles
 // plus the start-up cost; an empty segment costs nothing.
 __device__ __forceinline__ int segment_units(const DecodeParams &p, int Ts) {
@@ -450,7 +456,7 @@ __device__ __forceinline__ void batch_prefix(const DecodeParams &p, int *pre) {
     const int B = p.num_seqs;
     const int per = (B + nthr - 1) / nthr;
     const int s0 = tid * per;
-    const int segs = p.num_kv_heads * p.head_tiles;
+    const int segs = seq_segments(p);
     int local = 0;
     for (int i = 0; i < per; i++) {
         const int s = s0 + i;
@@ -700,6 +706,22 @@ __device__ __forceinline__ bool segment_partials(const DecodeParams &p, int seg_
         ps.sb = (size_t)w_first * 2;
         ps.sstride = 2;
     }
+    return true;
+}
+
+// segment_partials for a batch with paired head tiles (pair_tiles, no
+// wg_fix): the partials of head tile ht of the segment, under a plan of tpw
+// units per range (a range is two wavefronts).
+__device__ __forceinline__ bool segment_partials_paired(int seg_start, int first_tile, int Ts,
+                                                        int tpw, int ht, PartialSlots &ps) {
+    const int r_first = first_tile / tpw;
+    const int r_last = (first_tile + Ts - 1) / tpw;
+    if (r_first == r_last) return false;
+    const int slot0 = (r_first * tpw >= seg_start) ? 0 : 1;
+    ps.np = r_last - r_first + 1;
+    ps.sb = (size_t)(2 * r_first + ht) * 2;
+    ps.s0 = ps.sb + slot0;
+    ps.sstride = 4;
     return true;
 }
 

@@ -229,9 +229,10 @@ struct MfmaPiece {
 };
 
 // Cursor over the pieces of one wavefront's range [g, g_end) of the batch's
-// split units; s is the sequence holding unit g.
+// split units; s is the sequence holding unit g, w the wavefront (its
+// partial slots), ht its head tile under paired head tiles (else -1).
 struct RangeCursor {
-    int g, g_end, s, first, w;
+    int g, g_end, s, first, w, ht;
 };
 
 // The next piece of the range (false at its end).  Same decomposition as
@@ -240,7 +241,7 @@ struct RangeCursor {
 template <int TT>
 __device__ __forceinline__ bool next_piece(const DecodeParams &p, const int *__restrict__ lens,
                                            const int *pre, RangeCursor &c, MfmaPiece &pc) {
-    const int segs = p.num_kv_heads * p.head_tiles;
+    const int segs = seq_segments(p);
     while (c.g < c.g_end) {
         const int L = min(max(lens[c.s], 0), p.max_ctx);
         const int Ts = (L + TT - 1) / TT;
@@ -260,8 +261,13 @@ __device__ __forceinline__ bool next_piece(const DecodeParams &p, const int *__r
         }
         if (t1 <= t0) continue;  // only start-up units of this segment (the range's end)
         pc.s = cur_s;
-        pc.kvh = seg / p.head_tiles;
-        pc.ht = seg - pc.kvh * p.head_tiles;
+        if (c.ht >= 0) {  // paired head tiles: a segment per kv head
+            pc.kvh = seg;
+            pc.ht = c.ht;
+        } else {
+            pc.kvh = seg / p.head_tiles;
+            pc.ht = seg - pc.kvh * p.head_tiles;
+        }
         pc.t_begin = t0 * TT;
         pc.t_end = min(L, t1 * TT);
         pc.L = L;
@@ -464,9 +470,9 @@ template <int D, int R> struct MfmaSweepLds<1, D, R> {
 template <int D, int R> struct MfmaSweepLds<2, D, R> {
     MfmaRelaySlot<D, R> relay;
 };
-template <int D, int R> struct MfmaLds {
+template <int D, int R, int FIX = mfma_wg_fixup(kMfmaHeads * R, D)> struct MfmaLds {
     __attribute__((aligned(16))) char vtile[kMfmaWavesPerGroup][MfmaGeometry<D>::kLdsTile];
-    MfmaSweepLds<mfma_wg_fixup(kMfmaHeads * R, D), D, R> sw;
+    MfmaSweepLds<FIX, D, R> sw;
 };
 
 // st <- st (+) the fp32 partial in workspace slot `slot` (its l is the
@@ -532,15 +538,17 @@ __device__ __forceinline__ void absorb_partial(const DecodeParams &p, int slot, 
 //
 // The body runs one workgroup's four ranges: logical workgroup `wg` of a
 // plan of `waves` wavefronts over the batch of p, whose split-unit prefix
-// `pre` is in LDS.
-template <int KV, int D, int R>
-__device__ __forceinline__ void mfma_partition_body(const DecodeParams &p,
-                                                    const int *__restrict__ lens,
-                                                    const int *__restrict__ tables,
-                                                    const int *pre, int wg, int waves,
-                                                    MfmaLds<D, R> &sm) {
+// `pre` is in LDS.  PAIR: the batch's head tiles are paired
+// (DecodeParams::pair_tiles): the workgroup's two pairs of wavefronts walk
+// two ranges, one head tile per wavefront, and every cut piece leaves its
+// own partial (no workgroup combine).
+template <int KV, int D, int R, bool PAIR = false>
+__device__ __forceinline__ void mfma_partition_body(
+    const DecodeParams &p, const int *__restrict__ lens, const int *__restrict__ tables,
+    const int *pre, int wg, int waves,
+    MfmaLds<D, R, PAIR ? 0 : mfma_wg_fixup(kMfmaHeads * R, D)> &sm) {
     using G = MfmaGeometry<D>;
-    constexpr int FIX = mfma_wg_fixup(kMfmaHeads * R, D);
+    constexpr int FIX = PAIR ? 0 : mfma_wg_fixup(kMfmaHeads * R, D);
     constexpr int NW = kMfmaWavesPerGroup;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -553,8 +561,9 @@ __device__ __forceinline__ void mfma_partition_body(const DecodeParams &p,
     const int B = p.num_seqs;
     const int total = pre[B];
     const int w = wg * NW + wave;
-    const int tpw = tiles_per_wave(total, waves, p.min_tiles_per_wave);
-    const long long g_lo = (long long)w * tpw;
+    const int wr = PAIR ? w >> 1 : w;  // this wavefront's range
+    const int tpw = tiles_per_wave(total, PAIR ? waves >> 1 : waves, p.min_tiles_per_wave);
+    const long long g_lo = (long long)wr * tpw;
 
     MfmaState<D> st[R];   // the state of the piece being computed; after the loop, the last one's
     MfmaPiece pc;         // the piece being computed; after the loop, the last one
@@ -564,6 +573,7 @@ __device__ __forceinline__ void mfma_partition_body(const DecodeParams &p,
     cur.g_end = g_lo < total ? min(total, cur.g + tpw) : cur.g;
     cur.first = 1;
     cur.w = w;
+    cur.ht = PAIR ? (w & 1) : -1;
     {
         // the sequence holding unit g: the last s with pre[s] <= g (empty
         // sequences share their successor's prefix, so this lands on one

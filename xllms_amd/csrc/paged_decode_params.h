@@ -83,6 +83,14 @@ struct DecodeParams {
     int seg_cost;              // split units a segment costs on top of its tiles
     float scale_log2;          // scale * log2(e)
     int merge_per_segment;     // 1: merge with one workgroup per segment
+    int pair_tiles;            // 1 (MFMA path, head_tiles == 2, wg_fix == 0): paired head
+                               // tiles.  A segment is (sequence, kv head); the two
+                               // wavefronts 2k, 2k + 1 of the launch walk the same stream-K
+                               // range (range k of num_waves / 2), wavefront 2k + t
+                               // computing head tile t, so both read each page at the same
+                               // time on one CU.  Partial j of a cut segment whose first
+                               // range is k0, head tile t: slot 2 (2 (k0 + j) + t) + (j == 0 ?
+                               // the first range's slot : 0)
     int wg_fix;                // 1: the partition kernel combined each segment's pieces
                                // inside a workgroup (mfma_wg_fixup): partial j >= 1 of a
                                // segment is in slot 2 * kMfmaWavesPerGroup * (its
