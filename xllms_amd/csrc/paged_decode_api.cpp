@@ -187,9 +187,11 @@ bool head_tiling(int group, bool mfma, int head_size, HeadTiling *t) {
     return t->head_tiles <= xhip::kWavesPerGroup;
 }
 
-// Smallest stream-K range, in tiles, the automatic plan gives a wavefront:
-// below this the per-range setup (prefix lookup, Q load, merge) dominates.
-constexpr int kMinTilesPerWave = 4;
+// Smallest stream-K range, in split units, the automatic plan gives a
+// wavefront: it binds only batches too small to fill the launch, whose time
+// is the chain of dependent loads in each range.  Config 1 (8 sequences)
+// measured 14.3-14.6 / 14.8 / 14.9 / 16.0-16.1 us per step at 2 / 3 / 4 / 6.
+constexpr int kMinTilesPerWave = 2;
 
 
 int partition_occupancy(int kv_dtype, int head_size, int head_tile, bool mfma, size_t lds) {
