@@ -88,12 +88,17 @@ def test_cascade_config5_matches_oracle(cuda):
                                           ("fp16", 64, 8, 8), ("bf16", 256, 16, 1),
                                           ("fp16", 80, 16, 4), ("fp32", 64, 12, 12),
                                           ("fp32", 128, 32, 8), ("fp16", 96, 64, 2),
-                                          ("bf16", 32, 48, 1)])
+                                          ("bf16", 32, 48, 1), ("fp16", 128, 64, 1),
+                                          ("bf16", 64, 48, 2), ("bf16", 128, 64, 4),
+                                          ("fp16", 32, 16, 4)])
 def test_cascade_groups_match_oracle(cuda, dtype, D, H, KVH):
     """Groups of 1..21 members (prefix rows spanning several 16- or 32-row
     prefix sequences), members with an empty suffix, unshared sequences
     (L = 1, L = 0, long), on the MFMA (one and two 16-head row blocks per
-    wavefront) and VALU tile paths."""
+    wavefront) and VALU tile paths.  On the MFMA path with head_size <= 128
+    the two batches run in one launch with paired prefix head tiles: group 64
+    fills a 64-row prefix sequence with one member, group 24 splits some
+    members' rows between two prefix sequences."""
     spec = [(5, [3, 0, 40, 16, 1]), (1, [7] * 21), (12, [100]), (2, [0, 0])]
     wl, pg, pb = shared_case(spec, singles=[1, 0, 333], H=H, KVH=KVH, D=D, kv_dtype=DT[dtype],
                              seed=D + H)
