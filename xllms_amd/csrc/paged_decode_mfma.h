@@ -198,8 +198,13 @@ __device__ __forceinline__ void mfma_tile(const DecodeParams &p, const u32x4 (*q
         p_hi[b] = u32x2{h01, h23};
         p_lo[b] = u32x2{pack16<KV>(pe[0] - r01.x, pe[1] - r01.y),
                         pack16<KV>(pe[2] - r23.x, pe[3] - r23.y)};
+        // Rescale only when some head's running max moved: alpha is then
+        // exactly 1 in every lane, and x * 1 == x, so skipping is exact (past
+        // the first few hundred tokens most tiles skip).
+        if (__any(alpha != 1.0f)) {
 #pragma unroll
-        for (int n = 0; n < G::kDimBlocks; n++) st[b].o[n] *= alpha;
+            for (int n = 0; n < G::kDimBlocks; n++) st[b].o[n] *= alpha;
+        }
     }
 
     // O^T += V^T P for every 16-dim block.
