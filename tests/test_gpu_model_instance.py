@@ -19,6 +19,14 @@ from xllms_amd import workloads as W
 pytestmark = pytest.mark.gpu
 
 
+def as_model(bits, dtype):
+    """fp16 element bits -> a device tensor of the model's element type (fp32:
+    the same values, exactly)."""
+    if dtype == W.FP32:
+        return W.to_torch(np.ascontiguousarray(bits).view(np.float16).astype(np.float32), W.FP32)
+    return W.to_torch(bits, dtype)
+
+
 class Client:
     """Holds each request's token history; K/V and queries come from the
     same prefix-keyed rows as tests/test_gpu_kv_index_decode.py."""
@@ -36,13 +44,13 @@ class Client:
             if len(new_tokens) else None
         keep = {}
         if kv is not None:
-            keep["k"] = W.to_torch(np.ascontiguousarray(kv[:, 0]), self.dtype)
-            keep["v"] = W.to_torch(np.ascontiguousarray(kv[:, 1]), self.dtype)
+            keep["k"] = as_model(np.ascontiguousarray(kv[:, 0]), self.dtype)
+            keep["v"] = as_model(np.ascontiguousarray(kv[:, 1]), self.dtype)
         if attend:
             keep["q_bits"] = rng.standard_normal((self.ref.H, self.ref.D)).astype(np.float16) \
                 .view(np.uint16)
-            keep["q"] = W.to_torch(keep["q_bits"], self.dtype)
-            keep["o"] = torch.empty((self.ref.H, self.ref.D), dtype=torch.float16,
+            keep["q"] = as_model(keep["q_bits"], self.dtype)
+            keep["o"] = torch.empty((self.ref.H, self.ref.D), dtype=W.torch_dtype(self.dtype),
                                     device="cuda")
         rc = self.m.bind(rid, tokens=new_tokens if len(new_tokens) else None,
                          key=keep.get("k"), value=keep.get("v"), query=keep.get("q"),
@@ -63,7 +71,11 @@ class Client:
         self.ref.live.clear()
 
 
-def test_scheduler_style_and_batched_exec(cuda):
+@pytest.mark.parametrize("dtype", [W.FP16, W.FP32], ids=["fp16", "fp32"])
+def test_scheduler_style_and_batched_exec(cuda, dtype):
+    """fp16 runs the MFMA tile path and the one-launch cascade; fp32 the VALU
+    tile path and the two-pass cascade.  Both read each request's query and
+    write its output through the exec's row pointers."""
     import torch
     rng = np.random.default_rng(99)
     H, KVH, D, bs = 32, 8, 128, 16
@@ -71,10 +83,11 @@ def test_scheduler_style_and_batched_exec(cuda):
     ref.KVH, ref.H, ref.D, ref.bs = KVH, H, D, bs
     ref.scale = 1.0 / np.sqrt(D)
     ref.live, ref._rows = {}, {}
+    code = B.NXT_TYPE_FP32 if dtype == W.FP32 else B.NXT_TYPE_FP16
     m = B.DecodeModel(num_blocks=512, num_kv_heads=KVH, block_size=bs, head_size=D,
-                      num_heads=H, max_batch_size=16, max_blocks_per_seq=64)
+                      num_heads=H, dtype=code, max_batch_size=16, max_blocks_per_seq=64)
     assert m.status == 0 and m.model.instance_count == 1 and m.model.instances
-    c = Client(m, ref, W.FP16)
+    c = Client(m, ref, dtype)
     system = list(rng.integers(0, 60, 45))
     rids = [f"req{i}" for i in range(6)]
     # prompts one request per exec, as the scheduler's poll issues them
