@@ -64,6 +64,8 @@ __device__ __forceinline__ int cascade_prefix_groups(int tp, int ts, int G) {
 
 // LDS of the two bodies (one runs per workgroup): the prefix body's (paired
 // 32-row tiles, no workgroup combine) and the suffix body's.
+constexpr int kCascadeMergeLdsSeqs = 1024;
+
 template <int D, int RS> union MfmaLdsPair {
     MfmaLds<D, 2, 0> a;
     MfmaLds<D, RS> b;
@@ -152,6 +154,17 @@ __global__ __launch_bounds__(NT) void paged_decode_cascade_merge_kernel(
     constexpr int C4 = D / 4;
     constexpr int NW = kMfmaWavesPerGroup;
     constexpr int GTP = 2 * kMfmaHeads;
+    // The prefix batch's lengths and unit prefixes, loaded with the first
+    // round trip (a prefix batch of up to kCascadeMergeLdsSeqs sequences), so
+    // finding a column's prefix segment takes no round trip of its own.
+    __shared__ int l_vlen[kCascadeMergeLdsSeqs], l_vpre[kCascadeMergeLdsSeqs];
+    const bool v_lds = pp.num_seqs <= kCascadeMergeLdsSeqs;
+    if (v_lds) {
+        for (int v = threadIdx.x; v < pp.num_seqs; v += NT) {
+            l_vlen[v] = seq_len_of(pp, v);
+            l_vpre[v] = pp.ws_prefix[v];
+        }
+    }
     const int segs = ps.num_kv_heads * ps.head_tiles;
     const int s = blockIdx.x / segs;
     const int seg = blockIdx.x - s * segs;
@@ -167,6 +180,7 @@ __global__ __launch_bounds__(NT) void paged_decode_cascade_merge_kernel(
     const int tot_p = pp.ws_prefix[pp.num_seqs];
     const int gp = pp.ws_prefix[pp.num_seqs + 1];
     asm volatile("" ::"s"(Ls), "s"(fb), "s"(tot_s), "s"(pre_s), "s"(tot_p), "s"(gp));
+    __syncthreads();
     const int G = ps.num_waves / NW;
     const size_t srow0 = (size_t)s * ps.num_heads + (size_t)kvh * ps.group + g0;
     for (int col = threadIdx.x; col < ncols; col += NT) {
@@ -179,12 +193,12 @@ __global__ __launch_bounds__(NT) void paged_decode_cascade_merge_kernel(
         if (fb >= 0) {
             const int q = fb + g0 + h;
             const int v = q / rows, j = q - v * rows;
-            const int Lv = seq_len_of(pp, v);
+            const int Lv = v_lds ? l_vlen[v] : seq_len_of(pp, v);
             if (Lv > 0) {
                 const int htp = j / GTP;
                 const size_t prow = (size_t)v * pp.num_heads + (size_t)kvh * rows + j;
-                segment_state<GTP, D>(pp, v, Lv, kvh, pp.ws_prefix[v], tot_p, gp * NW, prow,
-                                      j - htp * GTP, c, m, l, acc, htp);
+                segment_state<GTP, D>(pp, v, Lv, kvh, v_lds ? l_vpre[v] : pp.ws_prefix[v], tot_p,
+                                      gp * NW, prow, j - htp * GTP, c, m, l, acc, htp);
             }
         }
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
