@@ -593,7 +593,8 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
                  o_vq = take((size_t)v_max * KR * head_size * eb),
                  o_sl = take(4 * (size_t)num_seqs), o_sb = take(4 * (size_t)num_seqs * mb),
                  o_po = take(4 * (size_t)v_max * KR * head_size), o_pl = take(4 * (size_t)v_max * KR),
-                 o_pr = take(4 * (size_t)num_seqs);
+                 o_pr = take(4 * (size_t)num_seqs), o_vd = take(4 * 8 * (size_t)v_max),
+                 o_spb = take(4 * (size_t)num_seqs);
     // one launch over both batches: each batch's split-K workspace (partials
     // for up to every wavefront, unit prefix), and the suffix batch's rows
     const size_t gts = (size_t)stile.head_tile;
@@ -645,6 +646,8 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
     c.s_lens = (int *)(w + o_sl);
     c.s_bt = (int *)(w + o_sb);
     c.p_row = (int *)(w + o_pr);
+    c.v_desc = (int *)(w + o_vd);
+    c.s_pblk = (int *)(w + o_spb);
     // plan -> prefix pass (R gathered query rows per kv head, cacheable K/V:
     // the rows of a group read the same pages) -> suffix pass, whose members
     // start from their prefix rows and which writes the output

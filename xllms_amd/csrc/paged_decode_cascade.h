@@ -52,6 +52,11 @@ struct CascadeParams {
     int *p_row;                // [num_seqs] fold base of each member: the row index, in
                                // the group's prefix-batch rows laid end to end, of its
                                // first query head (g_vbase * rows + rank * group); -1
+    // Descriptors the first plan kernel writes for the gather, so that each
+    // gather item waits on one load of them instead of a chain of lookups:
+    int *v_desc;               // [v_max][8] group (-1: unused), its g_vbase, g_count,
+                               // g_moff, g_first, prefix_blocks, 0, 0
+    int *s_pblk;               // [num_seqs] shared prefix pages of a member (0: none)
 };
 
 // Plan: group membership and the prefix / suffix batches.

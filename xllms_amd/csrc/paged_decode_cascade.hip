@@ -35,6 +35,8 @@ namespace {
 
 constexpr int kPlanThreads = 1024;
 
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ int clamp_len(int L, int max_ctx) {
     return L < 0 ? 0 : (L > max_ctx ? max_ctx : L);
 }
@@ -79,6 +81,23 @@ __device__ int block_exclusive_scan(int *a, int n, int *part) {
     return total;
 }
 
+// The gather's descriptors (CascadeParams::v_desc, s_pblk) and the suffix
+// batch's per-member lengths and fold bases, written by part 1.
+__device__ __forceinline__ void write_v_desc(const CascadeParams &c, int v, int g, int vbase,
+                                             int count, int moff, int first) {
+    i32x4_t *d = (i32x4_t *)(c.v_desc + (size_t)v * 8);
+    d[0] = i32x4_t{g, vbase, count, moff};
+    d[1] = i32x4_t{first, g >= 0 ? c.prefix_blocks[g] : 0, 0, 0};
+}
+
+// Member s with P shared pages (0: none; then vbase and rank are unused).
+__device__ __forceinline__ void write_s_desc(const CascadeParams &c, int s, int P, int vbase,
+                                             int rank) {
+    c.s_pblk[s] = P;
+    c.s_lens[s] = P > 0 ? clamp_len(c.seq_lens[s], c.max_ctx) - P * c.block_size : c.seq_lens[s];
+    c.p_row[s] = P > 0 ? vbase * c.rows + rank * c.group : -1;
+}
+
 // Plan, part 1 (one workgroup): members, ranks, and where every group's rows
 // go in the prefix batch.
 __global__ __launch_bounds__(kPlanThreads) void cascade_plan_meta_kernel(const CascadeParams c) {
@@ -115,9 +134,21 @@ __global__ __launch_bounds__(kPlanThreads) void cascade_plan_meta_kernel(const C
     }
     for (int g = tid; g < NG; g += kPlanThreads) {
         const int n = (c.g_count[g] * c.group + c.rows - 1) / c.rows;
-        for (int k = 0; k < n; k++) c.v_group[c.g_vbase[g] + k] = g;
+        for (int k = 0; k < n; k++) {
+            c.v_group[c.g_vbase[g] + k] = g;
+            write_v_desc(c, c.g_vbase[g] + k, g, c.g_vbase[g], c.g_count[g], c.g_moff[g],
+                         c.g_first[g]);
+        }
     }
-    for (int v = vt + tid; v < c.v_max; v += kPlanThreads) c.v_group[v] = -1;
+    for (int v = vt + tid; v < c.v_max; v += kPlanThreads) {
+        c.v_group[v] = -1;
+        write_v_desc(c, v, -1, 0, 0, 0, 0);
+    }
+    for (int s = tid; s < B; s += kPlanThreads) {
+        int g;
+        const int P = c.rank[s] >= 0 ? member_prefix(c, s, &g) : 0;
+        write_s_desc(c, s, P, P > 0 ? c.g_vbase[g] : 0, c.rank[s]);
+    }
 }
 
 // Plan, part 1 with the work arrays in LDS (batches of up to kPlanLdsSeqs
@@ -190,13 +221,21 @@ __global__ __launch_bounds__(kPlanThreads) void cascade_plan_meta_lds_kernel(con
         c.g_vbase[g] = l_vbase[g];
         c.g_moff[g] = l_moff[g];
         const int n = (l_count[g] * c.group + c.rows - 1) / c.rows;
-        for (int k = 0; k < n; k++) c.v_group[l_vbase[g] + k] = g;
+        for (int k = 0; k < n; k++) {
+            c.v_group[l_vbase[g] + k] = g;
+            write_v_desc(c, l_vbase[g] + k, g, l_vbase[g], l_count[g], l_moff[g], l_first[g]);
+        }
     }
     for (int s = tid; s < B; s += kPlanThreads) {
         const int r = l_rank[s];
-        if (r >= 0) c.member_seq[l_moff[l_group[s]] + r] = s;
+        const int g = l_group[s];
+        if (r >= 0) c.member_seq[l_moff[g] + r] = s;
+        write_s_desc(c, s, g >= 0 ? c.prefix_blocks[g] : 0, g >= 0 ? l_vbase[g] : 0, r);
     }
-    for (int v = vt + tid; v < c.v_max; v += kPlanThreads) c.v_group[v] = -1;
+    for (int v = vt + tid; v < c.v_max; v += kPlanThreads) {
+        c.v_group[v] = -1;
+        write_v_desc(c, v, -1, 0, 0, 0, 0);
+    }
 }
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -220,13 +259,14 @@ __global__ __launch_bounds__(256) void cascade_plan_gather_kernel(const CascadeP
             const long long row = i / CH;
             const int v = (int)(row / KR);
             const int hj = (int)(row - (long long)v * KR);
-            const int g = c.v_group[v];
-            if (g < 0) continue;  // unused: its length is 0, its rows are never read
+            // {group, its g_vbase, g_count, g_moff}
+            const i32x4_t d = *(const i32x4_t *)(c.v_desc + (size_t)v * 8);
+            if (d.x < 0) continue;  // unused: its length is 0, its rows are never read
             const int h = hj / R, j = hj - h * R;
-            const int rig = (v - c.g_vbase[g]) * R + j;
+            const int rig = (v - d.y) * R + j;
             const int r = rig / c.group, gq = rig - r * c.group;
-            if (r >= c.g_count[g]) continue;  // no member: never read
-            const int s = c.member_seq[c.g_moff[g] + r];
+            if (r >= d.z) continue;  // no member: never read
+            const int s = c.member_seq[d.w + r];
             const size_t hrow = (size_t)h * c.group + gq;
             const char *src = c.q_rows ? c.q_rows[s] + hrow * row_bytes
                                        : (const char *)c.q + ((size_t)s * c.num_heads + hrow) * row_bytes;
@@ -235,21 +275,16 @@ __global__ __launch_bounds__(256) void cascade_plan_gather_kernel(const CascadeP
         } else if (i < n1 + n2) {
             const long long k = i - n1;
             const int v = (int)(k / c.max_blocks), b = (int)(k - (long long)v * c.max_blocks);
-            const int g = c.v_group[v];
-            const int P = g >= 0 ? c.prefix_blocks[g] : 0;
+            // {g_first, prefix pages} (0 pages when the sequence is unused)
+            const i32x4_t d = *(const i32x4_t *)(c.v_desc + (size_t)v * 8 + 4);
+            const int P = d.y;
             if (b == 0) c.v_lens[v] = P * c.block_size;
-            if (b < P)
-                c.v_bt[k] = c.block_tables[(size_t)c.g_first[g] * c.max_blocks + b];
+            if (b < P) c.v_bt[k] = c.block_tables[(size_t)d.x * c.max_blocks + b];
         } else {
+            // (the suffix lengths and fold bases were written with s_pblk)
             const long long k = i - n1 - n2;
             const int s = (int)(k / c.max_blocks), b = (int)(k - (long long)s * c.max_blocks);
-            int g;
-            const int P = c.rank[s] >= 0 ? member_prefix(c, s, &g) : 0;
-            if (b == 0) {
-                c.s_lens[s] = P > 0 ? clamp_len(c.seq_lens[s], c.max_ctx) - P * c.block_size
-                                    : c.seq_lens[s];
-                c.p_row[s] = P > 0 ? c.g_vbase[g] * c.rows + c.rank[s] * c.group : -1;
-            }
+            const int P = c.s_pblk[s];
             c.s_bt[k] = b + P < c.max_blocks ? c.block_tables[(size_t)s * c.max_blocks + b + P]
                                               : -1;
         }
