@@ -152,3 +152,48 @@ def test_cascade_repeated_calls_reuse_the_plan_workspace(cuda):
         for i, ((wl, pg, pb), ref) in enumerate(zip(cases, refs)):
             print(f"case rep={rep} shape={i}", flush=True)
             assert_close(run_cascade(wl, pg, pb), ref, wl.kv_dtype, f"rep {rep} case {i}")
+
+
+@pytest.mark.parametrize("dtype,D,H,KVH", [("fp16", 128, 32, 8), ("bf16", 64, 48, 2),
+                                          ("fp16", 128, 64, 1), ("bf16", 128, 16, 8)])
+def test_cascade_inkernel_plan_matches_plan_kernels(cuda, dtype, D, H, KVH):
+    """Up to 256 groups the partition launch plans both batches itself (in
+    LDS, from the caller's arrays); with more groups the plan kernels build
+    them first.  The same batch both ways (the group table padded to 300
+    entries, the padding unused; a table holds at most one group per
+    sequence), with every group's rows in one 64-row prefix-batch sequence:
+    members then differ at most in their order within that sequence's rows,
+    which no row's result depends on, and the split is the same, so the
+    outputs are bit-identical.  Larger groups (several prefix-batch
+    sequences) match the oracle both ways, and the in-kernel plan, whose
+    member order is the sequence order, gives bit-identical repeats."""
+    import dataclasses
+    G = H // KVH
+    k = max(1, 64 // G)  # members per prefix-batch sequence
+    small = [(5, [3, 0, 40, 16, 1][:k]), (1, [7] * min(21, k)), (12, [100]), (2, [0, 0][:k]),
+             (3, [9] * min(40, k))]
+    large = [(5, [3, 0, 40, 16, 1]), (1, [7] * 21), (12, [100]), (2, [0, 0]), (3, [9] * 40)]
+    for name, spec in (("one prefix sequence per group", small), ("larger groups", large)):
+        members = sum(len(sfx) for _, sfx in spec)
+        singles = [1, 0, 333, 64] + [20 + 7 * (i % 40) for i in range(max(0, 300 - members - 4))]
+        wl, pg, pb = shared_case(spec, singles=singles, H=H, KVH=KVH, D=D, kv_dtype=DT[dtype],
+                                 seed=3 * D + H)
+        # members of the groups interleaved, as a scheduler's batch has them
+        perm = np.random.default_rng(D + H).permutation(wl.num_seqs)
+        wl = dataclasses.replace(wl, seq_lens=wl.seq_lens[perm],
+                                 block_tables=wl.block_tables[perm], query=wl.query[perm])
+        pg = pg[perm]
+        print(f"case {dtype} D={D} H={H} KVH={KVH} {name} seqs={wl.num_seqs}", flush=True)
+        ref = O.run_workload(wl, precision="mt")
+        dw = W.upload(wl)
+        got = run_cascade(wl, pg, pb, dw=dw).copy()
+        dw.out.zero_()
+        again = run_cascade(wl, pg, pb, dw=dw).copy()
+        assert np.array_equal(got, again)
+        padded = np.concatenate([pb, np.zeros(300 - len(pb), np.int32)]).astype(np.int32)
+        dw.out.zero_()
+        want = run_cascade(wl, pg, padded, max_groups=300, dw=dw)
+        if spec is small:
+            assert np.array_equal(got, want)
+        assert_close(got, ref, wl.kv_dtype, f"cascade {dtype} D={D}, in-kernel plan")
+        assert_close(want, ref, wl.kv_dtype, f"cascade {dtype} D={D}, plan kernels")

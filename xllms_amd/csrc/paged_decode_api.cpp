@@ -560,17 +560,25 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
     // run() one after the other, the suffix batch folding in the prefix rows.
     HeadTiling stile{};
     long long fw = 0;
+    bool inplan = false;  // the partition launch plans both batches itself
     if (wide && supported_head_size(head_size) &&
         head_tiling(group, true, head_size, &stile)) {
         const long long tiles = ((long long)max_num_blocks_per_seq * block_size + 15) / 16 + kSegmentCost;
         const bool fits = v_max * (long long)num_kv_heads * (rows / 32) * tiles < kMaxLaunchTiles &&
                           (long long)num_seqs * num_kv_heads * stile.head_tiles * tiles <
                               kMaxLaunchTiles;
-        const size_t lds = (size_t)(v_max + num_seqs + 2) * sizeof(int);
         const int rs = stile.head_tile / xhip::kMfmaHeads;
-        const int occ = !fits ? 0
-                        : kv_dtype == NXT_KV_FP16 ? xhip::cascade_attn_occupancy_f16(head_size, rs, lds)
-                                                  : xhip::cascade_attn_occupancy_bf16(head_size, rs, lds);
+        auto occupancy = [&](bool ip, size_t lds) {
+            return kv_dtype == NXT_KV_FP16 ? xhip::cascade_attn_occupancy_f16(head_size, rs, ip, lds)
+                                           : xhip::cascade_attn_occupancy_bf16(head_size, rs, ip, lds);
+        };
+        int occ = 0;
+        if (fits && max_groups <= xhip::kInPlanGroupsMax) {
+            // (only where it keeps two workgroups per CU)
+            occ = occupancy(true, xhip::inplan_lds_bytes(num_seqs, (int)v_max, max_groups));
+            inplan = occ >= 2;
+        }
+        if (fits && !inplan) occ = occupancy(false, (size_t)(v_max + num_seqs + 2) * sizeof(int));
         if (occ > 0) {
             int per_cu = occ * xhip::kMfmaWavesPerGroup;
             if (per_cu > kMfmaWavesPerCu) per_cu = kMfmaWavesPerCu;
@@ -585,16 +593,19 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
         off += align256(bytes);
         return o;
     };
-    const size_t o_gc = take(4 * (size_t)max_groups), o_gf = take(4 * (size_t)max_groups),
-                 o_gv = take(4 * (size_t)max_groups), o_gm = take(4 * (size_t)max_groups),
-                 o_ms = take(4 * (size_t)num_seqs), o_rk = take(4 * (size_t)num_seqs),
-                 o_vg = take(4 * (size_t)v_max), o_vl = take(4 * (size_t)v_max),
-                 o_vb = take(4 * (size_t)v_max * mb),
-                 o_vq = take((size_t)v_max * KR * head_size * eb),
-                 o_sl = take(4 * (size_t)num_seqs), o_sb = take(4 * (size_t)num_seqs * mb),
+    // (the in-kernel plan needs only the batches' lengths and p_row of the
+    // plan's arrays)
+    const size_t pn = inplan ? 0 : 1;
+    const size_t o_gc = take(4 * (size_t)max_groups * pn), o_gf = take(4 * (size_t)max_groups * pn),
+                 o_gv = take(4 * (size_t)max_groups * pn), o_gm = take(4 * (size_t)max_groups * pn),
+                 o_ms = take(4 * (size_t)num_seqs * pn), o_rk = take(4 * (size_t)num_seqs * pn),
+                 o_vg = take(4 * (size_t)v_max * pn), o_vl = take(4 * (size_t)v_max),
+                 o_vb = take(4 * (size_t)v_max * mb * pn),
+                 o_vq = take((size_t)v_max * KR * head_size * eb * pn),
+                 o_sl = take(4 * (size_t)num_seqs), o_sb = take(4 * (size_t)num_seqs * mb * pn),
                  o_po = take(4 * (size_t)v_max * KR * head_size), o_pl = take(4 * (size_t)v_max * KR),
-                 o_pr = take(4 * (size_t)num_seqs), o_vd = take(4 * 8 * (size_t)v_max),
-                 o_spb = take(4 * (size_t)num_seqs);
+                 o_pr = take(4 * (size_t)num_seqs), o_vd = take(4 * 8 * (size_t)v_max * pn),
+                 o_spb = take(4 * (size_t)num_seqs * pn);
     // one launch over both batches: each batch's split-K workspace (partials
     // for up to every wavefront, unit prefix), and the suffix batch's rows
     const size_t gts = (size_t)stile.head_tile;
@@ -650,20 +661,28 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
     c.s_pblk = (int *)(w + o_spb);
     // plan -> prefix pass (R gathered query rows per kv head, cacheable K/V:
     // the rows of a group read the same pages) -> suffix pass, whose members
-    // start from their prefix rows and which writes the output
-    e = xhip::launch_cascade_plan(c, stream);
-    if (e != hipSuccess)
-        return set_status(NXT_ATTN_E_HIP, "cascade plan launch: %s", hipGetErrorString(e));
+    // start from their prefix rows and which writes the output; or, with the
+    // in-kernel plan, one partition launch that plans both batches itself
+    if (!inplan) {
+        e = xhip::launch_cascade_plan(c, stream);
+        if (e != hipSuccess)
+            return set_status(NXT_ATTN_E_HIP, "cascade plan launch: %s", hipGetErrorString(e));
+    }
     if (fw) {
         DecodeParams pp, ps;
         memset(&pp, 0, sizeof(pp));
         memset(&ps, 0, sizeof(ps));
-        fill_batch(pp, c.v_q, key_cache, value_cache, c.v_bt, c.v_lens, (int)v_max, (int)KR,
-                   num_kv_heads, rows / 32, max_num_blocks_per_seq, block_size, kv_block_stride,
+        // (in-kernel plan: the batches' lengths are the workspace arrays the
+        // partition launch fills for the merge; tables and query rows are
+        // the caller's, read in place)
+        fill_batch(pp, inplan ? nullptr : c.v_q, key_cache, value_cache,
+                   inplan ? block_tables : c.v_bt, c.v_lens, (int)v_max, (int)KR, num_kv_heads,
+                   rows / 32, max_num_blocks_per_seq, block_size, kv_block_stride,
                    kv_head_stride, scale);
-        fill_batch(ps, rowp ? nullptr : query, key_cache, value_cache, c.s_bt, c.s_lens, num_seqs,
-                   num_heads, num_kv_heads, stile.head_tiles, max_num_blocks_per_seq, block_size,
-                   kv_block_stride, kv_head_stride, scale);
+        fill_batch(ps, rowp ? nullptr : query, key_cache, value_cache,
+                   inplan ? block_tables : c.s_bt, c.s_lens, num_seqs, num_heads, num_kv_heads,
+                   stile.head_tiles, max_num_blocks_per_seq, block_size, kv_block_stride,
+                   kv_head_stride, scale);
         ps.out = rowp ? nullptr : out;  // the merge's output rows
         ps.q_rows = rowp ? rowp->q : nullptr;
         ps.o_rows = rowp ? rowp->o : nullptr;
@@ -688,11 +707,14 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
         ps.ws_ml = (float *)(w + o_ym);
         ps.ws_prefix = (int *)(w + o_yp);
         const int rs = stile.head_tile / xhip::kMfmaHeads;
+        const xhip::CascadeInPlan ip{seq_lens, block_tables, prefix_group, prefix_blocks,
+                                     max_groups};
+        const xhip::CascadeInPlan *ipp = inplan ? &ip : nullptr;
         e = kv_dtype == NXT_KV_FP16
-                ? xhip::launch_cascade_attn_f16(pp, ps, c.p_row, rows, head_size, rs, stream,
+                ? xhip::launch_cascade_attn_f16(pp, ps, c.p_row, rows, head_size, rs, ipp, stream,
                                                 t_trace_start, t_trace_partition)
-                : xhip::launch_cascade_attn_bf16(pp, ps, c.p_row, rows, head_size, rs, stream,
-                                                 t_trace_start, t_trace_partition);
+                : xhip::launch_cascade_attn_bf16(pp, ps, c.p_row, rows, head_size, rs, ipp,
+                                                 stream, t_trace_start, t_trace_partition);
         if (e != hipSuccess)
             return set_status(NXT_ATTN_E_HIP, "cascade attention launch: %s", hipGetErrorString(e));
         return ok();

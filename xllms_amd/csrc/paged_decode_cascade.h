@@ -62,20 +62,42 @@ struct CascadeParams {
 // Plan: group membership and the prefix / suffix batches.
 hipError_t launch_cascade_plan(const CascadeParams &c, hipStream_t stream);
 
+// The caller's arrays for the cascade's in-kernel plan (at most
+// kInPlanGroupsMax groups, and LDS for two workgroups per CU): the partition
+// launch builds both batches from them in LDS, with no plan launches
+// (paged_decode_cascade_attn.h).
+// Wavefront 0 of every workgroup lays the groups out 64 at a time; beyond
+// 256 groups the plan kernels, which do it with 1024 threads once, are the
+// shorter path.
+constexpr int kInPlanGroupsMax = 256;
+struct CascadeInPlan {
+    const int *lens;           // [num_seqs] caller's sequence lengths
+    const int *tables;         // [num_seqs][max_blocks] caller's block tables
+    const int *prefix_group;   // [num_seqs]
+    const int *prefix_blocks;  // [num_groups]
+    int num_groups;            // max_groups, <= kInPlanGroupsMax
+};
+
 // Attention of the cascade on the MFMA tile path (paged_decode_cascade_attn.h):
 // the prefix batch pp (32-row head tiles) and the suffix batch ps (head
 // tiles of 16 * rs rows) in one partition launch of ps.num_waves
 // wavefronts (>= 8), then the merge that writes ps's output rows (ps.out or
-// ps.o_rows) from both.
+// ps.o_rows) from both.  ip null: the plan kernels built both batches
+// (launch_cascade_plan); else the partition launch plans them itself from
+// ip, and pp.seq_lens, ps.seq_lens and p_row are workspace it fills for the
+// merge.  lds_bytes: the launch's dynamic LDS (inplan_lds_bytes with ip).
 // head_size 32, 64, 96 or 128; hipErrorInvalidValue otherwise.
-int cascade_attn_occupancy_f16(int head_size, int rs, size_t lds_bytes);
-int cascade_attn_occupancy_bf16(int head_size, int rs, size_t lds_bytes);
+size_t inplan_lds_bytes(int num_seqs, int v_max, int num_groups);
+int cascade_attn_occupancy_f16(int head_size, int rs, bool inplan, size_t lds_bytes);
+int cascade_attn_occupancy_bf16(int head_size, int rs, bool inplan, size_t lds_bytes);
 hipError_t launch_cascade_attn_f16(const DecodeParams &pp, const DecodeParams &ps,
                                    const int *p_row, int rows, int head_size, int rs,
-                                   hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
+                                   const CascadeInPlan *ip, hipStream_t stream,
+                                   hipEvent_t ev_start, hipEvent_t ev_stop);
 hipError_t launch_cascade_attn_bf16(const DecodeParams &pp, const DecodeParams &ps,
                                     const int *p_row, int rows, int head_size, int rs,
-                                    hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop);
+                                    const CascadeInPlan *ip, hipStream_t stream,
+                                    hipEvent_t ev_start, hipEvent_t ev_stop);
 
 // Detection of shared prefixes from the block tables (one workgroup,
 // num_seqs <= kCascadeMaxSeqs): sequences whose first page is the same

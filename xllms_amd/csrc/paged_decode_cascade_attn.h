@@ -1,7 +1,9 @@
 // Attention of the cascade (prefix-aware) decode on the MFMA tile path, in
 // two launches: both batches of the plan (paged_decode_cascade.h) in one
 // partition launch, then one merge that combines every output row's suffix
-// state with its prefix state.
+// state with its prefix state.  With at most kInPlanGroupsMax groups (and
+// LDS for two workgroups per CU) the partition launch also builds the plan
+// itself (below); otherwise the plan kernels run first.
 //
 // Partition.  The workgroups of one launch are split between the prefix
 // batch (two 32-row head tiles per (sequence, kv head), R = 2, paired: the
@@ -13,10 +15,10 @@
 // both batches (LDS) and takes the same split: the prefix batch gets a share
 // of the workgroups proportional to its wavefront-units (a prefix unit
 // occupies a pair of wavefronts) weighted by kCascadeUnitCost.  Measured on
-// MI355X at config 5 (cascade step): weights 0.6 / 0.8 / 1.0 / 1.25 gave
-// 123.8 / 112.1-112.4 / 116.4-116.5 / 120.0 us on one box, 0.7 / 0.8 / 0.9 /
-// 1.0 gave 120.2-120.6 / 122.8-123.0 / 124.9-125.0 / 126.0-126.1 us on
-// another: the best weight differs between boxes, 0.75 is near it on both.
+// MI355X at config 5 (cascade step, in-kernel plan): weights 0.75 / 0.85 /
+// 0.95 / 1.05 gave 116.7 / 113.6-113.8 / 114.5-114.8 / 116.6-116.8 us on one
+// box.  (With the plan kernels, whose prefix pieces do not look up their
+// members, the best weight was 0.75-0.8 and differed between boxes.)
 // Run as two launches, the prefix batch (a few thousand short ranges) spent
 // ~30 us mostly in latency while the device's bandwidth went unused; here
 // its ranges stream beside the suffix batch's.  Both bodies run in
@@ -35,6 +37,7 @@
 
 #include <hip/hip_ext.h>
 
+#include <climits>
 #include <cstdint>
 
 #include "paged_decode_cascade.h"
@@ -45,7 +48,7 @@ namespace xhip {
 // Weight of a prefix-batch split unit against a suffix-batch unit in the
 // workgroup split, in percent.
 #ifndef XHIP_CASCADE_UNIT_COST
-#define XHIP_CASCADE_UNIT_COST 75
+#define XHIP_CASCADE_UNIT_COST 85
 #endif
 constexpr int kCascadeUnitCost = XHIP_CASCADE_UNIT_COST;
 
@@ -98,6 +101,180 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, 2) void paged_decode_casca
         mfma_partition_body<KV, D, 2, true>(pp, plens, ptables, pre_p, l, gp * NW, sm.a);
     else
         mfma_partition_body<KV, D, RS>(ps, slens, stables, pre_s, l - gp, (G - gp) * NW, sm.b);
+}
+
+// In-kernel plan.  With at most kInPlanGroupsMax groups, every workgroup of
+// the partition launch builds the plan from the caller's arrays in its own
+// LDS, instead of two plan launches writing the batches to memory first:
+//   1. the caller's lengths, group ids and prefix pages (one round trip);
+//   2. members, as in the plan kernels: a group id in range whose prefix of
+//      P pages (1 <= P <= max_blocks, P pages within the sequence) is
+//      shared; each sequence's suffix length, first private page and split
+//      units, scanned within each wavefront;
+//   3. by wavefront 0, 64 groups at a time, each group's
+//      ceil(members * G / rows) prefix-batch sequences (length, table row =
+//      the group's lowest member, split units); by all, the suffix batch's
+//      unit prefix;
+//   4. the workgroup split.
+// Every workgroup computes the same plan.  A prefix-batch piece finds the
+// members its query rows belong to when it starts (mfma_load_q, kSrcPrefix):
+// the members of a group are ranked in sequence order, so the rows a piece
+// computes are the same members' in every workgroup.  Workgroup 0 also
+// stores what the merge reads: both unit prefixes, the split and the
+// batches' lengths; p_row, every member's first row in the prefix batch, is
+// stored by the piece that starts its prefix-batch sequence (kv head 0), and
+// -1 for every other sequence by workgroup 0.
+// LDS ints of the in-kernel plan: B caller sequences, V prefix-batch
+// sequences, NG groups.
+__host__ __device__ constexpr long long inplan_lds_ints(long long B, long long V, long long NG) {
+    return (V + 1) + (B + 1) + 3 * B + 6 * V + 3 * NG;
+}
+
+// Partition launch over both batches with the in-kernel plan.  pp / ps are
+// the batches as the merge reads them (their seq_lens: workspace arrays this
+// kernel's workgroup 0 fills); lens / tables / pgroup / pblocks are the
+// caller's arrays, ps.q / ps.q_rows its query rows.
+template <int KV, int D, int RS>
+__global__ __launch_bounds__(64 * kMfmaWavesPerGroup, 2) void paged_decode_cascade_inplan_kernel(
+    const DecodeParams pp, const DecodeParams ps, const int *__restrict__ lens,
+    const int *__restrict__ tables, const int *__restrict__ pgroup,
+    const int *__restrict__ pblocks, int num_groups, int *__restrict__ p_row) {
+    constexpr int NW = kMfmaWavesPerGroup, NT = 64 * NW;
+    extern __shared__ int lds[];
+    __shared__ MfmaLdsPair<D, RS> sm;
+    __shared__ int s_part[NW];
+    __shared__ int s_win[NW][2 * kMfmaHeads];  // prefix pieces' members (mfma_load_q)
+    const int B = ps.num_seqs, V = pp.num_seqs, NG = num_groups;
+    const int G = ps.group, rows = pp.group, bsz = ps.block_size;
+    int *pre_p = lds;
+    int *pre_s = pre_p + V + 1;
+    int *slen = pre_s + B + 1, *soff = slen + B, *grp = soff + B;
+    int *vlen = grp + B, *vrow = vlen + V, *vdesc = vrow + V;
+    int *gP = vdesc + 4 * V, *gcnt = gP + NG, *gfirst = gcnt + NG;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    // 1. (every prefix-batch sequence unused until step 3)
+    for (int s = tid; s < B; s += NT) {
+        slen[s] = min(max(lens[s], 0), ps.max_ctx);
+        grp[s] = pgroup[s];
+    }
+    for (int g = tid; g < NG; g += NT) {
+        gP[g] = pblocks[g];
+        gcnt[g] = 0;
+        gfirst[g] = INT_MAX;
+    }
+    for (int v = tid; v < V; v += NT) {
+        vlen[v] = 0;
+        vrow[v] = 0;
+        vdesc[4 * v] = v;
+        vdesc[4 * v + 1] = 0;
+        vdesc[4 * v + 2] = 0;
+        vdesc[4 * v + 3] = -1;
+    }
+    __syncthreads();
+    // 2. (thread t takes sequences [t * per, (t + 1) * per), as batch_prefix)
+    const int per = (B + NT - 1) / NT;
+    const int segs_s = seq_segments(ps);
+    int ls = 0;
+    for (int i = 0; i < per; i++) {
+        const int s = tid * per + i;
+        if (s < B) {
+            const int g = grp[s], L = slen[s];
+            int P = 0;
+            if (g >= 0 && g < NG) {
+                P = gP[g];
+                if (P < 1 || P > ps.max_blocks || (long long)P * bsz > L) P = 0;
+            }
+            grp[s] = P > 0 ? g : -1;
+            soff[s] = P;
+            slen[s] = L - P * bsz;
+            if (P > 0) {
+                atomicAdd(&gcnt[g], 1);
+                atomicMin(&gfirst[g], s);
+            }
+            const int t = segment_units(ps, (L - P * bsz + 15) >> 4) * segs_s;
+            pre_s[s] = t;
+            ls += t;
+        }
+    }
+    int is = ls;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int u = __shfl_up(is, off);
+        if (lane >= off) is += u;
+    }
+    if (lane == 63) s_part[wave] = is;
+    __syncthreads();
+    // 3. (groups 64 at a time, lane g taking group g0 + g)
+    if (wave == 0) {
+        int vt = 0, tp = 0;  // prefix-batch sequences and units of the groups so far
+        for (int g0 = 0; g0 < NG; g0 += 64) {
+            const int g = g0 + lane;
+            const int n = g < NG ? gcnt[g] : 0;
+            const int nv = (n * G + rows - 1) / rows;
+            const int u = n > 0 ? segment_units(pp, (gP[g] * bsz + 15) >> 4) * seq_segments(pp) : 0;
+            int sv = nv, su = nv * u;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const int a = __shfl_up(sv, off), b = __shfl_up(su, off);
+                if (lane >= off) {
+                    sv += a;
+                    su += b;
+                }
+            }
+            const int vb = vt + sv - nv, pb = tp + su - nv * u;
+            for (int k = 0; k < nv; k++) {
+                const int v = vb + k;
+                vlen[v] = gP[g] * bsz;
+                vrow[v] = gfirst[g];
+                vdesc[4 * v] = vb;
+                vdesc[4 * v + 1] = n;
+                vdesc[4 * v + 3] = g;
+                pre_p[v] = pb + k * u;
+            }
+            vt += __builtin_amdgcn_readlane(sv, 63);
+            tp += __builtin_amdgcn_readlane(su, 63);
+        }
+        for (int v = vt + lane; v <= V; v += 64) pre_p[v] = tp;  // unused, and the total
+    }
+    {
+        int base = 0;
+#pragma unroll
+        for (int k = 0; k < NW - 1; k++) base += k < wave ? s_part[k] : 0;
+        int run = base + is - ls;
+        for (int i = 0; i < per; i++) {
+            const int s = tid * per + i;
+            if (s < B) {
+                const int t = pre_s[s];
+                pre_s[s] = run;
+                run += t;
+            }
+        }
+        if (tid == NT - 1) pre_s[B] = base + is;
+    }
+    __syncthreads();
+    // 4.
+    const int Gw = gridDim.x;
+    const int gp = cascade_prefix_groups(pre_p[V], pre_s[B], Gw);
+    const int l = xcd_local_block(blockIdx.x, Gw);
+    if (blockIdx.x == 0) {
+        for (int v = tid; v <= V; v += NT) pp.ws_prefix[v] = pre_p[v];
+        for (int q = tid; q <= B; q += NT) ps.ws_prefix[q] = pre_s[q];
+        if (tid == 0) pp.ws_prefix[V + 1] = gp;
+        for (int v = tid; v < V; v += NT) const_cast<int *>(pp.seq_lens)[v] = vlen[v];
+        for (int q = tid; q < B; q += NT) {
+            const_cast<int *>(ps.seq_lens)[q] = slen[q];
+            if (grp[q] < 0) p_row[q] = -1;
+        }
+    }
+    const CascadeLdsPlan cp{slen,  soff,       vlen, vrow, vdesc,         grp,  &s_win[0][0],
+                            p_row, (const char *)ps.q, ps.q_rows, ps.num_heads, G, rows, B};
+    if (l < gp)
+        mfma_partition_body<KV, D, 2, true, kSrcPrefix>(pp, nullptr, tables, pre_p, l, gp * NW,
+                                                        sm.a, &cp);
+    else
+        mfma_partition_body<KV, D, RS, false, kSrcSuffix>(ps, nullptr, tables, pre_s, l - gp,
+                                                          (Gw - gp) * NW, sm.b, &cp);
 }
 
 // (m, l, acc) <- (m, l, acc) (+) a finished row: the state (lse, 1, row).
@@ -210,18 +387,33 @@ __global__ __launch_bounds__(NT) void paged_decode_cascade_merge_kernel(
 
 template <int KV, int D, int RS>
 static hipError_t launch_cascade_attn_rs(const DecodeParams &pp, const DecodeParams &ps,
-                                         const int *p_row, int rows, hipStream_t st,
-                                         hipEvent_t ev_start, hipEvent_t ev_stop) {
+                                         const int *p_row, int rows, const CascadeInPlan *ip,
+                                         hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
     const unsigned grid = (unsigned)(ps.num_waves / kMfmaWavesPerGroup);
-    const size_t lds = (size_t)(pp.num_seqs + ps.num_seqs + 2) * sizeof(int);
-    auto kernel = paged_decode_cascade_mfma_kernel<KV, D, RS>;
-    if (ev_start || ev_stop)
-        hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWavesPerGroup),
-                              (std::uint32_t)lds, st, ev_start, ev_stop, 0u, pp, ps, pp.seq_lens,
-                              pp.block_tables, ps.seq_lens, ps.block_tables);
-    else
-        hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWavesPerGroup), lds, st, pp, ps,
-                           pp.seq_lens, pp.block_tables, ps.seq_lens, ps.block_tables);
+    const dim3 block(64 * kMfmaWavesPerGroup);
+    if (ip) {
+        const size_t lds =
+            (size_t)inplan_lds_ints(ps.num_seqs, pp.num_seqs, ip->num_groups) * sizeof(int);
+        auto kernel = paged_decode_cascade_inplan_kernel<KV, D, RS>;
+        int *prow = const_cast<int *>(p_row);
+        if (ev_start || ev_stop)
+            hipExtLaunchKernelGGL(kernel, dim3(grid), block, (std::uint32_t)lds, st, ev_start,
+                                  ev_stop, 0u, pp, ps, ip->lens, ip->tables, ip->prefix_group,
+                                  ip->prefix_blocks, ip->num_groups, prow);
+        else
+            hipLaunchKernelGGL(kernel, dim3(grid), block, lds, st, pp, ps, ip->lens, ip->tables,
+                               ip->prefix_group, ip->prefix_blocks, ip->num_groups, prow);
+    } else {
+        const size_t lds = (size_t)(pp.num_seqs + ps.num_seqs + 2) * sizeof(int);
+        auto kernel = paged_decode_cascade_mfma_kernel<KV, D, RS>;
+        if (ev_start || ev_stop)
+            hipExtLaunchKernelGGL(kernel, dim3(grid), block, (std::uint32_t)lds, st, ev_start,
+                                  ev_stop, 0u, pp, ps, pp.seq_lens, pp.block_tables, ps.seq_lens,
+                                  ps.block_tables);
+        else
+            hipLaunchKernelGGL(kernel, dim3(grid), block, lds, st, pp, ps, pp.seq_lens,
+                               pp.block_tables, ps.seq_lens, ps.block_tables);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const unsigned segs = (unsigned)(ps.num_seqs * ps.num_kv_heads * ps.head_tiles);
@@ -231,7 +423,14 @@ static hipError_t launch_cascade_attn_rs(const DecodeParams &pp, const DecodePar
 }
 
 template <int KV, int D>
-static const void *cascade_fn(int rs) {
+static const void *cascade_fn(int rs, bool inplan) {
+    if (inplan) {
+        if (rs == 1)
+            return reinterpret_cast<const void *>(&paged_decode_cascade_inplan_kernel<KV, D, 1>);
+        if (rs == 2)
+            return reinterpret_cast<const void *>(&paged_decode_cascade_inplan_kernel<KV, D, 2>);
+        return nullptr;
+    }
     if (rs == 1) return reinterpret_cast<const void *>(&paged_decode_cascade_mfma_kernel<KV, D, 1>);
     if (rs == 2) return reinterpret_cast<const void *>(&paged_decode_cascade_mfma_kernel<KV, D, 2>);
     return nullptr;
@@ -240,10 +439,10 @@ static const void *cascade_fn(int rs) {
 #define XHIP_FOR_CASCADE_HEAD_SIZES(X) X(32) X(64) X(96) X(128)
 
 template <int KV>
-static int cascade_occupancy_dtype(int head_size, int rs, size_t lds_bytes) {
+static int cascade_occupancy_dtype(int head_size, int rs, bool inplan, size_t lds_bytes) {
     const void *fn = nullptr;
     switch (head_size) {
-#define XHIP_CASE(d) case d: fn = cascade_fn<KV, d>(rs); break;
+#define XHIP_CASE(d) case d: fn = cascade_fn<KV, d>(rs, inplan); break;
         XHIP_FOR_CASCADE_HEAD_SIZES(XHIP_CASE)
 #undef XHIP_CASE
     default: break;
@@ -259,16 +458,16 @@ static int cascade_occupancy_dtype(int head_size, int rs, size_t lds_bytes) {
 template <int KV>
 static hipError_t launch_cascade_attn_dtype(const DecodeParams &pp, const DecodeParams &ps,
                                             const int *p_row, int rows, int head_size,
-                                            int rs, hipStream_t st, hipEvent_t ev_start,
-                                            hipEvent_t ev_stop) {
+                                            int rs, const CascadeInPlan *ip, hipStream_t st,
+                                            hipEvent_t ev_start, hipEvent_t ev_stop) {
     switch (head_size) {
 #define XHIP_CASE(d)                                                                          \
     case d:                                                                                   \
         if (rs == 1)                                                                          \
-            return launch_cascade_attn_rs<KV, d, 1>(pp, ps, p_row, rows, st, ev_start,   \
+            return launch_cascade_attn_rs<KV, d, 1>(pp, ps, p_row, rows, ip, st, ev_start,    \
                                                     ev_stop);                                 \
         if (rs == 2)                                                                          \
-            return launch_cascade_attn_rs<KV, d, 2>(pp, ps, p_row, rows, st, ev_start,   \
+            return launch_cascade_attn_rs<KV, d, 2>(pp, ps, p_row, rows, ip, st, ev_start,    \
                                                     ev_stop);                                 \
         return hipErrorInvalidValue;
         XHIP_FOR_CASCADE_HEAD_SIZES(XHIP_CASE)

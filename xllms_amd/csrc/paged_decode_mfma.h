@@ -225,6 +225,55 @@ __device__ __forceinline__ void mfma_tile(const DecodeParams &p, const u32x4 (*q
     }
 }
 
+// Where the partition body finds a sequence's length, block table and query
+// rows.  kSrcBatch: the batch's own arrays (DecodeParams and the lens /
+// tables kernel arguments).  The cascade's in-kernel plan
+// (paged_decode_cascade_attn.h) keeps the per-sequence data of its two
+// batches in LDS (CascadeLdsPlan) and reads the caller's block tables and
+// query rows in place: kSrcSuffix, the suffix of each caller sequence (its
+// length past the shared prefix, its pages from its first private one);
+// kSrcPrefix, the prefix-batch sequences (a group's shared pages, from its
+// lowest member's table row, and query rows gathered from its members).
+enum { kSrcBatch = 0, kSrcSuffix = 1, kSrcPrefix = 2 };
+
+struct CascadeLdsPlan {
+    const int *slen;    // [num_seqs] suffix length of caller sequence s
+    const int *soff;    // [num_seqs] its shared prefix pages (the suffix's first page)
+    const int *vlen;    // [v_max] length of prefix-batch sequence v (0: unused)
+    const int *vrow;    // [v_max] block-table row of v's pages (its group's lowest member)
+    const int *vdesc;   // [v_max][4] v's group: its first prefix-batch sequence, its
+                        // members, -, the group id (-1: v unused)
+    const int *grp;     // [num_seqs] group of caller sequence s (-1: none)
+    int *win;           // [waves per workgroup][32] each wavefront's members of a piece
+    int *p_row;         // [num_seqs] (global) a member's first row in the prefix batch
+    const char *q;      // caller's query rows: [num_seqs][num_heads][head_size]
+    const char *const *q_rows;  // or, when set, sequence s's rows at q_rows[s]
+    int num_heads;      // caller's query heads
+    int group;          // caller's query heads per kv head
+    int rows;           // query rows per kv head of a prefix-batch sequence
+    int num_seqs;       // caller's sequences
+};
+
+// Clamped length of sequence s of the batch under source SRC.
+template <int SRC>
+__device__ __forceinline__ int src_len(const DecodeParams &p, const int *__restrict__ lens, int s,
+                                       const CascadeLdsPlan *cp) {
+    if constexpr (SRC == kSrcBatch) return min(max(lens[s], 0), p.max_ctx);
+    else if constexpr (SRC == kSrcSuffix) return __builtin_amdgcn_readfirstlane(cp->slen[s]);
+    else return __builtin_amdgcn_readfirstlane(cp->vlen[s]);
+}
+
+// Block table of sequence s of the batch under source SRC.
+template <int SRC>
+__device__ __forceinline__ const int *src_table(const DecodeParams &p,
+                                                const int *__restrict__ tables, int s,
+                                                const CascadeLdsPlan *cp) {
+    if constexpr (SRC == kSrcBatch) return tables + (size_t)s * p.max_blocks;
+    else if constexpr (SRC == kSrcSuffix)
+        return tables + (size_t)s * p.max_blocks + __builtin_amdgcn_readfirstlane(cp->soff[s]);
+    else return tables + (size_t)__builtin_amdgcn_readfirstlane(cp->vrow[s]) * p.max_blocks;
+}
+
 // One piece of a wavefront's stream-K range: tokens [t_begin, t_end) of the
 // segment (sequence s, kv head kvh, head tile ht).  `whole`: the piece is the
 // entire segment (the output is written directly); else its partial goes to
@@ -243,12 +292,13 @@ struct RangeCursor {
 // The next piece of the range (false at its end).  Same decomposition as
 // stream_k_walk, one piece at a time, so the kernel can look one piece ahead.
 // A range that ends inside a segment's start-up units makes no piece of it.
-template <int TT>
+template <int TT, int SRC = kSrcBatch>
 __device__ __forceinline__ bool next_piece(const DecodeParams &p, const int *__restrict__ lens,
-                                           const int *pre, RangeCursor &c, MfmaPiece &pc) {
+                                           const int *pre, RangeCursor &c, MfmaPiece &pc,
+                                           const CascadeLdsPlan *cp = nullptr) {
     const int segs = seq_segments(p);
     while (c.g < c.g_end) {
-        const int L = min(max(lens[c.s], 0), p.max_ctx);
+        const int L = src_len<SRC>(p, lens, c.s, cp);
         const int Ts = (L + TT - 1) / TT;
         const int Cs = segment_units(p, Ts);
         const int base = __builtin_amdgcn_readfirstlane(pre[c.s]);
@@ -286,12 +336,61 @@ __device__ __forceinline__ bool next_piece(const DecodeParams &p, const int *__r
 
 // Q rows of the piece's (up to) 16R query heads in the MFMA B layout (row
 // block b, lane: head 16b + j, dims 32c+8g..+7); heads past the group read
-// as zero.
-template <int D, int R>
+// as zero.  kSrcPrefix: with the group's rows laid end to end (rows per
+// prefix-batch sequence), row k is query head k % G (of the kv head's G) of
+// the group's member of rank k / G, members ranked in sequence order; rows
+// past the last member read as zero.  The wavefront finds the (at most 16R)
+// members of its rows with one ballot per 64 caller sequences, and the piece
+// that starts its sequence's kv head 0 stores each member's first row
+// (p_row).
+template <int D, int R, int SRC = kSrcBatch>
 __device__ __forceinline__ void mfma_load_q(const DecodeParams &p, const MfmaPiece &pc, int lane,
-                                            u32x4 (&q)[R][MfmaGeometry<D>::kQkSteps]) {
+                                            u32x4 (&q)[R][MfmaGeometry<D>::kQkSteps],
+                                            const CascadeLdsPlan *cp = nullptr) {
     const int j = lane & 15, g = lane >> 4;
     const int g0 = pc.ht * kMfmaHeads * R;
+    if constexpr (SRC == kSrcPrefix) {
+        const int *d = cp->vdesc + 4 * pc.s;
+        const int vbase = __builtin_amdgcn_readfirstlane(d[0]);
+        const int count = __builtin_amdgcn_readfirstlane(d[1]);
+        const int gid = __builtin_amdgcn_readfirstlane(d[3]);
+        const int G = cp->group;
+        const int row0 = (pc.s - vbase) * cp->rows + g0;
+        const int r_lo = row0 / G, r_hi = min((row0 + 16 * R - 1) / G, count - 1);
+        int *win = cp->win + (threadIdx.x >> 6) * (16 * R);
+        int acc = 0;
+        for (int c0 = 0; c0 < cp->num_seqs && acc <= r_hi; c0 += 64) {
+            const int s = c0 + lane;
+            const bool in = s < cp->num_seqs && cp->grp[s] == gid;
+            const unsigned long long m = __ballot(in);
+            const int rk = acc + (int)__builtin_amdgcn_mbcnt_hi(
+                                     (unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+            if (in && rk >= r_lo && rk <= r_hi) win[rk - r_lo] = s;
+            acc += __popcll(m);
+        }
+        // (the window is written and read by this wavefront: its LDS
+        // accesses complete in order)
+        __builtin_amdgcn_wave_barrier();
+        const size_t row_bytes = (size_t)D * 2;
+        const bool first = pc.kvh == 0 && pc.t_begin == 0;
+#pragma unroll
+        for (int b = 0; b < R; b++) {
+            const int rig = row0 + 16 * b + j;
+            const int r = rig / G, gq = rig - r * G;
+            const char *src = nullptr;
+            if (r < count) {
+                const int s = win[r - r_lo];
+                const size_t h = (size_t)pc.kvh * G + gq;
+                src = cp->q_rows ? cp->q_rows[s] + h * row_bytes
+                                 : cp->q + ((size_t)s * cp->num_heads + h) * row_bytes;
+                if (first && gq == 0 && g == 0) cp->p_row[s] = vbase * cp->rows + r * G;
+            }
+#pragma unroll
+            for (int c = 0; c < MfmaGeometry<D>::kQkSteps; c++)
+                q[b][c] = src ? load16(src + (size_t)(32 * c + 8 * g) * 2) : u32x4{0, 0, 0, 0};
+        }
+        return;
+    }
     const int nh = min(kMfmaHeads * R, p.group - g0);
     const char *q0 = q_row(p, pc.s, pc.kvh * p.group + g0, D, 2);
 #pragma unroll
@@ -351,9 +450,11 @@ __device__ __forceinline__ void mfma_fold_apply(const MfmaFold<D, R> &f, int lan
 
 // Block ids of the piece's tiles first .. first+63, lane i holding tile
 // first+i (clamped to the piece's last tile).
+template <int SRC = kSrcBatch>
 __device__ __forceinline__ int mfma_load_ids(const DecodeParams &p, const int *__restrict__ tables,
-                                             const MfmaPiece &pc, int first, int lane) {
-    const int *bt = tables + (size_t)pc.s * p.max_blocks;
+                                             const MfmaPiece &pc, int first, int lane,
+                                             const CascadeLdsPlan *cp = nullptr) {
+    const int *bt = src_table<SRC>(p, tables, pc.s, cp);
     const int ti = pc.t_begin + 16 * (first + lane);
     return bt[(ti < pc.t_end ? ti : pc.t_end - 1) >> p.bs_shift];
 }
@@ -546,12 +647,15 @@ __device__ __forceinline__ void absorb_partial(const DecodeParams &p, int slot, 
 // `pre` is in LDS.  PAIR: the batch's head tiles are paired
 // (DecodeParams::pair_tiles): the workgroup's two pairs of wavefronts walk
 // two ranges, one head tile per wavefront, and every cut piece leaves its
-// own partial (no workgroup combine).
-template <int KV, int D, int R, bool PAIR = false>
+// own partial (no workgroup combine).  SRC: where the batch's per-sequence
+// data is (kSrcBatch: lens / tables and p; else the in-kernel cascade plan
+// cp).
+template <int KV, int D, int R, bool PAIR = false, int SRC = kSrcBatch>
 __device__ __forceinline__ void mfma_partition_body(
     const DecodeParams &p, const int *__restrict__ lens, const int *__restrict__ tables,
     const int *pre, int wg, int waves,
-    MfmaLds<D, R, PAIR ? 0 : mfma_wg_fixup(kMfmaHeads * R, D)> &sm) {
+    MfmaLds<D, R, PAIR ? 0 : mfma_wg_fixup(kMfmaHeads * R, D)> &sm,
+    const CascadeLdsPlan *cp = nullptr) {
     using G = MfmaGeometry<D>;
     constexpr int FIX = PAIR ? 0 : mfma_wg_fixup(kMfmaHeads * R, D);
     constexpr int NW = kMfmaWavesPerGroup;
@@ -593,10 +697,17 @@ __device__ __forceinline__ void mfma_partition_body(
 
     // A range inside one segment's start-up units holds no tile (only when
     // tpw <= seg_cost); the segment's tiles belong to the next wavefront.
-    if (g_lo < total && next_piece<16>(p, lens, pre, cur, pc)) {
+    if (g_lo < total && next_piece<16, SRC>(p, lens, pre, cur, pc, cp)) {
         u32x4 q[R][G::kQkSteps];
-        mfma_load_q<D, R>(p, pc, lane, q);
-        int ids = mfma_load_ids(p, tables, pc, 0, lane);
+        int ids;
+        if constexpr (SRC == kSrcPrefix) {
+            // (the block ids' round trip overlaps the members' lookup)
+            ids = mfma_load_ids<SRC>(p, tables, pc, 0, lane, cp);
+            mfma_load_q<D, R, SRC>(p, pc, lane, q, cp);
+        } else {
+            mfma_load_q<D, R, SRC>(p, pc, lane, q, cp);
+            ids = mfma_load_ids<SRC>(p, tables, pc, 0, lane, cp);
+        }
         // fold base of the current piece (requested a piece ahead from here on)
         int fold_base = (p.fold_row && pc.t_begin == 0) ? p.fold_row[pc.s] : -1;
         MfmaTileRegs<D> ra, rb;
@@ -610,12 +721,12 @@ __device__ __forceinline__ void mfma_partition_body(
 
         while (true) {
             MfmaPiece pn = pc;
-            const bool has_next = next_piece<16>(p, lens, pre, cur, pn);
+            const bool has_next = next_piece<16, SRC>(p, lens, pre, cur, pn, cp);
             // Issued whether or not there is a next piece (pn is then the
             // current one again), so every path through the loop below has
             // the same loads in flight and the compiler's wait counts stay
             // exact.
-            const int ids_n = mfma_load_ids(p, tables, pn, 0, lane);
+            const int ids_n = mfma_load_ids<SRC>(p, tables, pn, 0, lane, cp);
             const int fold_base_n =
                 (p.fold_row && has_next && pn.t_begin == 0) ? p.fold_row[pn.s] : -1;
             const char *kb = (const char *)p.k + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
@@ -624,7 +735,7 @@ __device__ __forceinline__ void mfma_partition_body(
             const char *vb_n = (const char *)p.v + (size_t)pn.kvh * (size_t)p.kv_head_stride * 2;
             const bool cached = pc.s < p.cached_seqs;
             const bool cached_n = has_next && pn.s < p.cached_seqs;
-            const int *bt = tables + (size_t)pc.s * p.max_blocks;
+            const int *bt = src_table<SRC>(p, tables, pc.s, cp);
 
 #pragma unroll
             for (int b = 0; b < R; b++) {
@@ -638,7 +749,7 @@ __device__ __forceinline__ void mfma_partition_body(
             if (R == 1 && fold.base >= 0) mfma_fold_load<D, R>(p, pc, lane, fold);
             const int ntiles = (pc.t_end - pc.t_begin + 15) >> 4;
             for (int i = 0; i < ntiles; i++) {
-                if (i > 0 && (i & 63) == 0) ids = mfma_load_ids(p, tables, pc, i, lane);
+                if (i > 0 && (i & 63) == 0) ids = mfma_load_ids<SRC>(p, tables, pc, i, lane, cp);
                 const int t0 = pc.t_begin + 16 * i;
                 // The next tile: this piece's, else the next piece's first (all
                 // rows out of range when there is none).
@@ -689,7 +800,7 @@ __device__ __forceinline__ void mfma_partition_body(
             pc = pn;
             ids = ids_n;
             fold_base = fold_base_n;
-            mfma_load_q<D, R>(p, pc, lane, q);
+            mfma_load_q<D, R, SRC>(p, pc, lane, q, cp);
         }
     }
 
