@@ -840,8 +840,8 @@ def main() -> int:
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "step_frac": round(step_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
-                     "kernel": ("cascade decode step (plan, one partition launch over the prefix "
-                                "and suffix batches, merge)") if args.cascade
+                     "kernel": ("cascade decode step (one partition launch that plans and "
+                                "computes the prefix and suffix batches, merge)") if args.cascade
                      else partition_kernel_name(wl),
                      "kernel_avg_us": round(kernel_avg_ms * 1e3, 2)},
         "measured_peak": measured_peak,
