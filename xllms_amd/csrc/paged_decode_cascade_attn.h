@@ -14,11 +14,13 @@
 // own stream-K plan.  Every workgroup scans the split units of
 // both batches (LDS) and takes the same split: the prefix batch gets a share
 // of the workgroups proportional to its wavefront-units (a prefix unit
-// occupies a pair of wavefronts) weighted by kCascadeUnitCost.  Measured on
-// MI355X at config 5 (cascade step, in-kernel plan): weights 0.75 / 0.85 /
-// 0.95 / 1.05 gave 116.7 / 113.6-113.8 / 114.5-114.8 / 116.6-116.8 us on one
-// box.  (With the plan kernels, whose prefix pieces do not look up their
-// members, the best weight was 0.75-0.8 and differed between boxes.)
+// occupies a pair of wavefronts) weighted by kCascadeUnitCost, plus the
+// workgroups the suffix plan would leave empty.  Measured on MI355X at
+// config 5 (cascade step, in-kernel plan, one box): weights 0.65 / 0.75 /
+// 0.85 gave 121.3-121.5 / 111.6-111.7 / 114.4-114.5 us (86 / 97 / 108 prefix
+// workgroups of 512); without the empty suffix workgroups moved over, 0.85
+// (99) gave 113.2-113.3 us.  The step is sensitive to the split: both
+// batches' ranges grow by a unit at some workgroup counts.
 // Run as two launches, the prefix batch (a few thousand short ranges) spent
 // ~30 us mostly in latency while the device's bandwidth went unused; here
 // its ranges stream beside the suffix batch's.  Both bodies run in
@@ -48,21 +50,29 @@ namespace xhip {
 // Weight of a prefix-batch split unit against a suffix-batch unit in the
 // workgroup split, in percent.
 #ifndef XHIP_CASCADE_UNIT_COST
-#define XHIP_CASCADE_UNIT_COST 85
+#define XHIP_CASCADE_UNIT_COST 75
 #endif
 constexpr int kCascadeUnitCost = XHIP_CASCADE_UNIT_COST;
 
 // Workgroups of the prefix body in a launch of G >= 2 workgroups, from the
 // split units of the prefix (tp) and suffix (ts) batches: each batch with
-// units gets at least one.  Integer arithmetic only: every workgroup
-// computes the same split.
-__device__ __forceinline__ int cascade_prefix_groups(int tp, int ts, int G) {
+// units gets at least one.  The suffix plan gives every wavefront
+// ceil(ts / its wavefronts) units (at least min_tpw), which can leave its
+// last workgroups nothing: those go to the prefix body, whose ranges get
+// shorter while the suffix's stay the same.  Integer arithmetic only: every
+// workgroup computes the same split.
+__device__ __forceinline__ int cascade_prefix_groups(int tp, int ts, int G, int min_tpw) {
     if (tp <= 0) return 0;
     if (ts <= 0) return G;
     // a prefix unit occupies both wavefronts of a pair
     const long long a = 2LL * tp * kCascadeUnitCost, b = (long long)ts * 100;
-    const int gp = (int)((a * G + (a + b) / 2) / (a + b));
-    return gp < 1 ? 1 : (gp > G - 1 ? G - 1 : gp);
+    int gp = (int)((a * G + (a + b) / 2) / (a + b));
+    gp = gp < 1 ? 1 : (gp > G - 1 ? G - 1 : gp);
+    const int ws = (G - gp) * kMfmaWavesPerGroup;
+    const int tpw = tiles_per_wave(ts, ws, min_tpw);
+    const int used = (ts + tpw - 1) / tpw;  // suffix wavefronts with units
+    gp += (ws - used) / kMfmaWavesPerGroup;
+    return gp > G - 1 ? G - 1 : gp;
 }
 
 // LDS of the two bodies (one runs per workgroup): the prefix body's (paired
@@ -91,7 +101,8 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, 2) void paged_decode_casca
     batch_prefix<16, NW>(pp, pre_p);
     batch_prefix<16, NW>(ps, pre_s);
     const int G = gridDim.x;
-    const int gp = cascade_prefix_groups(pre_p[pp.num_seqs], pre_s[ps.num_seqs], G);
+    const int gp = cascade_prefix_groups(pre_p[pp.num_seqs], pre_s[ps.num_seqs], G,
+                                         ps.min_tiles_per_wave);
     if (blockIdx.x == 0 && threadIdx.x == 0) pp.ws_prefix[pp.num_seqs + 1] = gp;
     // neighbouring logical workgroups share an XCD (and its L2).  (Giving
     // every XCD its share of prefix workgroups instead measured 0.5-1 us
@@ -255,7 +266,7 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, 2) void paged_decode_casca
     __syncthreads();
     // 4.
     const int Gw = gridDim.x;
-    const int gp = cascade_prefix_groups(pre_p[V], pre_s[B], Gw);
+    const int gp = cascade_prefix_groups(pre_p[V], pre_s[B], Gw, ps.min_tiles_per_wave);
     const int l = xcd_local_block(blockIdx.x, Gw);
     if (blockIdx.x == 0) {
         for (int v = tid; v <= V; v += NT) pp.ws_prefix[v] = pre_p[v];
