@@ -197,3 +197,23 @@ def test_cascade_inkernel_plan_matches_plan_kernels(cuda, dtype, D, H, KVH):
             assert np.array_equal(got, want)
         assert_close(got, ref, wl.kv_dtype, f"cascade {dtype} D={D}, in-kernel plan")
         assert_close(want, ref, wl.kv_dtype, f"cascade {dtype} D={D}, plan kernels")
+
+
+def test_cascade_inkernel_plan_with_many_groups(cuda):
+    """150 groups (the in-kernel plan lays them out 64 at a time) of one to
+    three members: the oracle's results, and bit-identical to the plan
+    kernels' (the group table padded to 300 entries)."""
+    rng = np.random.default_rng(21)
+    spec = [(1 + int(rng.integers(0, 4)), [int(x) for x in rng.integers(0, 60, size=1 + i % 3)])
+            for i in range(150)]
+    members = sum(len(sfx) for _, sfx in spec)
+    wl, pg, pb = shared_case(spec, singles=[1, 0, 45] + [17] * max(0, 300 - members - 3), H=32,
+                             KVH=8, D=128, seed=21)
+    print(f"case seqs={wl.num_seqs} groups={len(pb)}", flush=True)
+    dw = W.upload(wl)
+    got = run_cascade(wl, pg, pb, dw=dw).copy()
+    padded = np.concatenate([pb, np.zeros(300 - len(pb), np.int32)]).astype(np.int32)
+    dw.out.zero_()
+    want = run_cascade(wl, pg, padded, max_groups=300, dw=dw)
+    assert np.array_equal(got, want)
+    assert_close(got, O.run_workload(wl, precision="mt"), wl.kv_dtype, "cascade, 150 groups")
