@@ -576,6 +576,16 @@ XKV_EXPORT int nxt_kv_batch_tables(const NxtKvIndex *ix, const int32_t *seqs, in
     return NXT_KV_OK;
 }
 
+// Leading entries two page lists have in common, up to n (256- then
+// 32-byte runs compared with memcmp first).
+static int common_prefix(const int32_t *a, const int32_t *b, int n) {
+    int k = 0;
+    while (k + 64 <= n && std::memcmp(a + k, b + k, 64 * sizeof(int32_t)) == 0) k += 64;
+    while (k + 8 <= n && std::memcmp(a + k, b + k, 8 * sizeof(int32_t)) == 0) k += 8;
+    while (k < n && a[k] == b[k]) ++k;
+    return k;
+}
+
 XKV_EXPORT int nxt_kv_batch_prefix_groups(const NxtKvIndex *ix, const int32_t *seqs, int32_t n,
                                           int32_t *prefix_group, int32_t *prefix_blocks,
                                           int32_t *num_groups) {
@@ -586,36 +596,44 @@ XKV_EXPORT int nxt_kv_batch_prefix_groups(const NxtKvIndex *ix, const int32_t *s
         if (!(s[(size_t)i] = ix->seq(seqs[i]))) return NXT_KV_E_INVALID;
     const int bs = ix->block_size;
     auto full = [&](int32_t i) { return (int)(s[(size_t)i]->tokens.size() / (size_t)bs); };
-    // members by first page, in batch order
-    std::unordered_map<int32_t, std::vector<int32_t>> by_first;
-    std::vector<int32_t> firsts;
-    for (int32_t i = 0; i < n; ++i) {
-        if (full(i) < 1) continue;
-        const int32_t b = s[(size_t)i]->blocks[0];
-        auto &v = by_first[b];
-        if (v.empty()) firsts.push_back(b);
-        v.push_back(i);
-    }
-    std::vector<std::pair<int32_t, int32_t>> groups;  // (lowest member, prefix pages)
-    for (int32_t b : firsts) {
-        const std::vector<int32_t> &mem = by_first[b];
-        if (mem.size() < 2) continue;
-        const Sequence *lead = s[(size_t)mem[0]];
-        int P = full(mem[0]);
-        for (int32_t i : mem) {
-            const int lim = std::min(full(i), full(mem[0]));
-            int k = 0;
-            while (k < lim && s[(size_t)i]->blocks[(size_t)k] == lead->blocks[(size_t)k]) ++k;
-            P = std::min(P, k);
+    // members by first page, in batch order: (first page, batch index), sorted
+    std::vector<std::pair<int32_t, int32_t>> byf;
+    byf.reserve((size_t)n);
+    for (int32_t i = 0; i < n; ++i)
+        if (full(i) >= 1) byf.push_back({s[(size_t)i]->blocks[0], i});
+    std::sort(byf.begin(), byf.end());
+    // each run of two or more members: the pages every member shares with
+    // the lowest one, counting full pages only
+    struct Group {
+        int32_t lead, pages;
+        size_t begin, end;  // its members in byf
+    };
+    std::vector<Group> groups;
+    for (size_t a = 0; a < byf.size();) {
+        size_t b = a + 1;
+        while (b < byf.size() && byf[b].first == byf[a].first) ++b;
+        if (b - a >= 2) {
+            const int32_t lead = byf[a].second;
+            const int32_t *lb = s[(size_t)lead]->blocks.data();
+            int P = full(lead);
+            for (size_t k = a + 1; k < b && P > 0; ++k) {
+                const int32_t i = byf[k].second;
+                const int32_t *ib = s[(size_t)i]->blocks.data();
+                const int lim = std::min(full(i), P);
+                P = common_prefix(ib, lb, lim);
+            }
+            if (P >= 1) groups.push_back({lead, P, a, b});
         }
-        if (P >= 1) groups.push_back({mem[0], P});
+        a = b;
     }
-    std::sort(groups.begin(), groups.end());
+    // numbered by their lowest member
+    std::sort(groups.begin(), groups.end(),
+              [](const Group &x, const Group &y) { return x.lead < y.lead; });
     std::fill(prefix_group, prefix_group + n, -1);
     for (size_t g = 0; g < groups.size(); ++g) {
-        prefix_blocks[g] = groups[g].second;
-        for (int32_t i : by_first[s[(size_t)groups[g].first]->blocks[0]])
-            prefix_group[i] = (int32_t)g;
+        prefix_blocks[g] = groups[g].pages;
+        for (size_t k = groups[g].begin; k < groups[g].end; ++k)
+            prefix_group[byf[k].second] = (int32_t)g;
     }
     *num_groups = (int32_t)groups.size();
     return NXT_KV_OK;

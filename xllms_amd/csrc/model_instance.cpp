@@ -552,6 +552,7 @@ int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<st
                 st->h_bt.n = (size_t)B * width;
                 st->h_lens.n = st->h_group.n = (size_t)B;
                 nxt_kv_batch_tables(st->index, st->h_seqs.p, B, width, st->h_bt.p, st->h_lens.p);
+                tr.mark("tables");
                 nxt_kv_batch_prefix_groups(st->index, st->h_seqs.p, B, st->h_group.p,
                                            st->h_pblocks.p, &ng);
                 st->h_pblocks.n = (size_t)std::max(ng, 1);
@@ -559,7 +560,7 @@ int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<st
         }
     }
 
-    tr.mark("tables");
+    tr.mark("groups");
     // 3. one upload of everything the launches read, then the launches: the
     //    new rows, the copies of partly shared pages (a copy may read rows
     //    this exec writes), the query gather, the attention, the output scatter
