@@ -217,3 +217,14 @@ def test_cascade_inkernel_plan_with_many_groups(cuda):
     want = run_cascade(wl, pg, padded, max_groups=300, dw=dw)
     assert np.array_equal(got, want)
     assert_close(got, O.run_workload(wl, precision="mt"), wl.kv_dtype, "cascade, 150 groups")
+
+
+def test_cascade_every_suffix_empty(cuda):
+    """Every sequence is a member whose whole context is its group's prefix:
+    the suffix batch has no split units, so the launch's workgroups all run
+    the prefix batch, and the merge writes the prefix rows."""
+    wl, pg, pb = shared_case([(5, [0, 0, 0]), (2, [0, 0]), (9, [0] * 17)], H=32, KVH=8, D=128,
+                             seed=23)
+    print(f"case seqs={wl.num_seqs}", flush=True)
+    assert_close(run_cascade(wl, pg, pb), O.run_workload(wl, precision="mt"), wl.kv_dtype,
+                 "cascade, empty suffixes")
