@@ -228,3 +228,16 @@ def test_cascade_every_suffix_empty(cuda):
     print(f"case seqs={wl.num_seqs}", flush=True)
     assert_close(run_cascade(wl, pg, pb), O.run_workload(wl, precision="mt"), wl.kv_dtype,
                  "cascade, empty suffixes")
+
+
+@pytest.mark.parametrize("bs,dtype", [(32, "fp16"), (64, "bf16"), (8, "fp16")])
+def test_cascade_block_sizes(cuda, bs, dtype):
+    """Pages of 32 and 64 tokens (two and four 16-token tiles a page, on the
+    MFMA path with the in-kernel plan) and of 8 (the VALU tile path, two
+    passes with the prefix fold)."""
+    spec = [(3, [5, 0, 40]), (1, [bs] * 9), (6, [1, 2])]
+    wl, pg, pb = shared_case(spec, singles=[1, 0, 3 * bs + 5], H=32, KVH=8, D=128, bs=bs,
+                             kv_dtype=DT[dtype], seed=50 + bs)
+    print(f"case block_size {bs} {dtype}", flush=True)
+    assert_close(run_cascade(wl, pg, pb), O.run_workload(wl, precision="mt"), wl.kv_dtype,
+                 f"cascade bs={bs}")
