@@ -572,6 +572,7 @@ int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<st
                  o_lens = st->pack(st->h_lens), o_group = st->pack(st->h_group),
                  o_pblocks = st->pack(st->h_pblocks), o_qptr = st->pack(st->h_qptr),
                  o_optr = st->pack(st->h_optr);
+    tr.mark("pack");
     // The rows of requests admitted or extended before a failure are still
     // written: the index already holds their tokens.
     bool staged = false;
