@@ -177,6 +177,41 @@ def test_auto_split_many_short_segments(cuda, dtype):
     assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"auto split {dtype}")
 
 
+@pytest.mark.parametrize("case", [
+    # (H, KVH, D, dtype, tile tokens): fp32 at 64 / 128 / 256 dims (16, 8
+    # and 4 tokens per tile), bf16 at head_size 80 (16); groups of 1 and 2
+    ("mha64", 12, 12, 64, "fp32", 16),
+    ("gqa2-128", 8, 4, 128, "fp32", 8),
+    ("mha256", 2, 2, 256, "fp32", 4),
+    ("gqa2-80", 4, 2, 80, "bf16", 16),
+])
+def test_segment_launch_limits(cuda, case):
+    """Small VALU batches run one 16-wavefront workgroup per segment (no
+    merge) when every segment fits its 4 rounds of 2 tiles per wavefront,
+    i.e. block tables of at most 128 tiles: lengths 0, 1, a tile and one
+    token either side, and a sequence filling all 128 tiles; then one more
+    token, which widens the table past 128 tiles and puts the batch on the
+    stream-K plan; and the same lengths over batches of 252-256 segments
+    (one round of workgroups, one per CU of the MI355X's 256) and of 264-272
+    (stream-K)."""
+    name, H, KVH, D, dtype, tt = case
+    cap = 128 * tt
+    base = [0, 1, tt - 1, tt, tt + 1, cap - 1, cap // 2, 3]
+    for lens in (base[:-1] + [cap], base[:-1] + [cap + 1]):
+        wl = W.small_case(num_seqs=len(lens), H=H, KVH=KVH, D=D, kv_dtype=DT[dtype],
+                          seed=D + H, lens=lens)
+        print(f"case {name} lens={lens}", flush=True)
+        assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"{name} lens {lens}")
+    for segs in (256, 272):
+        nseq = segs // KVH
+        lens = (base * (nseq // len(base) + 1))[:nseq]
+        lens[-1] = cap
+        wl = W.small_case(num_seqs=nseq, H=H, KVH=KVH, D=D, kv_dtype=DT[dtype],
+                          seed=D + segs, lens=lens)
+        print(f"case {name} segments={segs}", flush=True)
+        assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"{name} segments {segs}")
+
+
 def test_back_to_back_launches_share_a_workspace(cuda):
     """Launches of different shapes on one stream share one split-K
     workspace (grown when a shape needs more): each launch's partials and

@@ -412,6 +412,18 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
                                   partition_tokens, waves);
         }
 
+        // Small batches on the VALU tile path: one workgroup per segment
+        // (paged_decode_segment_kernel) when the segments fit one round of
+        // workgroups, one per CU, and every segment fits the workgroup's
+        // rounds of tiles; no split-K workspace and no merge.  (Each load of
+        // a tile must lie in one page: block_size >= its rows.)
+        const bool seg_launch =
+            !mfma && partition_tokens == 0 && !po && !fold &&
+            tiling.head_tile <= xhip::kSegMaxHeadTile && block_size >= tile / xhip::kLoadsPerTile &&
+            (long long)nseq * segs <= cus &&
+            (max_ctx + tile - 1) / tile <=
+                (long long)xhip::kSegWaves * xhip::kSegTiles * xhip::kSegRounds;
+
         const size_t eb_total = (size_t)elem_bytes(kv_dtype);
         // workspace: fp32 partials o, their (m, l), the unit prefix
         const size_t pre_bytes = (size_t)(nseq + 1) * sizeof(int);
@@ -422,7 +434,7 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         auto ml_size = [&](long long w) {
             return ((size_t)w * 2 * tiling.head_tile * 2 * sizeof(float) + 255) & ~(size_t)255;
         };
-        if (fixed && o_size(waves) + ml_size(waves) + pre_bytes > fixed->bytes)
+        if (fixed && !seg_launch && o_size(waves) + ml_size(waves) + pre_bytes > fixed->bytes)
             return set_status(NXT_ATTN_E_UNSUPPORTED,
                               "this plan needs %zu bytes of split-K scratch; the allocation-free "
                               "entry point has %zu%s",
@@ -432,7 +444,9 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         const size_t ml_bytes = ml_size(waves);
         WsCache::Lease lease;  // held until this chunk's launches are enqueued
         void *ws = nullptr;
-        if (fixed) {
+        if (seg_launch) {
+            // (no workspace)
+        } else if (fixed) {
             ws = fixed->ptr;  // launches of one stream run in order: chunks reuse it
         } else {
             int st = get_workspace(device, stream, o_bytes + ml_bytes + pre_bytes, &lease);
@@ -463,9 +477,10 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
                    block_tables + (size_t)s0 * max_num_blocks_per_seq, seq_lens + s0, nseq,
                    num_heads, num_kv_heads, tiling.head_tiles, max_num_blocks_per_seq, block_size,
                    kv_block_stride, kv_head_stride, scale);
-        p.ws_o = (float *)ws;
-        p.ws_ml = (float *)((char *)ws + o_bytes);
-        p.ws_prefix = (int *)((char *)ws + o_bytes + ml_bytes);
+        p.ws_o = ws ? (float *)ws : nullptr;
+        p.ws_ml = ws ? (float *)((char *)ws + o_bytes) : nullptr;
+        p.ws_prefix = ws ? (int *)((char *)ws + o_bytes + ml_bytes) : nullptr;
+        p.segment_launch = seg_launch ? 1 : 0;
         p.num_waves = (int)waves;
         p.min_tiles_per_wave = min_tpw;
         p.seg_cost = seg_cost;

@@ -126,6 +126,17 @@ static hipError_t launch_for_head_size(const DecodeParams &p, int head_tile, boo
         }
         return hipErrorInvalidValue;
     }
+    if (p.segment_launch) {
+        // one workgroup per segment, no merge
+        const unsigned sgrid = (unsigned)(p.num_seqs * p.num_kv_heads * p.head_tiles);
+        if (head_tile == 1)
+            return launch_partition(paged_decode_segment_kernel<KV, D, 1>, sgrid,
+                                    64 * kSegWaves, 0, st, ev_start, ev_stop, p);
+        if (head_tile == 2)
+            return launch_partition(paged_decode_segment_kernel<KV, D, 2>, sgrid,
+                                    64 * kSegWaves, 0, st, ev_start, ev_stop, p);
+        return hipErrorInvalidValue;
+    }
     switch (head_tile) {
     case 1: {
         const hipError_t e = launch_partition(paged_decode_partition_kernel<KV, D, 1>, grid,

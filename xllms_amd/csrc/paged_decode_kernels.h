@@ -229,55 +229,69 @@ template <int KV, int D, int GT> struct ItemState {
     float o[GT][VEC];
 };
 
-// One tile: kLoadsPerTile loads of TPL rows each.  UNI: the TPL rows of every
-// load sit in one page (block_size >= TPL), whose id blk[k] was read with a
-// scalar load.  MASK: some token of the tile is past t_end or in a page with a
-// negative id; such tokens are neither loaded nor counted.
-template <int KV, int D, int GT, bool UNI, bool MASK>
-__device__ __forceinline__ void decode_tile(const DecodeParams &p, const int *bt, const char *kb,
-                                            const char *vb, int t0, int t_end, int row, int col,
-                                            bool col_ok, const int (&blk)[kLoadsPerTile],
-                                            ItemState<KV, D, GT> &st) {
+// One tile's K and V registers, loaded and not yet used, and which of its
+// kLoadsPerTile row groups hold tokens.
+struct TileRegs {
+    u32x4 k[kLoadsPerTile], v[kLoadsPerTile];
+    bool tv[kLoadsPerTile];
+};
+
+// Issue one tile's loads: kLoadsPerTile loads of TPL rows each.  UNI: the TPL
+// rows of every load sit in one page (block_size >= TPL), whose id blk[k] was
+// read with a scalar load.  MASK: some token of the tile is past t_end or in a
+// page with a negative id; such tokens are neither loaded nor counted.
+template <int KV, int D, bool UNI, bool MASK>
+__device__ __forceinline__ void tile_load(const DecodeParams &p, const int *bt, const char *kb,
+                                          const char *vb, int t0, int t_end, int row, int col,
+                                          bool col_ok, const int (&blk)[kLoadsPerTile],
+                                          TileRegs &r) {
     using Geo = Geometry<KV, D>;
     constexpr int VEC = Geo::kVec;
     constexpr int EB = Geo::kElemBytes;
-    constexpr int RL = Geo::kRowLanes;
     constexpr int TPL = Geo::kRows;
     constexpr int LPT = kLoadsPerTile;
     const int bmask = p.block_size - 1;
 
-    u32x4 kr[LPT], vr[LPT];
-    bool tv[LPT];
     long long eoff[LPT];
 #pragma unroll
     for (int k = 0; k < LPT; k++) {
         const int tok = t0 + k * TPL + row;
         if constexpr (UNI) {
             const int tk0 = t0 + k * TPL;
-            tv[k] = !MASK || (tok < t_end && blk[k] >= 0);
+            r.tv[k] = !MASK || (tok < t_end && blk[k] >= 0);
             eoff[k] = (long long)blk[k] * p.kv_block_stride +
                       (long long)((((tk0 & bmask) + row) * D) + col * VEC);
         } else {
             const int bi = (tok < t_end ? tok : t_end - 1) >> p.bs_shift;
             const int b = bt[bi];
-            tv[k] = tok < t_end && b >= 0;
+            r.tv[k] = tok < t_end && b >= 0;
             eoff[k] = (long long)b * p.kv_block_stride + (long long)(((tok & bmask) * D) + col * VEC);
         }
     }
 #pragma unroll
     for (int k = 0; k < LPT; k++) {
-        if ((!MASK || tv[k]) && col_ok)
-            kr[k] = stream_load16(kb + eoff[k] * EB);
+        if ((!MASK || r.tv[k]) && col_ok)
+            r.k[k] = stream_load16(kb + eoff[k] * EB);
         else
-            kr[k] = u32x4{0, 0, 0, 0};
+            r.k[k] = u32x4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int k = 0; k < LPT; k++) {
-        if ((!MASK || tv[k]) && col_ok)
-            vr[k] = stream_load16(vb + eoff[k] * EB);
+        if ((!MASK || r.tv[k]) && col_ok)
+            r.v[k] = stream_load16(vb + eoff[k] * EB);
         else
-            vr[k] = u32x4{0, 0, 0, 0};
+            r.v[k] = u32x4{0, 0, 0, 0};
     }
+}
+
+// Fold one loaded tile into the row's state: scores, online softmax, o += P V.
+template <int KV, int D, int GT, bool MASK>
+__device__ __forceinline__ void tile_compute(const DecodeParams &p, const TileRegs &r,
+                                             ItemState<KV, D, GT> &st) {
+    using Geo = Geometry<KV, D>;
+    constexpr int VEC = Geo::kVec;
+    constexpr int RL = Geo::kRowLanes;
+    constexpr int LPT = kLoadsPerTile;
 
     // Scores, log2 units: per-lane partial dots, then one interleaved row
     // reduction over all LPT*GT of them.
@@ -286,7 +300,7 @@ __device__ __forceinline__ void decode_tile(const DecodeParams &p, const int *bt
 #pragma unroll
     for (int k = 0; k < LPT; k++) {
 #pragma unroll
-        for (int g = 0; g < GT; g++) part[k * GT + g] = chunk_dot<KV>(kr[k], st.q[g], 0.0f);
+        for (int g = 0; g < GT; g++) part[k * GT + g] = chunk_dot<KV>(r.k[k], st.q[g], 0.0f);
     }
     row_sum_n<RL, LPT * GT>(part);
 #pragma unroll
@@ -294,7 +308,7 @@ __device__ __forceinline__ void decode_tile(const DecodeParams &p, const int *bt
 #pragma unroll
         for (int g = 0; g < GT; g++) {
             const float acc = part[k * GT + g] * p.scale_log2;
-            s[k][g] = (MASK && !tv[k]) ? -INFINITY : acc;
+            s[k][g] = (MASK && !r.tv[k]) ? -INFINITY : acc;
         }
     }
 
@@ -323,13 +337,24 @@ __device__ __forceinline__ void decode_tile(const DecodeParams &p, const int *bt
 #pragma unroll
     for (int k = 0; k < LPT; k++) {
         float vf[VEC];
-        chunk_to_float<KV, VEC>(vr[k], vf);
+        chunk_to_float<KV, VEC>(r.v[k], vf);
 #pragma unroll
         for (int g = 0; g < GT; g++) {
 #pragma unroll
             for (int e = 0; e < VEC; e++) st.o[g][e] = fmaf(s[k][g], vf[e], st.o[g][e]);
         }
     }
+}
+
+// One tile, loaded and folded in.
+template <int KV, int D, int GT, bool UNI, bool MASK>
+__device__ __forceinline__ void decode_tile(const DecodeParams &p, const int *bt, const char *kb,
+                                            const char *vb, int t0, int t_end, int row, int col,
+                                            bool col_ok, const int (&blk)[kLoadsPerTile],
+                                            ItemState<KV, D, GT> &st) {
+    TileRegs r;
+    tile_load<KV, D, UNI, MASK>(p, bt, kb, vb, t0, t_end, row, col, col_ok, blk, r);
+    tile_compute<KV, D, GT, MASK>(p, r, st);
 }
 
 // Block ids of the kLoadsPerTile loads of the tile at t0 (UNI geometry):
@@ -671,6 +696,133 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
             }
         }
     });
+}
+
+// Small batches on the VALU tile path (DecodeParams::segment_launch): one
+// workgroup of kSegWaves wavefronts per segment (sequence, kv head, head
+// tile), so no segment is cut between workgroups and there is no merge
+// launch.  Wavefront w takes the segment's tiles w, w + kSegWaves, ...,
+// kSegTiles of them in flight at a time; the sequence length, the query rows
+// and the first tiles' block ids are requested together, the block ids
+// without waiting for the length (entries past the sequence are read, within
+// the table row, but their tokens are masked).  The wavefronts' states are
+// combined through LDS and the workgroup writes the output rows.
+template <int KV, int D, int GT>
+__global__ __launch_bounds__(64 * kSegWaves) void paged_decode_segment_kernel(
+    const DecodeParams p) {
+    using Geo = Geometry<KV, D>;
+    constexpr int VEC = Geo::kVec;
+    constexpr int EB = Geo::kElemBytes;
+    constexpr int NCH = Geo::kChunks;
+    constexpr int RL = Geo::kRowLanes;
+    constexpr int TT = Geo::kTileTokens;
+    constexpr int TPL = Geo::kRows;
+    constexpr int LPT = kLoadsPerTile;
+    __shared__ float s_o[kSegWaves][GT][D];
+    __shared__ float s_m[kSegWaves][GT], s_l[kSegWaves][GT];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane % RL;
+    const int row = lane / RL;
+    const bool col_ok = (NCH == RL) || (col < NCH);
+    const int segs = p.num_kv_heads * p.head_tiles;
+    const int s = blockIdx.x / segs;
+    const int seg = blockIdx.x - s * segs;
+    const int kvh = seg / p.head_tiles;
+    const int ht = seg - kvh * p.head_tiles;
+    const int g0 = ht * GT;
+    const int nh = min(GT, p.group - g0);
+    const int *bt = p.block_tables + (size_t)s * p.max_blocks;
+    const char *kb = (const char *)p.k + (size_t)kvh * (size_t)p.kv_head_stride * EB;
+    const char *vb = (const char *)p.v + (size_t)kvh * (size_t)p.kv_head_stride * EB;
+
+    const int L = seq_len_of(p, s);
+    ItemState<KV, D, GT> st;
+#pragma unroll
+    for (int h = 0; h < GT; h++) {
+        st.q[h] = (h < nh && col_ok)
+                      ? load16(q_row(p, s, kvh * p.group + g0 + h, D, EB) + col * VEC * EB)
+                      : u32x4{0, 0, 0, 0};
+        st.m[h] = -INFINITY;
+        st.l[h] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < VEC; e++) st.o[h][e] = 0.0f;
+    }
+    int nxt[kSegTiles][LPT];
+#pragma unroll
+    for (int j = 0; j < kSegTiles; j++)
+        tile_blocks<TPL>(bt, (wave + kSegWaves * j) * TT, p.max_ctx, p.bs_shift, nxt[j]);
+    const int Ts = (L + TT - 1) / TT;
+    for (int r = 0; r < kSegRounds; r++) {
+        const int tb = wave + kSegWaves * kSegTiles * r;  // this wavefront's first tile of the round
+        if (tb >= Ts) break;
+        TileRegs regs[kSegTiles];
+#pragma unroll
+        for (int j = 0; j < kSegTiles; j++) {
+            int blk[LPT];
+#pragma unroll
+            for (int k = 0; k < LPT; k++) blk[k] = __builtin_amdgcn_readfirstlane(nxt[j][k]);
+            tile_load<KV, D, true, true>(p, bt, kb, vb, (tb + kSegWaves * j) * TT, L, row, col,
+                                         col_ok, blk, regs[j]);
+        }
+        if (r + 1 < kSegRounds) {
+#pragma unroll
+            for (int j = 0; j < kSegTiles; j++)
+                tile_blocks<TPL>(bt, (tb + kSegWaves * (kSegTiles + j)) * TT, p.max_ctx,
+                                 p.bs_shift, nxt[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < kSegTiles; j++) tile_compute<KV, D, GT, true>(p, regs[j], st);
+    }
+
+    // This wavefront's state: its rows merged (lane bits >= log2 RL), then
+    // through LDS to the workgroup's combine.
+#pragma unroll
+    for (int off = RL; off < 64; off <<= 1) {
+#pragma unroll
+        for (int h = 0; h < GT; h++) {
+            const float mo = __shfl_xor(st.m[h], off);
+            const float lo2 = __shfl_xor(st.l[h], off);
+            const float M = fmaxf(st.m[h], mo);
+            const float Ms = (M == -INFINITY) ? 0.0f : M;
+            const float a = fast_exp2(st.m[h] - Ms);
+            const float b = fast_exp2(mo - Ms);
+            st.l[h] = st.l[h] * a + lo2 * b;
+            st.m[h] = M;
+#pragma unroll
+            for (int e = 0; e < VEC; e++)
+                st.o[h][e] = st.o[h][e] * a + __shfl_xor(st.o[h][e], off) * b;
+        }
+    }
+    if (row == 0 && col_ok) {
+#pragma unroll
+        for (int h = 0; h < GT; h++) {
+#pragma unroll
+            for (int e = 0; e < VEC; e++) s_o[wave][h][col * VEC + e] = st.o[h][e];
+            if (col == 0) {
+                s_m[wave][h] = st.m[h];
+                s_l[wave][h] = st.l[h];
+            }
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < nh * D; i += 64 * kSegWaves) {
+        const int h = i / D, d = i - h * D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kSegWaves; w++) M = fmaxf(M, s_m[w][h]);
+        const float Ms = (M == -INFINITY) ? 0.0f : M;
+        float l = 0.0f, o = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kSegWaves; w++) {
+            const float a = fast_exp2(s_m[w][h] - Ms);
+            l += s_l[w][h] * a;
+            o += s_o[w][h][d] * a;
+        }
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        store_elem<KV>(o_row(p, s, kvh * p.group + g0 + h, D, EB), d, o * inv);
+    }
 }
 
 // The slots of a cut segment's partials: partial 0 in slot s0, partial

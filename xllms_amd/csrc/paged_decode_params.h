@@ -37,6 +37,16 @@ constexpr int kMergeCols = 32;       // float4 columns per workgroup of the chun
 constexpr int kLoadsPerTile = 4;     // 16-byte K (and V) loads per lane per tile
 constexpr int kMaxSeqsPerLaunch = 8192;  // the per-workgroup prefix scan lives in LDS
 
+// Small batches on the VALU tile path (DecodeParams::segment_launch): one
+// workgroup of kSegWaves wavefronts per segment, each wavefront with
+// kSegTiles tiles in flight, at most kSegRounds rounds of them (so segments
+// of at most kSegWaves * kSegTiles * kSegRounds tiles), head tiles of at most
+// kSegMaxHeadTile heads.
+constexpr int kSegWaves = 16;
+constexpr int kSegTiles = 2;
+constexpr int kSegRounds = 4;
+constexpr int kSegMaxHeadTile = 2;
+
 // Workgroup-level combine of cut segments (MFMA tile path, head_size <=
 // 128): the kMfmaWavesPerGroup wavefronts of a workgroup own consecutive
 // stream-K ranges, so the pieces of one segment that fall in one workgroup
@@ -83,6 +93,10 @@ struct DecodeParams {
     int seg_cost;              // split units a segment costs on top of its tiles
     float scale_log2;          // scale * log2(e)
     int merge_per_segment;     // 1: merge with one workgroup per segment
+    int segment_launch;        // 1 (VALU tile path, automatic plan, whole outputs): one
+                               // workgroup per segment and no merge
+                               // (paged_decode_segment_kernel); num_waves and the
+                               // split-K workspace are unused
     int pair_tiles;            // 1 (MFMA path, head_tiles == 2, wg_fix == 0): paired head
                                // tiles.  A segment is (sequence, kv head); the two
                                // wavefronts 2k, 2k + 1 of the launch walk the same stream-K
