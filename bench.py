@@ -203,10 +203,27 @@ def device_copy_peak(mib: int = 1024, steps: int = 10) -> dict:
 def partition_kernel_name(wl) -> str:
     """Kernel that streams K/V for this workload: the MFMA tile kernel serves
     fp16/bf16 pages with head_size % 32 == 0 and block_size >= 16, the VALU
-    tile kernel everything else (same rule as use_mfma in paged_decode_api.cpp)."""
+    tile kernel everything else (same rule as use_mfma in paged_decode_api.cpp);
+    on the VALU path, batches of at most one segment per CU with groups of
+    at most 2 heads and tables of at most 128 tiles run one workgroup per
+    segment (the seg_launch rule in paged_decode_api.cpp)."""
+    import torch
     from xllms_amd import workloads as W
     mfma = wl.kv_dtype != W.FP32 and wl.head_size % 32 == 0 and wl.block_size >= 16
-    return "paged_decode_partition_mfma_kernel" if mfma else "paged_decode_partition_kernel"
+    if mfma:
+        return "paged_decode_partition_mfma_kernel"
+    group = wl.num_heads // wl.num_kv_heads
+    lanes = 1
+    while lanes < wl.head_size * wl.elem_bytes // 16:
+        lanes *= 2
+    rows = 64 // lanes  # tile rows per 16-byte load
+    tile = 4 * rows
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    max_ctx = wl.max_num_blocks_per_seq * wl.block_size
+    if (group <= 2 and wl.block_size >= rows and wl.num_seqs * wl.num_kv_heads <= cus and
+            -(-max_ctx // tile) <= 128):
+        return "paged_decode_segment_kernel"
+    return "paged_decode_partition_kernel"
 
 
 def cpu_baseline(wl, budget_s: float) -> dict:

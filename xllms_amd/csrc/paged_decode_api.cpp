@@ -721,6 +721,15 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
         ps.ws_o = (float *)(w + o_yo);
         ps.ws_ml = (float *)(w + o_ym);
         ps.ws_prefix = (int *)(w + o_yp);
+        if (kv_dtype == NXT_KV_FP16) {
+            // fp16 states, in the same (fp32-sized) buffers
+            for (DecodeParams *q : {&pp, &ps}) {
+                q->out_h = q->out_f32;
+                q->ws_h = q->ws_o;
+                q->out_f32 = nullptr;
+                q->ws_o = nullptr;
+            }
+        }
         const int rs = stile.head_tile / xhip::kMfmaHeads;
         const xhip::CascadeInPlan ip{seq_lens, block_tables, prefix_group, prefix_blocks,
                                      max_groups};

@@ -24,10 +24,14 @@
 // Run as two launches, the prefix batch (a few thousand short ranges) spent
 // ~30 us mostly in latency while the device's bandwidth went unused; here
 // its ranges stream beside the suffix batch's.  Both bodies run in
-// partial-output mode: finished segments leave fp32 rows and their
-// log-sum-exp, cut segments their partials, and the suffix batch no longer
-// starts from the prefix result (that would make it wait for the prefix
-// batch).
+// partial-output mode: finished segments leave rows and their log-sum-exp,
+// cut segments their partials, and the suffix batch no longer starts from
+// the prefix result (that would make it wait for the prefix batch).  Over
+// fp16 K/V these states are fp16 (DecodeParams::out_h, ws_h): at config 5
+// the fp32 states were 15.4 MB written and 14.8 MB read back, and the step
+// took 7 us longer (MI355X).  Over bf16 they stay fp32: a bf16 state keeps 8
+// significant bits, too few where a prefix row and a suffix row of opposite
+// sign nearly cancel.
 //
 // Merge.  One workgroup per suffix segment (sequence, kv head, head tile);
 // for every float4 column of its rows the suffix state (finished row, or the
@@ -109,9 +113,11 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, 2) void paged_decode_casca
     // slower.)
     const int l = xcd_local_block(blockIdx.x, G);
     if (l < gp)
-        mfma_partition_body<KV, D, 2, true>(pp, plens, ptables, pre_p, l, gp * NW, sm.a);
+        mfma_partition_body<KV, D, 2, true, kSrcBatch, KV == KV_F16>(pp, plens, ptables, pre_p, l,
+                                                                      gp * NW, sm.a);
     else
-        mfma_partition_body<KV, D, RS>(ps, slens, stables, pre_s, l - gp, (G - gp) * NW, sm.b);
+        mfma_partition_body<KV, D, RS, false, kSrcBatch, KV == KV_F16>(
+            ps, slens, stables, pre_s, l - gp, (G - gp) * NW, sm.b);
 }
 
 // In-kernel plan.  With at most kInPlanGroupsMax groups, every workgroup of
@@ -281,11 +287,11 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, 2) void paged_decode_casca
     const CascadeLdsPlan cp{slen,  soff,       vlen, vrow, vdesc,         grp,  &s_win[0][0],
                             p_row, (const char *)ps.q, ps.q_rows, ps.num_heads, G, rows, B};
     if (l < gp)
-        mfma_partition_body<KV, D, 2, true, kSrcPrefix>(pp, nullptr, tables, pre_p, l, gp * NW,
-                                                        sm.a, &cp);
+        mfma_partition_body<KV, D, 2, true, kSrcPrefix, KV == KV_F16>(
+            pp, nullptr, tables, pre_p, l, gp * NW, sm.a, &cp);
     else
-        mfma_partition_body<KV, D, RS, false, kSrcSuffix>(ps, nullptr, tables, pre_s, l - gp,
-                                                          (Gw - gp) * NW, sm.b, &cp);
+        mfma_partition_body<KV, D, RS, false, kSrcSuffix, KV == KV_F16>(
+            ps, nullptr, tables, pre_s, l - gp, (Gw - gp) * NW, sm.b, &cp);
 }
 
 // (m, l, acc) <- (m, l, acc) (+) a finished row: the state (lse, 1, row).
@@ -304,8 +310,8 @@ __device__ __forceinline__ void absorb_row(float lse, const f32x4 &row, float &m
 // segment's index within its sequence, hrow the column's head in the
 // segment's tile (GT heads), c the float4 column in the head; pair_ht >= 0:
 // p's head tiles are paired (DecodeParams::pair_tiles) and the column is in
-// head tile pair_ht.
-template <int GT, int D>
+// head tile pair_ht.  HS: the states are fp16 (DecodeParams::out_h, ws_h).
+template <int GT, int D, bool HS>
 __device__ __forceinline__ void segment_state(const DecodeParams &p, int s, int L, int seg,
                                               int pre_s, int total, int waves, size_t row, int hrow,
                                               int c, float &m, float &l, f32x4 &acc,
@@ -322,10 +328,11 @@ __device__ __forceinline__ void segment_state(const DecodeParams &p, int s, int 
                   p, seg_start, seg_start + p.seg_cost, Ts,
                   tiles_per_wave(total, waves, p.min_tiles_per_wave), ps);
     if (cut) {
-        merge_partials<GT, D, 8>(p, ps, 0, 1, hrow * 2, hrow * D + c * 4, m, l, acc);
+        merge_partials<GT, D, 8, HS>(p, ps, 0, 1, hrow * 2, hrow * D + c * 4, m, l, acc);
     } else {
         const float lse = p.out_lse[row];
-        const f32x4 o = *(const f32x4 *)(p.out_f32 + row * D + c * 4);
+        const f32x4 o = HS ? unpack_h4(*(const u32x2 *)((const char *)p.out_h + (row * D + c * 4) * 2))
+                           : *(const f32x4 *)(p.out_f32 + row * D + c * 4);
         absorb_row(lse, o, m, l, acc);
     }
 }
@@ -342,6 +349,7 @@ __global__ __launch_bounds__(NT) void paged_decode_cascade_merge_kernel(
     constexpr int C4 = D / 4;
     constexpr int NW = kMfmaWavesPerGroup;
     constexpr int GTP = 2 * kMfmaHeads;
+    constexpr bool HS = KV == KV_F16;  // fp16 states (set by the host for fp16 K/V)
     // The prefix batch's lengths and unit prefixes, loaded with the first
     // round trip (a prefix batch of up to kCascadeMergeLdsSeqs sequences), so
     // finding a column's prefix segment takes no round trip of its own.
@@ -376,8 +384,8 @@ __global__ __launch_bounds__(NT) void paged_decode_cascade_merge_kernel(
         float m = -INFINITY, l = 0.0f;
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
         if (Ls > 0)
-            segment_state<GTS, D>(ps, s, Ls, seg, pre_s, tot_s, (G - gp) * NW, srow0 + h, h, c, m,
-                                  l, acc);
+            segment_state<GTS, D, HS>(ps, s, Ls, seg, pre_s, tot_s, (G - gp) * NW, srow0 + h, h,
+                                      c, m, l, acc);
         if (fb >= 0) {
             const int q = fb + g0 + h;
             const int v = q / rows, j = q - v * rows;
@@ -385,8 +393,8 @@ __global__ __launch_bounds__(NT) void paged_decode_cascade_merge_kernel(
             if (Lv > 0) {
                 const int htp = j / GTP;
                 const size_t prow = (size_t)v * pp.num_heads + (size_t)kvh * rows + j;
-                segment_state<GTP, D>(pp, v, Lv, kvh, v_lds ? l_vpre[v] : pp.ws_prefix[v], tot_p,
-                                      gp * NW, prow, j - htp * GTP, c, m, l, acc, htp);
+                segment_state<GTP, D, HS>(pp, v, Lv, kvh, v_lds ? l_vpre[v] : pp.ws_prefix[v],
+                                          tot_p, gp * NW, prow, j - htp * GTP, c, m, l, acc, htp);
             }
         }
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
@@ -402,6 +410,11 @@ static hipError_t launch_cascade_attn_rs(const DecodeParams &pp, const DecodePar
                                          hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
     const unsigned grid = (unsigned)(ps.num_waves / kMfmaWavesPerGroup);
     const dim3 block(64 * kMfmaWavesPerGroup);
+    // the merge reads fp16 states exactly when the K/V are fp16
+    const bool hs = KV == KV_F16;
+    if ((pp.out_h != nullptr) != hs || (ps.out_h != nullptr) != hs || (pp.ws_h != nullptr) != hs ||
+        (ps.ws_h != nullptr) != hs)
+        return hipErrorInvalidValue;
     if (ip) {
         const size_t lds =
             (size_t)inplan_lds_ints(ps.num_seqs, pp.num_seqs, ip->num_groups) * sizeof(int);

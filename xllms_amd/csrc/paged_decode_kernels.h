@@ -39,6 +39,7 @@
 namespace xhip {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -877,13 +878,28 @@ __device__ __forceinline__ bool segment_partials_paired(int seg_start, int first
     return true;
 }
 
+// Four fp16 values as fp32.
+__device__ __forceinline__ f32x4 unpack_h4(u32x2 h) {
+    const f32x2 a = unpack16<KV_F16>(h.x), b = unpack16<KV_F16>(h.y);
+    return f32x4{a.x, a.y, b.x, b.y};
+}
+
+// Four consecutive values of a partial's o at float index `at` of the
+// split-K workspace: fp32, or HS: fp16 states (DecodeParams::ws_h).
+template <bool HS>
+__device__ __forceinline__ f32x4 partial_f32x4(const DecodeParams &p, size_t at) {
+    if constexpr (HS) return unpack_h4(*(const u32x2 *)((const char *)p.ws_h + at * 2));
+    else return *(const f32x4 *)(p.ws_o + at);
+}
+
 // Online log-sum-exp merge, into (m, l, acc) of one float4 column, of a
 // segment's partials j = j0, j0 + step, ... < np (slots as in PartialSlots).
 // The partials go in batches of up to NB whose loads are all issued before
 // any is used, so a thread waits for one memory round trip per batch, not
 // per partial; batch slots past np load and combine nothing.  The column's
-// (m, l) and float4 of o sit at off_ml and off_o floats into a slot.
-template <int GT, int D, int NB>
+// (m, l) and float4 of o sit at off_ml and off_o floats into a slot.  HS:
+// fp16 states (DecodeParams::ws_h), whose o is read at the same index.
+template <int GT, int D, int NB, bool HS = false>
 __device__ __forceinline__ void merge_partials(const DecodeParams &p, const PartialSlots &ps,
                                                int j0, int step, int off_ml, int off_o,
                                                float &m, float &l, f32x4 &acc) {
@@ -891,15 +907,20 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p, const Part
     for (int jb = j0; jb < np; jb += NB * step) {
         f32x2 mlv[NB];
         f32x4 ov[NB];
+        u32x2 hv[NB];
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             const int j = jb + b * step;
             mlv[b] = f32x2{-INFINITY, 0.0f};  // (defined values for the slots left unread)
             ov[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            hv[b] = u32x2{0u, 0u};
             if (j < np) {
                 const size_t slot = j == 0 ? ps.s0 : ps.sb + (size_t)ps.sstride * j;
                 mlv[b] = *(const f32x2 *)(p.ws_ml + slot * GT * 2 + off_ml);
-                ov[b] = *(const f32x4 *)(p.ws_o + slot * GT * D + off_o);
+                if constexpr (HS)
+                    hv[b] = *(const u32x2 *)((const char *)p.ws_h + (slot * GT * D + off_o) * 2);
+                else
+                    ov[b] = *(const f32x4 *)(p.ws_o + slot * GT * D + off_o);
             }
         }
         // keep the scheduler from starting the combine (and waiting on the
@@ -908,6 +929,7 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p, const Part
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             if (jb + b * step >= np) break;
+            if constexpr (HS) ov[b] = unpack_h4(hv[b]);
             const float mj = mlv[b].x;
             const float M = fmaxf(m, mj);
             const float Ms = (M == -INFINITY) ? 0.0f : M;

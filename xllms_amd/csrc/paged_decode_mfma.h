@@ -36,7 +36,6 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr uint32_t kOobOffset = 0x80000000u;
 
@@ -466,7 +465,7 @@ namespace xhip {
 // Where a finished segment's rows go: its output rows (element type), or in
 // partial-output mode its fp32 rows and log-sum-exp.  st holds unreduced
 // per-lane sums (lane group g of head j); they are reduced here.
-template <int KV, int D, int R>
+template <int KV, int D, int R, bool HS = false>
 __device__ __forceinline__ void mfma_write_rows(const DecodeParams &p, const MfmaPiece &pc,
                                                 int lane, const MfmaState<D> (&st)[R]) {
     using G = MfmaGeometry<D>;
@@ -483,7 +482,16 @@ __device__ __forceinline__ void mfma_write_rows(const DecodeParams &p, const Mfm
         const int hj = 16 * b + j;  // head of this lane in the tile
         if (hj >= nh) continue;
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        if (p.out_f32) {
+        if constexpr (HS) {
+            char *dst = (char *)p.out_h + (qrow0 + (size_t)hj * D + 4 * gq) * 2;
+#pragma unroll
+            for (int n = 0; n < G::kDimBlocks; n++) {
+                const f32x4 o = st[b].o[n] * inv;
+                *(u32x2 *)(dst + 32 * n) =
+                    u32x2{pack16<KV_F16>(o[0], o[1]), pack16<KV_F16>(o[2], o[3])};
+            }
+            if (gq == 0) p.out_lse[qrow0 / D + hj] = l > 0.0f ? st[b].m + log2f(l) : -INFINITY;
+        } else if (p.out_f32) {
             float *dst = p.out_f32 + qrow0 + (size_t)hj * D + 4 * gq;
 #pragma unroll
             for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st[b].o[n] * inv;
@@ -499,9 +507,10 @@ __device__ __forceinline__ void mfma_write_rows(const DecodeParams &p, const Mfm
     }
 }
 
-// The fp32 partial (m, l, unnormalized o) of a cut segment's piece, in the
-// piece's slot of the split-K workspace.
-template <int D, int R>
+// The partial of a cut segment's piece, in the piece's slot of the split-K
+// workspace: fp32 (m, l, unnormalized o), or HS: an fp16 state
+// (DecodeParams::ws_h) (m + log2 l, 1, o / l in fp16).
+template <int D, int R, bool HS = false>
 __device__ __forceinline__ void mfma_write_partial(const DecodeParams &p, const MfmaPiece &pc,
                                                    int lane, const MfmaState<D> (&st)[R]) {
     using G = MfmaGeometry<D>;
@@ -515,6 +524,22 @@ __device__ __forceinline__ void mfma_write_partial(const DecodeParams &p, const 
         l += __shfl_xor(l, 32);
         const int hj = 16 * b + j;
         if (hj >= nh) continue;
+        if constexpr (HS) {
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            char *dst = (char *)p.ws_h + (((size_t)pc.slot * GT + hj) * D + 4 * gq) * 2;
+#pragma unroll
+            for (int n = 0; n < G::kDimBlocks; n++) {
+                const f32x4 o = st[b].o[n] * inv;
+                *(u32x2 *)(dst + 32 * n) =
+                    u32x2{pack16<KV_F16>(o[0], o[1]), pack16<KV_F16>(o[2], o[3])};
+            }
+            if (gq == 0) {
+                p.ws_ml[((size_t)pc.slot * GT + hj) * 2] =
+                    l > 0.0f ? st[b].m + log2f(l) : -INFINITY;
+                p.ws_ml[((size_t)pc.slot * GT + hj) * 2 + 1] = l > 0.0f ? 1.0f : 0.0f;
+            }
+            continue;
+        }
         float *dst = p.ws_o + ((size_t)pc.slot * GT + hj) * D + 4 * gq;
 #pragma unroll
         for (int n = 0; n < G::kDimBlocks; n++) *(f32x4 *)(dst + 16 * n) = st[b].o[n];
@@ -581,10 +606,10 @@ template <int D, int R, int FIX = mfma_wg_fixup(kMfmaHeads * R, D)> struct MfmaL
     MfmaSweepLds<FIX, D, R> sw;
 };
 
-// st <- st (+) the fp32 partial in workspace slot `slot` (its l is the
-// reduced sum: lane group 0 takes it).  Rows past the group were never
-// written; they are left alone.
-template <int D, int R>
+// st <- st (+) the partial in workspace slot `slot` (its l is the reduced
+// sum: lane group 0 takes it; fp32, or HS: an fp16 state).  Rows past the group
+// were never written; they are left alone.
+template <int D, int R, bool HS = false>
 __device__ __forceinline__ void absorb_partial(const DecodeParams &p, int slot, int ht, int lane,
                                                MfmaState<D> (&st)[R]) {
     constexpr int GT = kMfmaHeads * R;
@@ -594,7 +619,7 @@ __device__ __forceinline__ void absorb_partial(const DecodeParams &p, int slot, 
     for (int b = 0; b < R; b++) {
         const int hj = 16 * b + j;
         if (hj >= nh) continue;
-        const float *src = p.ws_o + ((size_t)slot * GT + hj) * D + 4 * gq;
+        const size_t at = ((size_t)slot * GT + hj) * D + 4 * gq;
         const float mo = p.ws_ml[((size_t)slot * GT + hj) * 2];
         const float lo = gq == 0 ? p.ws_ml[((size_t)slot * GT + hj) * 2 + 1] : 0.0f;
         const float M = fmaxf(st[b].m, mo);
@@ -603,7 +628,7 @@ __device__ __forceinline__ void absorb_partial(const DecodeParams &p, int slot, 
         st[b].l = st[b].l * a + lo * w;
 #pragma unroll
         for (int n = 0; n < MfmaGeometry<D>::kDimBlocks; n++)
-            st[b].o[n] = st[b].o[n] * a + *(const f32x4 *)(src + 16 * n) * w;
+            st[b].o[n] = st[b].o[n] * a + partial_f32x4<HS>(p, at + 16 * n) * w;
         st[b].m = M;
     }
 }
@@ -649,8 +674,9 @@ __device__ __forceinline__ void absorb_partial(const DecodeParams &p, int slot, 
 // two ranges, one head tile per wavefront, and every cut piece leaves its
 // own partial (no workgroup combine).  SRC: where the batch's per-sequence
 // data is (kSrcBatch: lens / tables and p; else the in-kernel cascade plan
-// cp).
-template <int KV, int D, int R, bool PAIR = false, int SRC = kSrcBatch>
+// cp).  HS: partial-output rows and partials are fp16 states
+// (DecodeParams::out_h, ws_h).
+template <int KV, int D, int R, bool PAIR = false, int SRC = kSrcBatch, bool HS = false>
 __device__ __forceinline__ void mfma_partition_body(
     const DecodeParams &p, const int *__restrict__ lens, const int *__restrict__ tables,
     const int *pre, int wg, int waves,
@@ -774,7 +800,7 @@ __device__ __forceinline__ void mfma_partition_body(
                 mfma_fold_apply<D, R>(fold, lane, st);
             }
             if (pc.whole) {
-                mfma_write_rows<KV, D, R>(p, pc, lane, st);
+                mfma_write_rows<KV, D, R, HS>(p, pc, lane, st);
             } else if constexpr (FIX == 1) {
                 if (has_next) {
                     // a cut piece with more pieces after it: the wavefront's
@@ -783,18 +809,18 @@ __device__ __forceinline__ void mfma_partition_body(
                         fix_store<D>(sm.sw.fix[wave], lane, st[0]);
                         if (lane == 0) sm.sw.fix[wave].ends = 1;
                     } else {
-                        mfma_write_partial<D, R>(p, pc, lane, st);
+                        mfma_write_partial<D, R, HS>(p, pc, lane, st);
                     }
                 } else {
                     have_last = true;  // the sweep below decides where it goes
                 }
             } else if constexpr (FIX == 2) {
                 if (has_next)
-                    mfma_write_partial<D, R>(p, pc, lane, st);
+                    mfma_write_partial<D, R, HS>(p, pc, lane, st);
                 else
                     have_last = true;
             } else {
-                mfma_write_partial<D, R>(p, pc, lane, st);
+                mfma_write_partial<D, R, HS>(p, pc, lane, st);
             }
             if (!has_next) break;
             pc = pn;
@@ -830,7 +856,7 @@ __device__ __forceinline__ void mfma_partition_body(
                         // the neighbour's first piece, followed by more
                         // pieces, was written as a partial in its slot 0;
                         // it ends the segment in that range
-                        absorb_partial<D, R>(p, (w + 1) * 2, pc.ht, lane, st);
+                        absorb_partial<D, R, HS>(p, (w + 1) * 2, pc.ht, lane, st);
                         ends = true;
                     }
                 }
@@ -847,9 +873,9 @@ __device__ __forceinline__ void mfma_partition_body(
                         sm.sw.relay.ends[i] = ends ? 1 : 0;
                     }
                 } else if (!cut_start && ends) {
-                    mfma_write_rows<KV, D, R>(p, pc, lane, st);
+                    mfma_write_rows<KV, D, R, HS>(p, pc, lane, st);
                 } else {
-                    mfma_write_partial<D, R>(p, pc, lane, st);
+                    mfma_write_partial<D, R, HS>(p, pc, lane, st);
                 }
             }
             __syncthreads();
@@ -874,9 +900,9 @@ __device__ __forceinline__ void mfma_partition_body(
                     fix_store<D>(sm.sw.fix[i], lane, st[0]);
                     if (lane == 0) sm.sw.fix[i].ends = ends ? 1 : 0;
                 } else if (!cut_start && ends) {
-                    mfma_write_rows<KV, D, R>(p, pc, lane, st);
+                    mfma_write_rows<KV, D, R, HS>(p, pc, lane, st);
                 } else {
-                    mfma_write_partial<D, R>(p, pc, lane, st);
+                    mfma_write_partial<D, R, HS>(p, pc, lane, st);
                 }
             }
             __syncthreads();

@@ -115,6 +115,16 @@ struct DecodeParams {
     // out_lse[seq * num_heads + head] (-inf for an empty row); out is unused.
     float *out_f32;
     float *out_lse;
+    // fp16 states (the fused cascade launch over fp16 K/V): the rows of
+    // partial-output mode go to out_h instead of out_f32, and the partials
+    // of cut pieces to ws_h instead of ws_o, both normalized (o / l) in fp16
+    // and indexed like the fp32 buffers; a partial's ws_ml pair is then
+    // (m + log2 l, 1), or (-inf, 0) when empty.  This is the state format of
+    // the reference's partition merge (element-type partial outputs with an
+    // fp32 log-sum-exp, operators/flashinfer_adapter.cu:255-260), at half
+    // the bytes of fp32 states.
+    void *out_h;
+    void *ws_h;
     int cached_seqs;           // sequences [0, cached_seqs) load K/V cacheable (pages read
                                // by several wavefronts close in time); the rest nontemporal
     int skip_empty;            // 1: the rows of empty sequences are left unwritten (their
