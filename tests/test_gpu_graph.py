@@ -82,12 +82,14 @@ def _decode_call(wl, dw, entry):
 
 
 @pytest.mark.parametrize("entry", ["nxt_paged_attention_ex", "nxt_paged_attention_noalloc"])
-@pytest.mark.parametrize("dtype,H,KVH,D", [("fp16", 32, 8, 128), ("bf16", 64, 4, 128),
-                                          ("fp32", 12, 12, 64)])
-def test_decode_replays_in_a_graph(cuda, entry, dtype, H, KVH, D):
+@pytest.mark.parametrize("dtype,H,KVH,D,B", [("fp16", 32, 8, 128, 24), ("bf16", 64, 4, 128, 24),
+                                            ("fp32", 12, 12, 64, 24), ("fp32", 12, 12, 64, 8)])
+def test_decode_replays_in_a_graph(cuda, entry, dtype, H, KVH, D, B):
+    """(The fp32 batch of 8 sequences, 96 segments, runs one workgroup per
+    segment and no merge; the others the stream-K plan and a merge.)"""
     kv = {"fp16": W.FP16, "bf16": W.BF16, "fp32": W.FP32}[dtype]
-    wl = W.small_case(num_seqs=24, H=H, KVH=KVH, D=D, kv_dtype=kv, seed=41 + H, max_len=900)
-    print(f"case {entry} {dtype} H={H} KVH={KVH} D={D}", flush=True)
+    wl = W.small_case(num_seqs=B, H=H, KVH=KVH, D=D, kv_dtype=kv, seed=41 + H, max_len=900)
+    print(f"case {entry} {dtype} H={H} KVH={KVH} D={D} seqs={B}", flush=True)
     dw = W.upload(wl)
     _replays(_decode_call(wl, dw, entry), dw, _new_queries_and_lengths(wl, dw))
 

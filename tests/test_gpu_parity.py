@@ -367,6 +367,22 @@ def test_context_bound_splits_launches(cuda, dtype):
     assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"context bound {dtype}")
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
+def test_many_sequences_split_launches(cuda, dtype):
+    """More sequences than one launch takes (8192: each workgroup scans the
+    batch's split units in LDS): 8192 + 301 short sequences go in two
+    launches, the second of 301 sequences, with empty ones on both sides of
+    the cut."""
+    rng = np.random.default_rng(8493)
+    lens = rng.integers(0, 40, size=8192 + 301)
+    lens[8190:8195] = [0, 33, 0, 1, 17]
+    lens[0] = 39
+    wl = W.small_case(num_seqs=lens.size, H=8, KVH=2, D=64, kv_dtype=DT[dtype], seed=8493,
+                      lens=lens.tolist())
+    print(f"case {dtype} seqs={lens.size}", flush=True)
+    assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"{lens.size} sequences {dtype}")
+
+
 # ---------------------------------------------------- benchmark configs
 def test_config1_full(cuda):
     wl = W.config1()
