@@ -205,8 +205,9 @@ def partition_kernel_name(wl) -> str:
     fp16/bf16 pages with head_size % 32 == 0 and block_size >= 16, the VALU
     tile kernel everything else (same rule as use_mfma in paged_decode_api.cpp);
     on the VALU path, batches of at most one segment per CU with groups of
-    at most 2 heads and tables of at most 128 tiles run one workgroup per
-    segment (the seg_launch rule in paged_decode_api.cpp)."""
+    at most 2 heads run one round of workgroups over the segments, 1, 2 or 4
+    per segment of at most 128 tiles each (the seg_split rule in
+    paged_decode_api.cpp)."""
     import torch
     from xllms_amd import workloads as W
     mfma = wl.kv_dtype != W.FP32 and wl.head_size % 32 == 0 and wl.block_size >= 16
@@ -220,9 +221,14 @@ def partition_kernel_name(wl) -> str:
     tile = 4 * rows
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     max_ctx = wl.max_num_blocks_per_seq * wl.block_size
-    if (group <= 2 and wl.block_size >= rows and wl.num_seqs * wl.num_kv_heads <= cus and
-            -(-max_ctx // tile) <= 128):
-        return "paged_decode_segment_kernel"
+    segs = wl.num_seqs * wl.num_kv_heads
+    if group <= 2 and wl.block_size >= rows and segs <= cus:
+        tiles, seg_bytes, split = -(-max_ctx // tile), max_ctx * wl.head_size * wl.elem_bytes * 2, 1
+        while split < 4 and segs * split * 2 <= cus and (seg_bytes // (split * 2) >= 160 << 10 or
+                                                         tiles > split * 128):
+            split *= 2
+        if tiles <= split * 128:
+            return "paged_decode_segment_kernel"
     return "paged_decode_partition_kernel"
 
 

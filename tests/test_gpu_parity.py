@@ -186,26 +186,27 @@ def test_auto_split_many_short_segments(cuda, dtype):
     ("gqa2-80", 4, 2, 80, "bf16", 16),
 ])
 def test_segment_launch_limits(cuda, case):
-    """Small VALU batches run one 16-wavefront workgroup per segment (no
-    merge) when every segment fits its 4 rounds of 2 tiles per wavefront,
-    i.e. block tables of at most 128 tiles: lengths 0, 1, a tile and one
-    token either side, and a sequence filling all 128 tiles; then one more
-    token, which widens the table past 128 tiles and puts the batch on the
-    stream-K plan; and the same lengths over batches of 252-256 segments
-    (one round of workgroups, one per CU of the MI355X's 256) and of 264-272
-    (stream-K)."""
+    """Small VALU batches (at most one segment per CU) run one round of
+    16-wavefront workgroups, S = 1, 2 or 4 per segment by the width of the
+    block table (S > 1: each workgroup leaves a partial of its share of the
+    tiles and a merge combines them), each workgroup taking at most 128
+    tiles.  Lengths 0, 1, a tile and one token either side, and tables of
+    128 and 256 tiles filled to their last token and one token beyond (the
+    wider table: a larger split, or the stream-K plan); then the same
+    lengths over batches of 252-256 segments (S = 1, one workgroup per CU
+    of the MI355X's 256) and of 264-272 (stream-K)."""
     name, H, KVH, D, dtype, tt = case
-    cap = 128 * tt
-    base = [0, 1, tt - 1, tt, tt + 1, cap - 1, cap // 2, 3]
-    for lens in (base[:-1] + [cap], base[:-1] + [cap + 1]):
+    base = [0, 1, tt - 1, tt, tt + 1, 3, 64 * tt]
+    for top in (128 * tt, 128 * tt + 1, 256 * tt, 256 * tt + 1):
+        lens = base + [top - 1, top]
         wl = W.small_case(num_seqs=len(lens), H=H, KVH=KVH, D=D, kv_dtype=DT[dtype],
-                          seed=D + H, lens=lens)
+                          seed=D + H + top, lens=lens)
         print(f"case {name} lens={lens}", flush=True)
         assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"{name} lens {lens}")
     for segs in (256, 272):
         nseq = segs // KVH
         lens = (base * (nseq // len(base) + 1))[:nseq]
-        lens[-1] = cap
+        lens[-1] = 128 * tt
         wl = W.small_case(num_seqs=nseq, H=H, KVH=KVH, D=D, kv_dtype=DT[dtype],
                           seed=D + segs, lens=lens)
         print(f"case {name} segments={segs}", flush=True)

@@ -412,39 +412,54 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
                                   partition_tokens, waves);
         }
 
-        // Small batches on the VALU tile path: one workgroup per segment
-        // (paged_decode_segment_kernel) when the segments fit one round of
-        // workgroups, one per CU, and every segment fits the workgroup's
-        // rounds of tiles; no split-K workspace and no merge.  (Each load of
-        // a tile must lie in one page: block_size >= its rows.)
-        const bool seg_launch =
-            !mfma && partition_tokens == 0 && !po && !fold &&
+        // Small batches on the VALU tile path: one round of workgroups over
+        // the segments (paged_decode_segment_kernel) when they fit one per
+        // CU, S of them per segment.  A workgroup streams its share of a
+        // segment through one CU (~68 GB/s measured on MI355X), so a segment
+        // is split while each share keeps at least kSegSplitBytes of K/V,
+        // which one CU streams in about the time the merge launch then
+        // needed takes (~2.3 us).  With S = 1 there is no split-K workspace
+        // and no merge.  (Each load of a tile must lie in one page:
+        // block_size >= its rows.)
+        long long seg_split = 0;  // 0: the stream-K plan
+        if (!mfma && partition_tokens == 0 && !po && !fold &&
             tiling.head_tile <= xhip::kSegMaxHeadTile && block_size >= tile / xhip::kLoadsPerTile &&
-            (long long)nseq * segs <= cus &&
-            (max_ctx + tile - 1) / tile <=
-                (long long)xhip::kSegWaves * xhip::kSegTiles * xhip::kSegRounds;
+            (long long)nseq * segs <= cus) {
+            constexpr long long kSegSplitBytes = 160 << 10;
+            const long long cap = (long long)xhip::kSegWaves * xhip::kSegTiles * xhip::kSegRounds;
+            const long long seg_tiles = (max_ctx + tile - 1) / tile;
+            const long long seg_bytes = max_ctx * head_size * elem_bytes(kv_dtype) * 2;
+            long long S = 1;
+            while (S < 4 && (long long)nseq * segs * S * 2 <= cus &&
+                   (seg_bytes / (S * 2) >= kSegSplitBytes || seg_tiles > S * cap))
+                S *= 2;
+            if (seg_tiles <= S * cap) seg_split = S;
+        }
+        const bool seg_launch = seg_split > 0;
 
         const size_t eb_total = (size_t)elem_bytes(kv_dtype);
-        // workspace: fp32 partials o, their (m, l), the unit prefix
-        const size_t pre_bytes = (size_t)(nseq + 1) * sizeof(int);
-        auto o_size = [&](long long w) {
-            return ((size_t)w * 2 * tiling.head_tile * head_size * sizeof(float) + 255) &
-                   ~(size_t)255;
+        // workspace: fp32 partials o, their (m, l), the unit prefix; under a
+        // split segment launch, one partial per workgroup
+        const size_t pre_bytes = seg_launch ? 0 : (size_t)(nseq + 1) * sizeof(int);
+        const long long slots = seg_launch ? (seg_split > 1 ? nseq * segs * seg_split : 0)
+                                           : 2 * waves;
+        auto o_size = [&](long long n) {
+            return ((size_t)n * tiling.head_tile * head_size * sizeof(float) + 255) & ~(size_t)255;
         };
-        auto ml_size = [&](long long w) {
-            return ((size_t)w * 2 * tiling.head_tile * 2 * sizeof(float) + 255) & ~(size_t)255;
+        auto ml_size = [&](long long n) {
+            return ((size_t)n * tiling.head_tile * 2 * sizeof(float) + 255) & ~(size_t)255;
         };
-        if (fixed && !seg_launch && o_size(waves) + ml_size(waves) + pre_bytes > fixed->bytes)
+        if (fixed && o_size(slots) + ml_size(slots) + pre_bytes > fixed->bytes)
             return set_status(NXT_ATTN_E_UNSUPPORTED,
                               "this plan needs %zu bytes of split-K scratch; the allocation-free "
                               "entry point has %zu%s",
-                              o_size(waves) + ml_size(waves) + pre_bytes, fixed->bytes,
+                              o_size(slots) + ml_size(slots) + pre_bytes, fixed->bytes,
                               partition_tokens ? " (raise partition_tokens)" : "");
-        const size_t o_bytes = o_size(waves);
-        const size_t ml_bytes = ml_size(waves);
+        const size_t o_bytes = o_size(slots);
+        const size_t ml_bytes = ml_size(slots);
         WsCache::Lease lease;  // held until this chunk's launches are enqueued
         void *ws = nullptr;
-        if (seg_launch) {
+        if (seg_launch && seg_split == 1) {
             // (no workspace)
         } else if (fixed) {
             ws = fixed->ptr;  // launches of one stream run in order: chunks reuse it
@@ -479,8 +494,9 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
                    kv_block_stride, kv_head_stride, scale);
         p.ws_o = ws ? (float *)ws : nullptr;
         p.ws_ml = ws ? (float *)((char *)ws + o_bytes) : nullptr;
-        p.ws_prefix = ws ? (int *)((char *)ws + o_bytes + ml_bytes) : nullptr;
+        p.ws_prefix = ws && !seg_launch ? (int *)((char *)ws + o_bytes + ml_bytes) : nullptr;
         p.segment_launch = seg_launch ? 1 : 0;
+        p.segment_split = seg_launch ? (int)seg_split : 1;
         p.num_waves = (int)waves;
         p.min_tiles_per_wave = min_tpw;
         p.seg_cost = seg_cost;

@@ -127,15 +127,22 @@ static hipError_t launch_for_head_size(const DecodeParams &p, int head_tile, boo
         return hipErrorInvalidValue;
     }
     if (p.segment_launch) {
-        // one workgroup per segment, no merge
-        const unsigned sgrid = (unsigned)(p.num_seqs * p.num_kv_heads * p.head_tiles);
+        // segment_split workgroups per segment; above one, a merge
+        const unsigned segs = (unsigned)(p.num_seqs * p.num_kv_heads * p.head_tiles);
+        const unsigned sgrid = segs * (unsigned)p.segment_split;
+        hipError_t e = hipErrorInvalidValue;
         if (head_tile == 1)
-            return launch_partition(paged_decode_segment_kernel<KV, D, 1>, sgrid,
-                                    64 * kSegWaves, 0, st, ev_start, ev_stop, p);
-        if (head_tile == 2)
-            return launch_partition(paged_decode_segment_kernel<KV, D, 2>, sgrid,
-                                    64 * kSegWaves, 0, st, ev_start, ev_stop, p);
-        return hipErrorInvalidValue;
+            e = launch_partition(paged_decode_segment_kernel<KV, D, 1>, sgrid, 64 * kSegWaves, 0,
+                                 st, ev_start, ev_stop, p);
+        else if (head_tile == 2)
+            e = launch_partition(paged_decode_segment_kernel<KV, D, 2>, sgrid, 64 * kSegWaves, 0,
+                                 st, ev_start, ev_stop, p);
+        if (e != hipSuccess || p.segment_split == 1) return e;
+        if (head_tile == 1)
+            paged_decode_segment_merge_kernel<KV, D, 1><<<segs, 256, 0, st>>>(p);
+        else
+            paged_decode_segment_merge_kernel<KV, D, 2><<<segs, 256, 0, st>>>(p);
+        return hipGetLastError();
     }
     switch (head_tile) {
     case 1: {

@@ -728,8 +728,11 @@ __global__ __launch_bounds__(64 * kSegWaves) void paged_decode_segment_kernel(
     const int row = lane / RL;
     const bool col_ok = (NCH == RL) || (col < NCH);
     const int segs = p.num_kv_heads * p.head_tiles;
-    const int s = blockIdx.x / segs;
-    const int seg = blockIdx.x - s * segs;
+    const int S = p.segment_split;
+    const int gseg = blockIdx.x / S;         // segment of the batch
+    const int part = blockIdx.x - gseg * S;  // this workgroup's share of its tiles
+    const int s = gseg / segs;
+    const int seg = gseg - s * segs;
     const int kvh = seg / p.head_tiles;
     const int ht = seg - kvh * p.head_tiles;
     const int g0 = ht * GT;
@@ -750,28 +753,32 @@ __global__ __launch_bounds__(64 * kSegWaves) void paged_decode_segment_kernel(
 #pragma unroll
         for (int e = 0; e < VEC; e++) st.o[h][e] = 0.0f;
     }
+    // The workgroup's tiles are u * S + part for u = 0, 1, ...: wavefront w
+    // takes u = w + kSegWaves * j in round 0, and kSegWaves * kSegTiles more
+    // in each later round.
     int nxt[kSegTiles][LPT];
 #pragma unroll
     for (int j = 0; j < kSegTiles; j++)
-        tile_blocks<TPL>(bt, (wave + kSegWaves * j) * TT, p.max_ctx, p.bs_shift, nxt[j]);
+        tile_blocks<TPL>(bt, ((wave + kSegWaves * j) * S + part) * TT, p.max_ctx, p.bs_shift,
+                         nxt[j]);
     const int Ts = (L + TT - 1) / TT;
     for (int r = 0; r < kSegRounds; r++) {
-        const int tb = wave + kSegWaves * kSegTiles * r;  // this wavefront's first tile of the round
-        if (tb >= Ts) break;
+        const int ub = wave + kSegWaves * kSegTiles * r;  // this wavefront's first tile of the round
+        if (ub * S + part >= Ts) break;
         TileRegs regs[kSegTiles];
 #pragma unroll
         for (int j = 0; j < kSegTiles; j++) {
             int blk[LPT];
 #pragma unroll
             for (int k = 0; k < LPT; k++) blk[k] = __builtin_amdgcn_readfirstlane(nxt[j][k]);
-            tile_load<KV, D, true, true>(p, bt, kb, vb, (tb + kSegWaves * j) * TT, L, row, col,
-                                         col_ok, blk, regs[j]);
+            tile_load<KV, D, true, true>(p, bt, kb, vb, ((ub + kSegWaves * j) * S + part) * TT, L,
+                                         row, col, col_ok, blk, regs[j]);
         }
         if (r + 1 < kSegRounds) {
 #pragma unroll
             for (int j = 0; j < kSegTiles; j++)
-                tile_blocks<TPL>(bt, (tb + kSegWaves * (kSegTiles + j)) * TT, p.max_ctx,
-                                 p.bs_shift, nxt[j]);
+                tile_blocks<TPL>(bt, ((ub + kSegWaves * (kSegTiles + j)) * S + part) * TT,
+                                 p.max_ctx, p.bs_shift, nxt[j]);
         }
 #pragma unroll
         for (int j = 0; j < kSegTiles; j++) tile_compute<KV, D, GT, true>(p, regs[j], st);
@@ -820,6 +827,49 @@ __global__ __launch_bounds__(64 * kSegWaves) void paged_decode_segment_kernel(
             const float a = fast_exp2(s_m[w][h] - Ms);
             l += s_l[w][h] * a;
             o += s_o[w][h][d] * a;
+        }
+        if (S > 1) {
+            // this workgroup's fp32 partial (m, l, o), combined by
+            // paged_decode_segment_merge_kernel
+            const size_t slot = (size_t)blockIdx.x * GT + h;
+            p.ws_o[slot * D + d] = o;
+            if (d == 0) {
+                p.ws_ml[slot * 2] = M;
+                p.ws_ml[slot * 2 + 1] = l;
+            }
+            continue;
+        }
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        store_elem<KV>(o_row(p, s, kvh * p.group + g0 + h, D, EB), d, o * inv);
+    }
+}
+
+// The rows of the segments paged_decode_segment_kernel split over S =
+// DecodeParams::segment_split workgroups: one workgroup per segment
+// combines their fp32 partials (slots segment * S + j) by the online
+// log-sum-exp rule and writes the output rows.
+template <int KV, int D, int GT>
+__global__ __launch_bounds__(256) void paged_decode_segment_merge_kernel(const DecodeParams p) {
+    constexpr int EB = Geometry<KV, D>::kElemBytes;
+    const int segs = p.num_kv_heads * p.head_tiles;
+    const int S = p.segment_split;
+    const int s = blockIdx.x / segs;
+    const int seg = blockIdx.x - s * segs;
+    const int kvh = seg / p.head_tiles;
+    const int g0 = (seg - kvh * p.head_tiles) * GT;
+    const int nh = min(GT, p.group - g0);
+    for (int i = threadIdx.x; i < nh * D; i += 256) {
+        const int h = i / D, d = i - h * D;
+        float m = -INFINITY, l = 0.0f, o = 0.0f;
+        for (int j = 0; j < S; j++) {
+            const size_t slot = ((size_t)blockIdx.x * S + j) * GT + h;
+            const float mj = p.ws_ml[slot * 2];
+            const float M = fmaxf(m, mj);
+            const float Ms = (M == -INFINITY) ? 0.0f : M;
+            const float a = fast_exp2(m - Ms), w = fast_exp2(mj - Ms);
+            l = l * a + p.ws_ml[slot * 2 + 1] * w;
+            o = o * a + p.ws_o[slot * D + d] * w;
+            m = M;
         }
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         store_elem<KV>(o_row(p, s, kvh * p.group + g0 + h, D, EB), d, o * inv);

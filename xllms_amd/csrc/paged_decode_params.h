@@ -38,10 +38,11 @@ constexpr int kLoadsPerTile = 4;     // 16-byte K (and V) loads per lane per til
 constexpr int kMaxSeqsPerLaunch = 8192;  // the per-workgroup prefix scan lives in LDS
 
 // Small batches on the VALU tile path (DecodeParams::segment_launch): one
-// workgroup of kSegWaves wavefronts per segment, each wavefront with
-// kSegTiles tiles in flight, at most kSegRounds rounds of them (so segments
-// of at most kSegWaves * kSegTiles * kSegRounds tiles), head tiles of at most
-// kSegMaxHeadTile heads.
+// workgroup of kSegWaves wavefronts per segment (or per share of a segment,
+// DecodeParams::segment_split), each wavefront with kSegTiles tiles in
+// flight, at most kSegRounds rounds of them (so segments of at most
+// kSegWaves * kSegTiles * kSegRounds tiles per workgroup), head tiles of at
+// most kSegMaxHeadTile heads.
 constexpr int kSegWaves = 16;
 constexpr int kSegTiles = 2;
 constexpr int kSegRounds = 4;
@@ -94,9 +95,14 @@ struct DecodeParams {
     float scale_log2;          // scale * log2(e)
     int merge_per_segment;     // 1: merge with one workgroup per segment
     int segment_launch;        // 1 (VALU tile path, automatic plan, whole outputs): one
-                               // workgroup per segment and no merge
-                               // (paged_decode_segment_kernel); num_waves and the
-                               // split-K workspace are unused
+                               // round of workgroups over the segments
+                               // (paged_decode_segment_kernel); num_waves is unused
+    int segment_split;         // workgroups per segment under segment_launch (1, 2 or 4):
+                               // with 1 the workgroup writes the rows and nothing else
+                               // runs; above 1 workgroup j of a segment takes its tiles
+                               // j, j + S, ... and leaves an fp32 partial in ws_o / ws_ml
+                               // slot (segment * S + j), which
+                               // paged_decode_segment_merge_kernel combines
     int pair_tiles;            // 1 (MFMA path, head_tiles == 2, wg_fix == 0): paired head
                                // tiles.  A segment is (sequence, kv head); the two
                                // wavefronts 2k, 2k + 1 of the launch walk the same stream-K
