@@ -699,15 +699,17 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void paged_decode_partition_ke
     });
 }
 
-// Small batches on the VALU tile path (DecodeParams::segment_launch): one
-// workgroup of kSegWaves wavefronts per segment (sequence, kv head, head
-// tile), so no segment is cut between workgroups and there is no merge
-// launch.  Wavefront w takes the segment's tiles w, w + kSegWaves, ...,
-// kSegTiles of them in flight at a time; the sequence length, the query rows
-// and the first tiles' block ids are requested together, the block ids
-// without waiting for the length (entries past the sequence are read, within
-// the table row, but their tokens are masked).  The wavefronts' states are
-// combined through LDS and the workgroup writes the output rows.
+// Small batches on the VALU tile path (DecodeParams::segment_launch): S =
+// DecodeParams::segment_split workgroups of kSegWaves wavefronts per segment
+// (sequence, kv head, head tile), one round of workgroups for the batch.
+// Workgroup j of a segment takes its tiles j, j + S, ...; of those, wavefront
+// w takes the w-th, (w + kSegWaves)-th, ..., kSegTiles of them in flight at a
+// time.  The sequence length, the query rows and the first tiles' block ids
+// are requested together, the block ids without waiting for the length
+// (entries past the sequence are read, within the table row, but their
+// tokens are masked).  The wavefronts' states are combined through LDS; with
+// S = 1 the workgroup writes the output rows (no merge launch), else its
+// fp32 partial for paged_decode_segment_merge_kernel.
 template <int KV, int D, int GT>
 __global__ __launch_bounds__(64 * kSegWaves) void paged_decode_segment_kernel(
     const DecodeParams p) {
