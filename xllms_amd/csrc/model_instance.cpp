@@ -576,19 +576,7 @@ int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<st
     // The rows of requests admitted or extended before a failure are still
     // written: the index already holds their tokens.
     bool staged = false;
-    if (st->h_pack.n == (size_t)-1) {
-        rc = fail("exec: out of host memory");
-    } else if (st->h_pack.n > 0) {
-        if (!st->d_pack.reserve((st->h_pack.n + 15) & ~(size_t)15)) {
-            rc = fail("exec: out of device memory");
-        } else {
-            e = xhip::launch_stage_copy(st->d_pack.p, st->h_pack.p, (st->h_pack.n + 15) & ~(size_t)15,
-                                        st->stream);
-            staged = e == hipSuccess;
-        }
-    }
-    char *const dp = st->d_pack.p;
-    auto at = [dp](size_t off) { return (void *)(dp + off); };
+    char *const hp = st->h_pack.p;
     xhip::KvAppendParams p;
     std::memset(&p, 0, sizeof(p));
     p.key_cache = st->key_cache;
@@ -600,14 +588,31 @@ int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<st
     p.row_chunks = p.row_bytes / 16;
     p.block_size = s.block_size;
     p.bs_shift = __builtin_ctz((unsigned)s.block_size);
-    if (staged && st->h_slots.n) {
-        xhip::KvAppendParams w = p;
-        w.slots = (const int *)at(o_slots);
-        w.key_rows = (const char *const *)at(o_kptr);
-        w.value_rows = (const char *const *)at(o_vptr);
-        w.num_tokens = (int)st->h_slots.n;
-        e = xhip::launch_kv_append(w, st->stream);
+    // The staging copy, and in the same launch the new tokens' K/V rows,
+    // whose slots and row pointers that launch reads from the host-pinned
+    // pack (launch_stage_copy_append).
+    if (st->h_pack.n == (size_t)-1) {
+        rc = fail("exec: out of host memory");
+    } else if (st->h_pack.n > 0) {
+        if (!st->d_pack.reserve((st->h_pack.n + 15) & ~(size_t)15)) {
+            rc = fail("exec: out of device memory");
+        } else {
+            const size_t bytes = (st->h_pack.n + 15) & ~(size_t)15;
+            if (st->h_slots.n) {
+                xhip::KvAppendParams w = p;
+                w.slots = (const int *)(hp + o_slots);
+                w.key_rows = (const char *const *)(hp + o_kptr);
+                w.value_rows = (const char *const *)(hp + o_vptr);
+                w.num_tokens = (int)st->h_slots.n;
+                e = xhip::launch_stage_copy_append(st->d_pack.p, hp, bytes, w, st->stream);
+            } else {
+                e = xhip::launch_stage_copy(st->d_pack.p, hp, bytes, st->stream);
+            }
+            staged = e == hipSuccess;
+        }
     }
+    char *const dp = st->d_pack.p;
+    auto at = [dp](size_t off) { return (void *)(dp + off); };
     if (staged && e == hipSuccess && st->h_src.n) {
         xhip::KvAppendParams c = p;
         c.key = st->key_cache;

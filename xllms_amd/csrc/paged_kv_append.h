@@ -43,4 +43,10 @@ hipError_t launch_kv_append(const KvAppendParams &p, hipStream_t stream);
 // host-pinned memory to device memory with a kernel on `stream`.
 hipError_t launch_stage_copy(void *dst, const void *host_src, size_t bytes, hipStream_t stream);
 
+// launch_stage_copy and launch_kv_append(p) in one launch; p's per-token
+// arrays (slots, key_rows, value_rows; src_slots unused) must be readable
+// by the device where they are, e.g. in the host-pinned source being copied.
+hipError_t launch_stage_copy_append(void *dst, const void *host_src, size_t bytes,
+                                    const KvAppendParams &p, hipStream_t stream);
+
 }  // namespace xhip

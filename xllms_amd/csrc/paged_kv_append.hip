@@ -31,8 +31,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kKvAppendBlock = 64;  // one wavefront per workgroup
 constexpr long long kKvAppendMaxChunks = (1LL << 31) - 1;
 
-__global__ __launch_bounds__(kKvAppendBlock) void paged_kv_append_kernel(const KvAppendParams p) {
-    const uint32_t i = blockIdx.x * kKvAppendBlock + threadIdx.x;
+// Chunk i of a launch's K/V rows to its page slot.
+__device__ __forceinline__ void append_chunk(const KvAppendParams &p, uint32_t i) {
     if (i >= p.chunks) return;
     const uint32_t row_l = div_by(i, p.row_div);  // row of the launch: token * kv heads + head
     const int c = (int)(i - row_l * (uint32_t)p.row_chunks);
@@ -75,6 +75,10 @@ __global__ __launch_bounds__(kKvAppendBlock) void paged_kv_append_kernel(const K
     *(u32x4 *)((char *)p.value_cache + dst) = v;
 }
 
+__global__ __launch_bounds__(kKvAppendBlock) void paged_kv_append_kernel(const KvAppendParams p) {
+    append_chunk(p, blockIdx.x * kKvAppendBlock + threadIdx.x);
+}
+
 hipError_t launch_kv_append(const KvAppendParams &params, hipStream_t stream) {
     KvAppendParams p = params;
     const long long per_token = (long long)p.num_kv_heads * p.row_chunks;
@@ -114,6 +118,48 @@ hipError_t launch_stage_copy(void *dst, const void *host_src, size_t bytes, hipS
     if (blocks > 1024) blocks = 1024;
     stage_copy_kernel<<<(unsigned)blocks, 256, 0, stream>>>((const u32x4 *)host_src, (u32x4 *)dst,
                                                              n16);
+    return hipGetLastError();
+}
+
+// The staging copy and a K/V append in one launch: workgroups [0,
+// copy_blocks) copy the staged arrays, the others write the new rows, whose
+// slots and row pointers `p` reads from the host-pinned staging buffer
+// itself (its device copy is being made by the same launch).  One launch
+// fewer per exec: a launch costs ~2.5 us of host time (HIP runtime, as
+// measured on the MI355X hosts).
+__global__ __launch_bounds__(256) void stage_append_kernel(const u32x4 *__restrict__ src,
+                                                           u32x4 *__restrict__ dst, long long n16,
+                                                           unsigned copy_blocks,
+                                                           const KvAppendParams p) {
+    if (blockIdx.x < copy_blocks) {
+        const long long stride = (long long)copy_blocks * 256;
+        for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride)
+            dst[i] = src[i];
+        return;
+    }
+    append_chunk(p, (blockIdx.x - copy_blocks) * 256 + threadIdx.x);
+}
+
+hipError_t launch_stage_copy_append(void *dst, const void *host_src, size_t bytes,
+                                    const KvAppendParams &params, hipStream_t stream) {
+    KvAppendParams p = params;
+    const long long per_token = (long long)p.num_kv_heads * p.row_chunks;
+    const long long chunks = (long long)p.num_tokens * per_token;
+    if (bytes == 0 || chunks <= 0 || chunks > (1LL << 24)) {  // (the separate launches)
+        hipError_t e = launch_stage_copy(dst, host_src, bytes, stream);
+        return e != hipSuccess ? e : launch_kv_append(params, stream);
+    }
+    if ((bytes | (uintptr_t)dst | (uintptr_t)host_src) & 15) return hipErrorInvalidValue;
+    p.row_div = div_magic((uint32_t)p.row_chunks);
+    p.head_div = div_magic((uint32_t)p.num_kv_heads);
+    p.tok0 = 0;
+    p.chunks = (uint32_t)chunks;
+    const long long n16 = (long long)(bytes / 16);
+    long long copy_blocks = (n16 + 255) / 256;
+    if (copy_blocks > 1024) copy_blocks = 1024;
+    const long long blocks = copy_blocks + (chunks + 255) / 256;
+    stage_append_kernel<<<(unsigned)blocks, 256, 0, stream>>>(
+        (const u32x4 *)host_src, (u32x4 *)dst, n16, (unsigned)copy_blocks, p);
     return hipGetLastError();
 }
 
