@@ -213,6 +213,25 @@ def test_segment_launch_limits(cuda, case):
         assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"{name} segments {segs}")
 
 
+@pytest.mark.parametrize("case", [
+    # (H, KVH, D, dtype, block_size): pages of 4 and 8 tokens under tiles of
+    # 16 (fp32 d=64; a load's 4 rows within a page), bf16 at head_size 112
+    ("fp32-bs4", 12, 12, 64, "fp32", 4),
+    ("fp32-bs8", 8, 4, 64, "fp32", 8),
+    ("bf16-112", 4, 2, 112, "bf16", 16),
+])
+def test_segment_split_small_pages_and_heads(cuda, case):
+    """The split segment launch (2 or 4 workgroups per segment, each taking
+    every S-th tile) over pages smaller than a tile and at head_size 112,
+    with empty, one-token and page-boundary lengths."""
+    name, H, KVH, D, dtype, bs = case
+    lens = [0, 1, bs - 1, bs, bs + 1, 700, 1500, 2047]
+    wl = W.small_case(num_seqs=len(lens), H=H, KVH=KVH, D=D, bs=bs, kv_dtype=DT[dtype],
+                      seed=D + bs, lens=lens)
+    print(f"case {name} lens={lens}", flush=True)
+    assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"{name}")
+
+
 def test_back_to_back_launches_share_a_workspace(cuda):
     """Launches of different shapes on one stream share one split-K
     workspace (grown when a shape needs more): each launch's partials and
