@@ -4,7 +4,8 @@ included), split-K partition and entry point at random, so that the plans
 (stream-K, the small-batch segment launch with its split, automatic and
 explicit partitions) meet combinations the hand-written cases do not list.
 The cascade draws random groups (sizes, prefix lengths, empty suffixes,
-unshared sequences) the same way.  Same tolerances as the parity tests:
+unshared sequences) the same way, and the plugin ABI (run_ex) takes draws
+like the decode's.  Same tolerances as the parity tests:
 fp32 rel 1e-5 per (sequence, head), fp16/bf16 atol 2e-3 + rtol 1e-2."""
 from __future__ import annotations
 
@@ -95,3 +96,35 @@ def test_random_cascade_matches_oracle(cuda, seed):
     torch.cuda.synchronize()
     assert_close(dw.out.float().cpu().numpy(), O.run_workload(wl, precision="mt"), wl.kv_dtype,
                  f"cascade seed {seed}")
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_plugin_run_ex_matches_oracle(cuda, seed):
+    """The same draws through the plugin ABI (nxt_backend_init -> run_ex ->
+    fini on the reference's descriptor, dlopen'ed like the backend manager)."""
+    import torch
+    from xllms_amd import backend as B
+    rng = np.random.default_rng(3000 + seed)
+    dtype, D, bs, G, KVH, lens, part, _ = _draw(rng)
+    H = G * KVH
+    wl = W.small_case(num_seqs=len(lens), H=H, KVH=KVH, D=D, bs=bs, kv_dtype=DT[dtype],
+                      seed=seed, lens=lens)
+    print(f"case seed={seed} {dtype} d={D} bs={bs} H={H} KVH={KVH} seqs={len(lens)} "
+          f"max_len={max(lens)} partition={part} plugin run_ex", flush=True)
+    dw = W.upload(wl)
+    plugin = B.LoadedBackend()
+    assert plugin.init() == 0
+    try:
+        ex = B.NxtPagedAttentionInputEx()
+        ex.struct_size = ctypes.sizeof(B.NxtPagedAttentionInputEx)
+        ex.base = B.make_input(dw.query, dw.key_cache, dw.value_cache, dw.block_tables,
+                               dw.seq_lens, num_kv_heads=KVH, scale=wl.scale,
+                               stream=torch.cuda.current_stream().cuda_stream)
+        ex.kv_dtype = wl.kv_dtype
+        ex.partition_tokens = part
+        assert plugin.run_ex(ex, dw.out.data_ptr()) == 0
+        torch.cuda.synchronize()
+    finally:
+        assert plugin.fini() == 0
+    assert_close(dw.out.float().cpu().numpy(), O.run_workload(wl, precision="mt"), wl.kv_dtype,
+                 f"plugin seed {seed}")
