@@ -1,15 +1,16 @@
 """Seeded random shapes against the oracle: every draw picks a dtype, head
 size, kv heads and GQA group, block size, batch, lengths (empty ones
-included), split-K partition and entry point at random, so that the plans
-(stream-K, the small-batch segment launch with its split, automatic and
-explicit partitions) meet combinations the hand-written cases do not list.
-The cascade draws random groups (sizes, prefix lengths, empty suffixes,
-unshared sequences) the same way, and the plugin ABI (run_ex) takes draws
-like the decode's.  Same tolerances as the parity tests:
-fp32 rel 1e-5 per (sequence, head), fp16/bf16 atol 2e-3 + rtol 1e-2."""
+included), softmax scale, split-K partition and entry point at random, so
+that the plans (stream-K, the small-batch segment launch with its split,
+automatic and explicit partitions) meet combinations the hand-written cases
+do not list.  The cascade draws random groups (sizes, prefix lengths, empty
+suffixes, unshared sequences) the same way, and the plugin ABI (run_ex)
+takes draws like the decode's.  Same tolerances as the parity tests: fp32
+rel 1e-5 per (sequence, head), fp16/bf16 atol 2e-3 + rtol 1e-2."""
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 
 import numpy as np
 import pytest
@@ -46,16 +47,31 @@ def _draw(rng):
     return dtype, D, bs, G, KVH, lens.tolist(), part, entry
 
 
+def _oracle(wl):
+    """fp32 draws against the oracle's double-precision form: at 4-16 times
+    the reference's scale (scores of tens) the fp32 restatement itself is
+    1-2e-5 (relative, per row) off the exact result, the kernels 2-6e-6
+    (measured on MI355X over such draws).  fp16/bf16 draws against the fp32
+    restatement."""
+    return O.run_workload(wl, precision="f64" if wl.kv_dtype == W.FP32 else "mt")
+
+
+def _rescale(wl, rng):
+    """The draw's softmax scale: 1/sqrt(d) times 0.1, 1, 4 or 16 (flat to
+    nearly one-hot score rows)."""
+    return dataclasses.replace(wl, scale=wl.scale * float(rng.choice([0.1, 1.0, 4.0, 16.0])))
+
+
 @pytest.mark.parametrize("seed", range(200))
 def test_random_decode_matches_oracle(cuda, seed):
     import torch
     rng = np.random.default_rng(1000 + seed)
     dtype, D, bs, G, KVH, lens, part, entry = _draw(rng)
     H = G * KVH
-    wl = W.small_case(num_seqs=len(lens), H=H, KVH=KVH, D=D, bs=bs, kv_dtype=DT[dtype],
-                      seed=seed, lens=lens)
+    wl = _rescale(W.small_case(num_seqs=len(lens), H=H, KVH=KVH, D=D, bs=bs,
+                               kv_dtype=DT[dtype], seed=seed, lens=lens), rng)
     print(f"case seed={seed} {dtype} d={D} bs={bs} H={H} KVH={KVH} seqs={len(lens)} "
-          f"max_len={max(lens)} partition={part} {entry}", flush=True)
+          f"max_len={max(lens)} scale={wl.scale:.4f} partition={part} {entry}", flush=True)
     dw = W.upload(wl)
     fn = getattr(_lib.backend(), entry)
     rc = fn(dw.out.data_ptr(), dw.query.data_ptr(), dw.key_cache.data_ptr(),
@@ -65,8 +81,7 @@ def test_random_decode_matches_oracle(cuda, seed):
             torch.cuda.current_stream().cuda_stream, wl.kv_dtype, part)
     assert rc == PA.NXT_ATTN_OK, PA.last_status()
     torch.cuda.synchronize()
-    assert_close(dw.out.float().cpu().numpy(), O.run_workload(wl, precision="mt"), wl.kv_dtype,
-                 f"seed {seed}")
+    assert_close(dw.out.float().cpu().numpy(), _oracle(wl), wl.kv_dtype, f"seed {seed}")
 
 
 @pytest.mark.parametrize("seed", range(60))
@@ -126,5 +141,4 @@ def test_random_plugin_run_ex_matches_oracle(cuda, seed):
         torch.cuda.synchronize()
     finally:
         assert plugin.fini() == 0
-    assert_close(dw.out.float().cpu().numpy(), O.run_workload(wl, precision="mt"), wl.kv_dtype,
-                 f"plugin seed {seed}")
+    assert_close(dw.out.float().cpu().numpy(), _oracle(wl), wl.kv_dtype, f"plugin seed {seed}")
