@@ -100,8 +100,9 @@ def test_random_cascade_matches_oracle(cuda, seed):
     singles = [int(x) for x in rng.integers(0, 500, size=int(rng.integers(0, 6)))]
     wl, pg, pb = shared_case(spec, singles=singles, H=G * KVH, KVH=KVH, D=D,
                              kv_dtype=DT[dtype], seed=seed)
+    wl = _rescale(wl, rng)
     print(f"case seed={seed} {dtype} d={D} H={G * KVH} KVH={KVH} groups={len(pb)} "
-          f"seqs={wl.num_seqs}", flush=True)
+          f"seqs={wl.num_seqs} scale={wl.scale:.4f}", flush=True)
     dw = W.upload(wl)
     d_pg = torch.from_numpy(pg.astype(np.int32)).cuda()
     d_pb = torch.from_numpy(pb.astype(np.int32)).cuda()
@@ -109,8 +110,7 @@ def test_random_cascade_matches_oracle(cuda, seed):
                                dw.seq_lens, d_pg, d_pb, num_kv_heads=KVH, scale=wl.scale,
                                max_groups=len(pb), kv_dtype=wl.kv_dtype)
     torch.cuda.synchronize()
-    assert_close(dw.out.float().cpu().numpy(), O.run_workload(wl, precision="mt"), wl.kv_dtype,
-                 f"cascade seed {seed}")
+    assert_close(dw.out.float().cpu().numpy(), _oracle(wl), wl.kv_dtype, f"cascade seed {seed}")
 
 
 @pytest.mark.parametrize("seed", range(40))
