@@ -6,7 +6,9 @@ automatic and explicit partitions) meet combinations the hand-written cases
 do not list.  The cascade draws random groups (sizes, prefix lengths, empty
 suffixes, unshared sequences) the same way, and the plugin ABI (run_ex)
 takes draws like the decode's.  Same tolerances as the parity tests: fp32
-rel 1e-5 per (sequence, head), fp16/bf16 atol 2e-3 + rtol 1e-2."""
+rel 1e-5 per (sequence, head) against the fp32 restatement, fp16/bf16 atol
+2e-3 + rtol 1e-2; fp32 draws at 4-16x the reference's softmax scale use the
+double-precision rule of `_check`."""
 from __future__ import annotations
 
 import ctypes
@@ -47,19 +49,45 @@ def _draw(rng):
     return dtype, D, bs, G, KVH, lens.tolist(), part, entry
 
 
-def _oracle(wl):
-    """fp32 draws against the oracle's double-precision form: at 4-16 times
-    the reference's scale (scores of tens) the fp32 restatement itself is
-    1-2e-5 (relative, per row) off the exact result, the kernels 2-6e-6
-    (measured on MI355X over such draws).  fp16/bf16 draws against the fp32
-    restatement."""
-    return O.run_workload(wl, precision="f64" if wl.kv_dtype == W.FP32 else "mt")
+def _check(got, wl, factor, what):
+    """Compare one draw's output with the oracle.
+
+    fp16/bf16 draws, and fp32 draws at the reference's own softmax scale or
+    below (factor <= 1: `text_gen.c:732` always uses 1/sqrtf(hd)), go against
+    the fp32 restatement of `text_gen.c:1284-1310` at the stated tolerance.
+
+    fp32 draws at 4 or 16 times that scale (scores of tens, nearly one-hot
+    rows) are checked against the oracle's double-precision form instead:
+    there the fp32 restatement is itself 1-2e-5 (relative, per row) off the
+    exact result, and the kernel 2-6e-6 (measured on MI355X).  The rule, per
+    (sequence, head) row: max|g - f64| <= max(1e-5 * max|f64|, max|f32 - f64|),
+    so the kernel is never further from the exact result than the reference's
+    own fp32 arithmetic is, or within rel 1e-5 of it.  The deviation from the
+    fp32 restatement is printed."""
+    if wl.kv_dtype != W.FP32 or factor <= 1.0:
+        return assert_close(got, O.run_workload(wl, precision="mt"), wl.kv_dtype, what)
+    f64 = O.run_workload(wl, precision="f64")
+    f32 = O.run_workload(wl, precision="mt").astype(np.float64)
+    g = np.asarray(got, dtype=np.float64)
+    assert np.isfinite(g).all(), f"{what}: non-finite output"
+    dev = np.abs(g - f64).max(axis=-1)
+    ref_dev = np.abs(f32 - f64).max(axis=-1)
+    bound = np.maximum(1e-5 * np.abs(f64).max(axis=-1), ref_dev)
+    scale = np.maximum(np.abs(f64).max(axis=-1), 1e-30)
+    vs_f32 = float((np.abs(g - f32).max(axis=-1) / scale).max(initial=0.0))
+    print(f"{what}: scale x{factor}: max rel row vs f64 {float((dev / scale).max(initial=0.0)):.2e}, "
+          f"fp32 oracle vs f64 {float((ref_dev / scale).max(initial=0.0)):.2e}, "
+          f"vs fp32 oracle {vs_f32:.2e}", flush=True)
+    bad = dev > bound
+    assert not bad.any(), (f"{what}: {int(bad.sum())} rows further from the f64 oracle than "
+                           f"max(1e-5 rel, the fp32 oracle's own deviation)")
 
 
 def _rescale(wl, rng):
     """The draw's softmax scale: 1/sqrt(d) times 0.1, 1, 4 or 16 (flat to
-    nearly one-hot score rows)."""
-    return dataclasses.replace(wl, scale=wl.scale * float(rng.choice([0.1, 1.0, 4.0, 16.0])))
+    nearly one-hot score rows).  Returns the workload and the factor."""
+    factor = float(rng.choice([0.1, 1.0, 4.0, 16.0]))
+    return dataclasses.replace(wl, scale=wl.scale * factor), factor
 
 
 @pytest.mark.parametrize("seed", range(200))
@@ -68,8 +96,8 @@ def test_random_decode_matches_oracle(cuda, seed):
     rng = np.random.default_rng(1000 + seed)
     dtype, D, bs, G, KVH, lens, part, entry = _draw(rng)
     H = G * KVH
-    wl = _rescale(W.small_case(num_seqs=len(lens), H=H, KVH=KVH, D=D, bs=bs,
-                               kv_dtype=DT[dtype], seed=seed, lens=lens), rng)
+    wl, factor = _rescale(W.small_case(num_seqs=len(lens), H=H, KVH=KVH, D=D, bs=bs,
+                                       kv_dtype=DT[dtype], seed=seed, lens=lens), rng)
     print(f"case seed={seed} {dtype} d={D} bs={bs} H={H} KVH={KVH} seqs={len(lens)} "
           f"max_len={max(lens)} scale={wl.scale:.4f} partition={part} {entry}", flush=True)
     dw = W.upload(wl)
@@ -81,7 +109,7 @@ def test_random_decode_matches_oracle(cuda, seed):
             torch.cuda.current_stream().cuda_stream, wl.kv_dtype, part)
     assert rc == PA.NXT_ATTN_OK, PA.last_status()
     torch.cuda.synchronize()
-    assert_close(dw.out.float().cpu().numpy(), _oracle(wl), wl.kv_dtype, f"seed {seed}")
+    _check(dw.out.float().cpu().numpy(), wl, factor, f"seed {seed}")
 
 
 @pytest.mark.parametrize("seed", range(60))
@@ -100,7 +128,7 @@ def test_random_cascade_matches_oracle(cuda, seed):
     singles = [int(x) for x in rng.integers(0, 500, size=int(rng.integers(0, 6)))]
     wl, pg, pb = shared_case(spec, singles=singles, H=G * KVH, KVH=KVH, D=D,
                              kv_dtype=DT[dtype], seed=seed)
-    wl = _rescale(wl, rng)
+    wl, factor = _rescale(wl, rng)
     print(f"case seed={seed} {dtype} d={D} H={G * KVH} KVH={KVH} groups={len(pb)} "
           f"seqs={wl.num_seqs} scale={wl.scale:.4f}", flush=True)
     dw = W.upload(wl)
@@ -110,7 +138,7 @@ def test_random_cascade_matches_oracle(cuda, seed):
                                dw.seq_lens, d_pg, d_pb, num_kv_heads=KVH, scale=wl.scale,
                                max_groups=len(pb), kv_dtype=wl.kv_dtype)
     torch.cuda.synchronize()
-    assert_close(dw.out.float().cpu().numpy(), _oracle(wl), wl.kv_dtype, f"cascade seed {seed}")
+    _check(dw.out.float().cpu().numpy(), wl, factor, f"cascade seed {seed}")
 
 
 @pytest.mark.parametrize("seed", range(40))
@@ -141,4 +169,5 @@ def test_random_plugin_run_ex_matches_oracle(cuda, seed):
         torch.cuda.synchronize()
     finally:
         assert plugin.fini() == 0
-    assert_close(dw.out.float().cpu().numpy(), _oracle(wl), wl.kv_dtype, f"plugin seed {seed}")
+    # never rescaled: the reference's own 1/sqrt(d), so the fp32 restatement
+    _check(dw.out.float().cpu().numpy(), wl, 1.0, f"plugin seed {seed}")
