@@ -7,7 +7,10 @@ with garbage).  A step is one call of the reference entry point
 nxt_paged_attention over the whole batch, with every input already resident in
 HBM.  Steps rotate over several independent copies of the K/V pool (>= 3 and
 >= 768 MB in total) so no step is served from the 256 MB MALL of the previous
-one.
+one.  The reference bench's shape flags (--batch --ctx --heads --kv-heads
+--head-size --dtype, tests/test_attention_bench.c:421-435) select its
+workload instead: every sequence at --ctx tokens (defaults B 16, ctx 1024,
+32 q / 8 kv heads, d 128, fp16), seeded N(0,1) data and a permuted table.
 
 Prints ONE JSON line:
   value        seqs/s = num_seqs / (GPU time per step), whole job on 1 GPU
@@ -267,7 +270,7 @@ def bench_kv_append(args) -> int:
     from xllms_amd import paged_attention as PA
     from xllms_amd import workloads as W
 
-    wl = W.make(args.config)
+    wl = workload_from_args(args)
     dw = W.upload(wl)
     bs, kvh, d = wl.block_size, wl.num_kv_heads, wl.head_size
     slots = []
@@ -600,13 +603,154 @@ def bench_serve(args) -> int:
     return 0 if ok else 1
 
 
+def _pct(xs, q):
+    import numpy as np
+    return round(float(np.percentile(np.asarray(xs, dtype=np.float64), q)), 2) if len(xs) else None
+
+
+def wg_trace_report(args, wl, lib, step, i0, stream, ms_per_step, alg_bytes, entry, waves) -> int:
+    """Per-workgroup timeline of one step through the instrumented build
+    (xllms_amd/csrc/wg_trace.h): 5 traced steps, the last one summarised.
+    Times in us from the first workgroup's entry (s_memrealtime, 100 MHz)."""
+    import numpy as np
+    import torch
+    words = int(lib.xhip_wg_trace_words())
+    buf = torch.zeros(words, dtype=torch.int64, device="cuda")
+    for i in range(5):
+        buf.zero_()
+        torch.cuda.synchronize()
+        lib.xhip_set_wg_trace(buf.data_ptr())
+        step(i0 + i)
+        lib.xhip_set_wg_trace(None)
+        torch.cuda.synchronize()
+    rec = buf.cpu().numpy().view(np.uint64).astype(np.int64)
+    part = rec[:4096 * 16].reshape(4096, 16)
+    used = part[:, 0] > 0
+    part = part[used]
+    merge = rec[4096 * 16:].reshape(-1, 2)
+    merge = merge[merge[:, 0] > 0]
+    t0 = int(part[:, 0].min())
+    us = lambda x: (np.asarray(x, dtype=np.int64) - t0) / 100.0  # noqa: E731
+    info = part[:, 3]
+    role = (info >> 32) & 0xFF
+    entry_us, pro_us, exit_us = us(part[:, 0]), us(part[:, 1]), us(part[:, 2])
+    groups = np.nonzero(used)[0]
+    lines = []
+    lines.append(f"# Per-workgroup timeline: {wl.name}" + (" (cascade)" if args.cascade else ""))
+    lines.append("")
+    lines.append(f"Command: `python bench.py {' '.join(sys.argv[1:])}`")
+    lines.append("")
+    lines.append(f"Instrumented build `libxllm_hip_backend_trace.so` (XHIP_WG_TRACE, "
+                 f"`xllms_amd/csrc/wg_trace.h`): s_memrealtime stamps (100 MHz) per workgroup "
+                 f"of one step, the 5th of 5 traced steps after {args.warmup} warm-up and "
+                 f"{2 * args.steps} untraced steps. Times in us from the first workgroup's entry. "
+                 f"Untraced step in the same run: {ms_per_step * 1e3:.2f} us.")
+    lines.append("")
+    roles = {0: "all", 1: "prefix body", 2: "suffix body"}
+    summary = {"workload": wl.name, "cascade": bool(args.cascade), "step_us": round(ms_per_step * 1e3, 2),
+               "workgroups": int(used.sum()), "merge_workgroups": int(len(merge))}
+    lines.append("| Workgroups | n | entry p50 / max | prologue done p50 / p90 / max | "
+                 "first tile p50 / max | last tile done p10 / p50 / p90 / max | exit p10 / p50 / p90 / max |")
+    lines.append("|---|---|---|---|---|---|---|")
+    for r in sorted(set(role.tolist())):
+        sel = role == r
+        wf = part[sel][:, 4:16].reshape(-1, 4, 3)
+        ft = wf[:, :, 0].ravel()
+        le = wf[:, :, 1].ravel()
+        ft_us, le_us = us(ft[ft > 0]), us(le[le > 0])
+        row = {"n": int(sel.sum()),
+               "entry": [_pct(entry_us[sel], 50), _pct(entry_us[sel], 100)],
+               "prologue_done": [_pct(pro_us[sel], q) for q in (50, 90, 100)],
+               "first_tile": [_pct(ft_us, 50), _pct(ft_us, 100)],
+               "last_tile_done": [_pct(le_us, q) for q in (10, 50, 90, 100)],
+               "exit": [_pct(exit_us[sel], q) for q in (10, 50, 90, 100)]}
+        summary[roles.get(r, str(r))] = row
+        lines.append(f"| {roles.get(r, str(r))} | {row['n']} | {row['entry'][0]} / {row['entry'][1]} | "
+                     f"{' / '.join(map(str, row['prologue_done']))} | "
+                     f"{row['first_tile'][0]} / {row['first_tile'][1]} | "
+                     f"{' / '.join(map(str, row['last_tile_done']))} | "
+                     f"{' / '.join(map(str, row['exit']))} |")
+    # per XCD (dispatch deals workgroup b to XCD b % 8)
+    xcd = groups % 8
+    lines.append("")
+    lines.append("Exit by XCD (workgroup b runs on XCD b % 8), p50 / max: " + ", ".join(
+        f"{x}: {_pct(exit_us[xcd == x], 50)} / {_pct(exit_us[xcd == x], 100)}" for x in range(8)))
+    # streaming rate per wavefront: tiles x bytes per tile / (last tile done - first tile)
+    tile_bytes = 16 * wl.head_size * wl.elem_bytes * 2
+    wf = part[:, 4:16].reshape(-1, 4, 3).reshape(-1, 3)
+    ok = (wf[:, 0] > 0) & (wf[:, 1] > wf[:, 0])
+    tiles = wf[ok, 2] & 0xFFFFFFFF
+    pieces = wf[ok, 2] >> 32
+    dur = (wf[ok, 1] - wf[ok, 0]) / 100.0
+    rate = tiles * tile_bytes / np.maximum(dur, 1e-3) / 1e3  # GB/s
+    lines.append("")
+    lines.append(f"Wavefronts with tiles: {int(ok.sum())}; tiles per wavefront p10 / p50 / max "
+                 f"{_pct(tiles, 10)} / {_pct(tiles, 50)} / {_pct(tiles, 100)}; pieces p50 / max "
+                 f"{_pct(pieces, 50)} / {_pct(pieces, 100)}; per-wavefront K/V rate (first tile "
+                 f"issued to last tile done) p10 / p50 / p90 {_pct(rate, 10)} / {_pct(rate, 50)} / "
+                 f"{_pct(rate, 90)} GB/s.")
+    summary["tiles_per_wave"] = [_pct(tiles, 10), _pct(tiles, 50), _pct(tiles, 100)]
+    summary["wave_rate_gbs"] = [_pct(rate, 10), _pct(rate, 50), _pct(rate, 90)]
+    if len(merge):
+        me, mx = us(merge[:, 0]), us(merge[:, 1][merge[:, 1] > 0])
+        summary["merge"] = {"entry": [_pct(me, 0), _pct(me, 50), _pct(me, 100)],
+                            "exit": [_pct(mx, 50), _pct(mx, 100)]}
+        lines.append("")
+        lines.append(f"Merge launch: {len(merge)} workgroups; entry min / p50 / max "
+                     f"{_pct(me, 0)} / {_pct(me, 50)} / {_pct(me, 100)}; exit p50 / max "
+                     f"{_pct(mx, 50)} / {_pct(mx, 100)}.")
+    span = float(exit_us.max())
+    summary["partition_span_us"] = round(span, 2)
+    lines.append("")
+    lines.append(f"Partition launch span (first entry to last exit): {span:.2f} us; algorithmic "
+                 f"bytes {alg_bytes} = {alg_bytes / (span * 1e-6) / 1e9:.0f} GB/s over it.")
+    text = "\n".join(lines) + "\n"
+    with open(args.wg_trace, "w") as f:
+        f.write(text)
+    log(text)
+    print(json.dumps({"metric": "per-workgroup timeline (instrumented build)", **summary}), flush=True)
+    return 0
+
+
+SHAPE_FLAGS = ("batch", "ctx", "heads", "kv_heads", "head_size", "dtype", "block_size")
+
+
+def workload_from_args(args):
+    """--config's workload, or the reference bench's shape when any of its
+    flags is given (defaults tests/test_attention_bench.c:34-41)."""
+    from xllms_amd import workloads as W
+    if all(getattr(args, f) is None for f in SHAPE_FLAGS):
+        return W.make(args.config)
+    if args.cascade:
+        raise SystemExit("--cascade needs a shared-prefix --config, not the reference-bench shape")
+    dt = {"fp16": W.FP16, "bf16": W.BF16, "fp32": W.FP32}[args.dtype or "fp16"]
+    return W.ref_bench_shape(batch=args.batch or 16, ctx=args.ctx or 1024, heads=args.heads or 32,
+                             kv_heads=args.kv_heads or 8, head_size=args.head_size or 128,
+                             kv_dtype=dt, block_size=args.block_size or 16)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--steps", "--iterations", dest="steps", type=int, default=200,
+                    help="timed steps (--iterations: the reference bench's name for it)")
     ap.add_argument("--warmup", type=int, default=200,
                     help="untimed steps first (>= ~20 ms of work: the GPU clocks ramp up over it)")
     ap.add_argument("--config", type=int, default=2, help="1..5, 6 = config 4b (GQA16)")
+    # The reference bench's shape flags (tests/test_attention_bench.c:421-435; its
+    # defaults :34-41).  Any of them selects that workload instead of --config:
+    # every sequence at --ctx tokens, seeded N(0,1) data, a permuted table.
+    ap.add_argument("--batch", type=int, default=None, help="reference-bench shape: sequences (16)")
+    ap.add_argument("--ctx", type=int, default=None, help="reference-bench shape: context (1024)")
+    ap.add_argument("--heads", type=int, default=None, help="reference-bench shape: q heads (32)")
+    ap.add_argument("--kv-heads", type=int, default=None,
+                    help="reference-bench shape: kv heads (8)")
+    ap.add_argument("--head-size", type=int, default=None,
+                    help="reference-bench shape: head size (128)")
+    ap.add_argument("--dtype", choices=["fp16", "bf16", "fp32"], default=None,
+                    help="reference-bench shape: K/V element type (fp16)")
+    ap.add_argument("--block-size", type=int, default=None,
+                    help="reference-bench shape: tokens per page (16)")
     ap.add_argument("--partition", type=int, default=0,
                     help="split-K tokens per wavefront (0 = automatic stream-K plan)")
     ap.add_argument("--pools", type=int, default=0, help="K/V pool copies to rotate (0 = auto)")
@@ -635,6 +779,10 @@ def main() -> int:
                     help="instead of the benchmark, measure the ceilings the roofline fraction "
                          "is read against: a plain 1 GiB device copy and the workload's K/V "
                          "access pattern streamed with no arithmetic (xllm_stream_probe)")
+    ap.add_argument("--wg-trace", default=None, metavar="MD",
+                    help="after the timed steps, run 5 steps through the instrumented build "
+                         "(libxllm_hip_backend_trace.so) and write the per-workgroup timeline "
+                         "of the last to MD (markdown); the JSON line is then that summary")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run 5 plain device copies of MIB MiB "
                          "(the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -677,7 +825,7 @@ def main() -> int:
     dev = torch.device("cuda:0")
 
     t0 = time.perf_counter()
-    wl = W.make(args.config)
+    wl = workload_from_args(args)
     log(f"[bench] workload {wl.name}: {wl.describe()} built in {time.perf_counter() - t0:.1f}s")
     alg_bytes = wl.algorithmic_bytes()
     logical_bytes = wl.logical_bytes()
@@ -693,7 +841,7 @@ def main() -> int:
     log(f"[bench] {pools} K/V pools of {pool_bytes / 2**20:.0f} MiB each resident in HBM")
 
     stream = torch.cuda.current_stream().cuda_stream
-    lib = PA._lib.backend()
+    lib = PA._lib.backend(trace=bool(args.wg_trace))
     entry = "nxt_paged_attention" if args.partition == 0 and wl.kv_dtype != W.BF16 else None
     waves = PA.auto_waves(wl.num_seqs, wl.num_heads, wl.head_size, wl.num_kv_heads,
                           wl.max_num_blocks_per_seq, wl.block_size, wl.kv_dtype)
@@ -782,6 +930,10 @@ def main() -> int:
             raise RuntimeError(f"launch failed: {msg}")
         kern_ms = np.array([ev.elapsed_ms(a, b) for a, b in zip(k_start, k_done)])
     ev.destroy_all()
+
+    if args.wg_trace:
+        return wg_trace_report(args, wl, lib, step, args.warmup + 2 * args.steps, stream,
+                               total_ms / args.steps, alg_bytes, entry, waves)
 
     ms_per_step = total_ms / args.steps
     # A cascade step is several kernels (plan, two partition + merge passes,

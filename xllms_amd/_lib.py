@@ -15,6 +15,9 @@ LIB_DIR = os.path.join(_HERE, "lib")
 BACKEND_SO = os.path.join(LIB_DIR, "libxllm_hip_backend.so")
 WORKLOAD_SO = os.path.join(LIB_DIR, "libxllm_workload.so")
 STREAM_PROBE_SO = os.path.join(LIB_DIR, "libxllm_stream_probe.so")
+# The same library with per-workgroup timestamps (measurement tool of
+# bench.py --wg-trace; never the product path).
+BACKEND_TRACE_SO = os.path.join(LIB_DIR, "libxllm_hip_backend_trace.so")
 
 _lock = threading.Lock()
 _cache: dict[str, ctypes.CDLL] = {}
@@ -90,8 +93,16 @@ _LEGACY_ARGS = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                 c_int, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_int, c_void_p]
 
 
-def backend() -> ctypes.CDLL:
-    lib = _load(BACKEND_SO)
+def backend(trace: bool = False) -> ctypes.CDLL:
+    """The product library, or with trace=True its instrumented build (the
+    same entry points plus xhip_set_wg_trace / xhip_wg_trace_words)."""
+    lib = _load(BACKEND_TRACE_SO if trace else BACKEND_SO)
+    if trace and not getattr(lib, "_xllm_trace_typed", False):
+        lib.xhip_set_wg_trace.argtypes = [c_void_p]
+        lib.xhip_set_wg_trace.restype = None
+        lib.xhip_wg_trace_words.argtypes = []
+        lib.xhip_wg_trace_words.restype = ctypes.c_ulonglong
+        lib._xllm_trace_typed = True
     if not getattr(lib, "_xllm_typed", False):
         for name in ("nxt_paged_attention", "nxt_paged_attention_v2", "nxt_paged_attention_flash"):
             fn = getattr(lib, name)

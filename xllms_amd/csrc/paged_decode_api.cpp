@@ -23,6 +23,7 @@
 #include "paged_kv_append.h"
 #include "workspace.h"
 #include "workspace_cache.h"
+#include "wg_trace.h"
 #include "xllm_hip_operator_api.h"
 
 namespace {
@@ -33,6 +34,9 @@ thread_local int t_status = NXT_ATTN_OK;
 thread_local char t_message[512] = "ok";
 thread_local hipEvent_t t_trace_start = nullptr;
 thread_local hipEvent_t t_trace_partition = nullptr;
+// Per-workgroup timestamp buffer of the instrumented measurement build
+// (wg_trace.h); the product build never sets it.
+thread_local unsigned long long *t_wg_trace = nullptr;
 
 int set_status(int status, const char *fmt, ...) {
     t_status = status;
@@ -504,6 +508,7 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         p.ws_o = ws ? (float *)ws : nullptr;
         p.ws_ml = ws ? (float *)((char *)ws + o_bytes) : nullptr;
         p.ws_prefix = ws && !seg_launch ? (int *)((char *)ws + o_bytes + ml_bytes) : nullptr;
+        p.wg_trace = t_wg_trace;
         p.segment_launch = seg_launch ? 1 : 0;
         p.segment_split = seg_launch ? (int)seg_split : 1;
         p.num_waves = (int)waves;
@@ -733,6 +738,7 @@ int cascade_run(void *out, const void *query, const void *key_cache, const void 
             q->wg_fix = 1;
             q->skip_empty = 1;  // merged from the other batch, or zeros, by the merge
         }
+        pp.wg_trace = ps.wg_trace = t_wg_trace;
         pp.pair_tiles = 1;  // the two 32-row head tiles share each range
         pp.wg_fix = 0;
         pp.out_f32 = (float *)(w + o_po);
@@ -1178,6 +1184,18 @@ __attribute__((visibility("default"))) int nxt_paged_prefix_groups(
 __attribute__((visibility("default"))) int nxt_attn_last_status(void) { return t_status; }
 
 __attribute__((visibility("default"))) const char *nxt_attn_last_error(void) { return t_message; }
+
+#if XHIP_WG_TRACE
+// Measurement build only (libxllm_hip_backend_trace.so): the calling thread's
+// next calls stamp per-workgroup timestamps into `buffer` (device memory of
+// xhip::kWgTraceBufferWords 64-bit words, layout in wg_trace.h); NULL stops.
+__attribute__((visibility("default"))) void xhip_set_wg_trace(void *buffer) {
+    t_wg_trace = (unsigned long long *)buffer;
+}
+__attribute__((visibility("default"))) unsigned long long xhip_wg_trace_words() {
+    return xhip::kWgTraceBufferWords;
+}
+#endif
 
 __attribute__((visibility("default"))) void nxt_attn_set_trace_events(void *start_event,
                                                                     void *partition_done_event) {

@@ -169,6 +169,7 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, 2) void paged_decode_casca
     int *vlen = grp + B, *vrow = vlen + V, *vdesc = vrow + V;
     int *gP = vdesc + 4 * V, *gcnt = gP + NG, *gfirst = gcnt + NG;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    XHIP_WG_STAMP(pp, 0);
 
     // 1. (every prefix-batch sequence unused until step 3)
     for (int s = tid; s < B; s += NT) {
@@ -286,12 +287,18 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, 2) void paged_decode_casca
     }
     const CascadeLdsPlan cp{slen,  soff,       vlen, vrow, vdesc,         grp,  &s_win[0][0],
                             p_row, (const char *)ps.q, ps.q_rows, ps.num_heads, G, rows, B};
+    XHIP_WG_STAMP(pp, 1);
+    XHIP_WG_PUT(pp, 3, (unsigned long long)l | ((unsigned long long)(l < gp ? 1 : 2) << 32));
     if (l < gp)
         mfma_partition_body<KV, D, 2, true, kSrcPrefix, KV == KV_F16>(
             pp, nullptr, tables, pre_p, l, gp * NW, sm.a, &cp);
     else
         mfma_partition_body<KV, D, RS, false, kSrcSuffix, KV == KV_F16>(
             ps, nullptr, tables, pre_s, l - gp, (Gw - gp) * NW, sm.b, &cp);
+#if XHIP_TRACING
+    __syncthreads();
+    XHIP_WG_STAMP(pp, 2);
+#endif
 }
 
 // (m, l, acc) <- (m, l, acc) (+) a finished row: the state (lse, 1, row).
@@ -346,6 +353,7 @@ __device__ __forceinline__ void segment_state(const DecodeParams &p, int s, int 
 template <int KV, int D, int GTS, int NT>
 __global__ __launch_bounds__(NT) void paged_decode_cascade_merge_kernel(
     const DecodeParams pp, const DecodeParams ps, const int *__restrict__ p_row, int rows) {
+    XHIP_MERGE_SCOPE(pp);
     constexpr int C4 = D / 4;
     constexpr int NW = kMfmaWavesPerGroup;
     constexpr int GTP = 2 * kMfmaHeads;

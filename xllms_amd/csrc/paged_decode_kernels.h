@@ -35,6 +35,7 @@
 #include <stdint.h>
 
 #include "paged_decode_params.h"
+#include "wg_trace.h"
 
 namespace xhip {
 
@@ -1034,6 +1035,7 @@ constexpr int kMergeSplit = 8;
 template <int KV, int D, int GT, int TT>
 __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_kernel(
     const DecodeParams p) {
+    XHIP_MERGE_SCOPE(p);
     constexpr int C4 = D / 4;
     __shared__ f32x4 s_acc[kMergeSplit][kMergeCols];
     __shared__ float s_m[kMergeSplit][kMergeCols];
@@ -1123,6 +1125,7 @@ constexpr int kMergeSegThreads = 64;  // the smallest NT (LDS split below that m
 
 template <int KV, int D, int GT, int TT, int NT>
 __global__ __launch_bounds__(NT) void paged_decode_merge_segment_kernel(const DecodeParams p) {
+    XHIP_MERGE_SCOPE(p);
     constexpr int C4 = D / 4;
     __shared__ f32x4 s_acc[NT];
     __shared__ float s_m[NT];

@@ -29,6 +29,7 @@
 #pragma once
 
 #include "paged_decode_kernels.h"
+#include "wg_trace.h"
 
 namespace xhip {
 
@@ -703,6 +704,9 @@ __device__ __forceinline__ void mfma_partition_body(
     MfmaState<D> st[R];   // the state of the piece being computed; after the loop, the last one's
     MfmaPiece pc;         // the piece being computed; after the loop, the last one
     bool have_last = false;  // FIX: the last piece is cut (its state is kept for the sweep)
+#if XHIP_TRACING
+    int n_tiles = 0, n_pieces = 0;
+#endif
     RangeCursor cur;
     cur.g = (int)g_lo;
     cur.g_end = g_lo < total ? min(total, cur.g + tpw) : cur.g;
@@ -738,6 +742,7 @@ __device__ __forceinline__ void mfma_partition_body(
         int fold_base = (p.fold_row && pc.t_begin == 0) ? p.fold_row[pc.s] : -1;
         MfmaTileRegs<D> ra, rb;
         int blk_a = __builtin_amdgcn_readlane(ids, 0);
+        XHIP_WAVE_STAMP(p, wave, 0);
         {
             const char *kb = (const char *)p.k + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
             const char *vb = (const char *)p.v + (size_t)pc.kvh * (size_t)p.kv_head_stride * 2;
@@ -774,6 +779,10 @@ __device__ __forceinline__ void mfma_partition_body(
             fold.base = fold_base;
             if (R == 1 && fold.base >= 0) mfma_fold_load<D, R>(p, pc, lane, fold);
             const int ntiles = (pc.t_end - pc.t_begin + 15) >> 4;
+#if XHIP_TRACING
+            n_tiles += ntiles;
+            n_pieces++;
+#endif
             for (int i = 0; i < ntiles; i++) {
                 if (i > 0 && (i & 63) == 0) ids = mfma_load_ids<SRC>(p, tables, pc, i, lane, cp);
                 const int t0 = pc.t_begin + 16 * i;
@@ -828,7 +837,11 @@ __device__ __forceinline__ void mfma_partition_body(
             fold_base = fold_base_n;
             mfma_load_q<D, R, SRC>(p, pc, lane, q, cp);
         }
+        XHIP_WAVE_STAMP(p, wave, 1);
     }
+#if XHIP_TRACING
+    XHIP_WAVE_PUT(p, wave, 2, (unsigned long long)n_tiles | ((unsigned long long)n_pieces << 32));
+#endif
 
     if constexpr (FIX == 2) {
         // As below, with the one relay slot.
@@ -921,9 +934,16 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, D <= 128 ? 2 : 1) void pag
     // which do not wait behind the K/V loads in flight.
     extern __shared__ int pre[];  // num_seqs + 1 split-unit prefixes
     __shared__ MfmaLds<D, R> sm;
+    XHIP_WG_STAMP(p, 0);
     batch_prefix<16, kMfmaWavesPerGroup>(p, pre);
-    mfma_partition_body<KV, D, R>(p, lens, tables, pre, logical_block(p, pre[p.num_seqs]),
-                                  p.num_waves, sm);
+    XHIP_WG_STAMP(p, 1);
+    const int lb = logical_block(p, pre[p.num_seqs]);
+    XHIP_WG_PUT(p, 3, lb);
+    mfma_partition_body<KV, D, R>(p, lens, tables, pre, lb, p.num_waves, sm);
+#if XHIP_TRACING
+    __syncthreads();
+    XHIP_WG_STAMP(p, 2);
+#endif
 }
 
 }  // namespace xhip

@@ -149,6 +149,9 @@ struct DecodeParams {
     const float *fold_lse;
     int fold_rows;
     int fold_kr;
+    // Per-workgroup timestamps (wg_trace.h): written only by the kernels of
+    // the instrumented measurement build (XHIP_WG_TRACE); null otherwise.
+    unsigned long long *wg_trace;
 };
 
 

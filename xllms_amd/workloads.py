@@ -331,6 +331,25 @@ def config5(seed: int = 20260005, num_seqs: int = 256, groups: int = 16,
     return wl
 
 
+def ref_bench_shape(batch: int = 16, ctx: int = 1024, heads: int = 32, kv_heads: int = 8,
+                    head_size: int = 128, kv_dtype: int = FP16, block_size: int = 16,
+                    seed: int = 20260010) -> Workload:
+    """The reference bench's workload shape (tests/test_attention_bench.c:34-41
+    defaults: batch 16, context 1024, 32 q / 8 kv heads, d 128, fp16, block
+    size 16; every sequence at the full context, :134-137): a pool of exactly
+    the pages the batch needs.  Unlike the reference's buffers (zeros and an
+    identity block table, :125-139), Q/K/V are seeded N(0,1) and the table is
+    a seeded permutation of the pool, so the output check means something."""
+    if min(batch, ctx, heads, kv_heads, head_size, block_size) <= 0 or heads % kv_heads:
+        raise ValueError("batch, ctx, heads, kv_heads, head_size, block_size must be positive "
+                         "and heads a multiple of kv_heads")
+    rng = np.random.default_rng(seed)
+    name = (f"refbench-b{batch}-ctx{ctx}-{heads}x{kv_heads}-d{head_size}-"
+            f"{ {FP16: 'fp16', BF16: 'bf16', FP32: 'fp32'}[kv_dtype] }")
+    return _make(name, seed, [ctx] * batch, H=heads, KVH=kv_heads, D=head_size, bs=block_size,
+                 kv_dtype=kv_dtype, pool_factor=1, rng=rng, poison=True)
+
+
 def serve_prompts(config: int, token_seed: int = 7):
     """Token-level prompts with the sequence lengths of a config's batch (the
     same seeded draws as its generator) for the serving path, which builds
