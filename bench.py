@@ -624,6 +624,7 @@ def wg_trace_report(args, wl, lib, step, i0, stream, ms_per_step, alg_bytes, ent
         lib.xhip_set_wg_trace(None)
         torch.cuda.synchronize()
     rec = buf.cpu().numpy().view(np.uint64).astype(np.int64)
+    np.save(args.wg_trace + ".npy", rec)  # the raw words, for further reading
     part = rec[:4096 * 16].reshape(4096, 16)
     used = part[:, 0] > 0
     part = part[used]

@@ -232,6 +232,31 @@ def test_segment_split_small_pages_and_heads(cuda, case):
     assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, f"{name}")
 
 
+@pytest.mark.parametrize("case", [
+    # (name, H, KVH, D, dtype, lengths)
+    ("one-long", 12, 12, 64, "fp32", [1024] + [16] * 7),
+    ("all-long", 12, 12, 64, "fp32", [2040, 2047, 2048, 1999]),
+    ("mostly-empty", 12, 12, 64, "fp32", [0, 0, 1, 0, 0, 0, 0, 1300, 0, 0]),
+    ("ragged-128-segs", 4, 4, 64, "fp32", [0, 1, 15, 16, 17, 700, 2000, 4000] * 4),
+    ("single-seq-wide", 2, 1, 128, "fp32", [8000]),
+    ("gqa2-bf16-80", 8, 4, 80, "bf16", [3000, 5, 1, 0, 2048, 2049]),
+])
+def test_segment_length_profiles(cuda, case):
+    """Small VALU batches (the segment launch, split or not, or stream-K)
+    over length profiles: one long sequence among short ones, only long
+    ones, mostly empty sequences, a ragged batch of 128 segments, one
+    sequence over a wide table, GQA-2 bf16 at head_size 80; each twice in a
+    row on one stream and its workspace."""
+    name, H, KVH, D, dtype, lens = case
+    wl = W.small_case(num_seqs=len(lens), H=H, KVH=KVH, D=D, kv_dtype=DT[dtype],
+                      seed=len(lens) + D, lens=lens)
+    ref = oracle(wl)
+    dw = W.upload(wl)
+    for rep in range(2):
+        print(f"case {name} rep={rep} lens={lens}", flush=True)
+        assert_close(run_gpu(wl, tensors=dw), ref, wl.kv_dtype, f"{name} rep {rep}")
+
+
 def test_back_to_back_launches_share_a_workspace(cuda):
     """Launches of different shapes on one stream share one split-K
     workspace (grown when a shape needs more): each launch's partials and

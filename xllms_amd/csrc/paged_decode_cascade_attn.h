@@ -169,7 +169,7 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, 2) void paged_decode_casca
     int *vlen = grp + B, *vrow = vlen + V, *vdesc = vrow + V;
     int *gP = vdesc + 4 * V, *gcnt = gP + NG, *gfirst = gcnt + NG;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    XHIP_WG_STAMP(pp, 0);
+    XHIP_WG_BEGIN(pp);
 
     // 1. (every prefix-batch sequence unused until step 3)
     for (int s = tid; s < B; s += NT) {
@@ -295,10 +295,7 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, 2) void paged_decode_casca
     else
         mfma_partition_body<KV, D, RS, false, kSrcSuffix, KV == KV_F16>(
             ps, nullptr, tables, pre_s, l - gp, (Gw - gp) * NW, sm.b, &cp);
-#if XHIP_TRACING
-    __syncthreads();
-    XHIP_WG_STAMP(pp, 2);
-#endif
+    XHIP_WG_FLUSH(pp);
 }
 
 // (m, l, acc) <- (m, l, acc) (+) a finished row: the state (lse, 1, row).

@@ -730,6 +730,7 @@ __global__ __launch_bounds__(64 * kSegWaves) void paged_decode_segment_kernel(
     const int col = lane % RL;
     const int row = lane / RL;
     const bool col_ok = (NCH == RL) || (col < NCH);
+    XHIP_WG_BEGIN(p);
     const int segs = p.num_kv_heads * p.head_tiles;
     const int S = p.segment_split;
     const int gseg = blockIdx.x / S;         // segment of the batch
@@ -768,6 +769,7 @@ __global__ __launch_bounds__(64 * kSegWaves) void paged_decode_segment_kernel(
     for (int r = 0; r < kSegRounds; r++) {
         const int ub = wave + kSegWaves * kSegTiles * r;  // this wavefront's first tile of the round
         if (ub * S + part >= Ts) break;
+        if (r == 0 && wave == 0) XHIP_WG_STAMP(p, 7);
         TileRegs regs[kSegTiles];
 #pragma unroll
         for (int j = 0; j < kSegTiles; j++) {
@@ -787,6 +789,7 @@ __global__ __launch_bounds__(64 * kSegWaves) void paged_decode_segment_kernel(
         for (int j = 0; j < kSegTiles; j++) tile_compute<KV, D, GT, true>(p, regs[j], st);
     }
 
+    if (wave == 0) XHIP_WG_STAMP(p, 8);
     // This wavefront's state: its rows merged (lane bits >= log2 RL), then
     // through LDS to the workgroup's combine.
 #pragma unroll
@@ -845,6 +848,7 @@ __global__ __launch_bounds__(64 * kSegWaves) void paged_decode_segment_kernel(
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         store_elem<KV>(o_row(p, s, kvh * p.group + g0 + h, D, EB), d, o * inv);
     }
+    XHIP_WG_FLUSH(p);
 }
 
 // The rows of the segments paged_decode_segment_kernel split over S =
@@ -853,6 +857,7 @@ __global__ __launch_bounds__(64 * kSegWaves) void paged_decode_segment_kernel(
 // log-sum-exp rule and writes the output rows.
 template <int KV, int D, int GT>
 __global__ __launch_bounds__(256) void paged_decode_segment_merge_kernel(const DecodeParams p) {
+    XHIP_MERGE_SCOPE(p);
     constexpr int EB = Geometry<KV, D>::kElemBytes;
     const int segs = p.num_kv_heads * p.head_tiles;
     const int S = p.segment_split;

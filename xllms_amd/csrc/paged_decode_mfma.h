@@ -934,16 +934,13 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, D <= 128 ? 2 : 1) void pag
     // which do not wait behind the K/V loads in flight.
     extern __shared__ int pre[];  // num_seqs + 1 split-unit prefixes
     __shared__ MfmaLds<D, R> sm;
-    XHIP_WG_STAMP(p, 0);
+    XHIP_WG_BEGIN(p);
     batch_prefix<16, kMfmaWavesPerGroup>(p, pre);
     XHIP_WG_STAMP(p, 1);
     const int lb = logical_block(p, pre[p.num_seqs]);
     XHIP_WG_PUT(p, 3, lb);
     mfma_partition_body<KV, D, R>(p, lens, tables, pre, lb, p.num_waves, sm);
-#if XHIP_TRACING
-    __syncthreads();
-    XHIP_WG_STAMP(p, 2);
-#endif
+    XHIP_WG_FLUSH(p);
 }
 
 }  // namespace xhip
