@@ -625,10 +625,11 @@ def wg_trace_report(args, wl, lib, step, i0, stream, ms_per_step, alg_bytes, ent
         torch.cuda.synchronize()
     rec = buf.cpu().numpy().view(np.uint64).astype(np.int64)
     np.save(args.wg_trace + ".npy", rec)  # the raw words, for further reading
-    part = rec[:4096 * 16].reshape(4096, 16)
+    W_ = 24  # words per partition record (xllms_amd/csrc/wg_trace.h)
+    part = rec[:4096 * W_].reshape(4096, W_)
     used = part[:, 0] > 0
     part = part[used]
-    merge = rec[4096 * 16:].reshape(-1, 2)
+    merge = rec[4096 * W_:].reshape(-1, 2)
     merge = merge[merge[:, 0] > 0]
     t0 = int(part[:, 0].min())
     us = lambda x: (np.asarray(x, dtype=np.int64) - t0) / 100.0  # noqa: E731
@@ -671,6 +672,12 @@ def wg_trace_report(args, wl, lib, step, i0, stream, ms_per_step, alg_bytes, ent
                      f"{row['first_tile'][0]} / {row['first_tile'][1]} | "
                      f"{' / '.join(map(str, row['last_tile_done']))} | "
                      f"{' / '.join(map(str, row['exit']))} |")
+    extra = [w for w in range(16, W_) if (part[:, w] > 0).mean() > 0.5]
+    if extra:
+        lines.append("")
+        lines.append("Kernel-specific phase stamps (`wg_trace.h`), p50 / max: " + ", ".join(
+            f"[{w}] {_pct(us(part[:, w][part[:, w] > 0]), 50)} / "
+            f"{_pct(us(part[:, w][part[:, w] > 0]), 100)}" for w in extra))
     # per XCD (dispatch deals workgroup b to XCD b % 8)
     xcd = groups % 8
     lines.append("")

@@ -190,6 +190,7 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, 2) void paged_decode_casca
         vdesc[4 * v + 3] = -1;
     }
     __syncthreads();
+    XHIP_WG_STAMP(pp, 16);
     // 2. (thread t takes sequences [t * per, (t + 1) * per), as batch_prefix)
     const int per = (B + NT - 1) / NT;
     const int segs_s = seq_segments(ps);
@@ -223,6 +224,7 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, 2) void paged_decode_casca
     }
     if (lane == 63) s_part[wave] = is;
     __syncthreads();
+    XHIP_WG_STAMP(pp, 17);
     // 3. (groups 64 at a time, lane g taking group g0 + g)
     if (wave == 0) {
         int vt = 0, tp = 0;  // prefix-batch sequences and units of the groups so far
@@ -271,6 +273,7 @@ __global__ __launch_bounds__(64 * kMfmaWavesPerGroup, 2) void paged_decode_casca
         if (tid == NT - 1) pre_s[B] = base + is;
     }
     __syncthreads();
+    XHIP_WG_STAMP(pp, 18);
     // 4.
     const int Gw = gridDim.x;
     const int gp = cascade_prefix_groups(pre_p[V], pre_s[B], Gw, ps.min_tiles_per_wave);

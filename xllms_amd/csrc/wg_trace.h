@@ -9,19 +9,21 @@
 //
 // Layout of the buffer DecodeParams::wg_trace points at (unsigned 64-bit
 // words), filled by one traced call:
-//   partition launch, record b (physical workgroup b), 16 words at 16 * b:
+//   partition launch, record b (physical workgroup b), 24 words at 24 * b:
 //     [0] entry  [1] prologue done (split-unit scan / plan)  [2] exit
 //     [3] logical workgroup | role << 32 (cascade: 1 prefix body, 2 suffix)
 //     MFMA kernels, wavefront w: [4 + 3w] first tile issued  [5 + 3w] last
 //     tile done  [6 + 3w] tiles | pieces << 32
 //     segment kernel: [7] first tile issued [8] last tile done (wavefront 0)
+//     [16..23] kernel-specific phase stamps (cascade plan: [16] caller arrays
+//     loaded, [17] members and suffix units, [18] groups laid out)
 //   merge launch, record b at kWgTraceMergeBase + 2 * b:
 //     [0] entry  [1] exit
 #pragma once
 
 namespace xhip {
 
-constexpr int kWgTraceWords = 16;
+constexpr int kWgTraceWords = 24;
 constexpr unsigned long long kWgTraceMaxGroups = 4096;
 constexpr unsigned long long kWgTraceMergeBase = kWgTraceMaxGroups * kWgTraceWords;
 constexpr unsigned long long kWgTraceMergeMax = 65536;
