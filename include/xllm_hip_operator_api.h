@@ -113,7 +113,14 @@ enum {
  * evenly over one resident round of wavefronts; otherwise it is the token
  * range each wavefront streams (a power of two >= the kernel tile, 16 tokens
  * for fp16/bf16 head_size 128), e.g. to check that results do not depend on
- * where sequences are cut.  Returns NXT_ATTN_OK or a negative status. */
+ * where sequences are cut.  Returns NXT_ATTN_OK or a negative status.
+ * Graph capture: the split-K workspace is the library's, per (device,
+ * stream); a captured call holds its address, so the library keeps every
+ * buffer a capture used alive (a later larger call on the stream allocates
+ * a new one beside it) until nxt_attn_release_workspaces().  A call under
+ * capture that would need a larger workspace than its stream has returns
+ * NXT_ATTN_E_UNSUPPORTED without launching: make one call of the shape on
+ * that stream before capturing. */
 int nxt_paged_attention_ex(void *out, const void *query, const void *key_cache,
                            const void *value_cache, const int *block_tables,
                            const int *seq_lens, int num_seqs, int num_heads,
@@ -129,11 +136,19 @@ int nxt_paged_attention_ex(void *out, const void *query, const void *key_cache,
  * scratch array of 66 MiB that the library holds until the process ends,
  * instead of the library's per-stream workspace: the call makes no hipMalloc
  * or hipFree.  Every automatic plan (partition_tokens = 0) fits on a 256-CU
- * MI355X, so results equal nxt_paged_attention_ex's bit for bit; a plan
- * that needs more scratch (an explicit partition_tokens over a large batch)
- * returns NXT_ATTN_E_UNSUPPORTED without launching.  Every
- * call on one device shares that device's scratch: calls that overlap on one
- * device (other streams or threads) race, so serialize them. */
+ * MI355X, so results equal nxt_paged_attention_ex's bit for bit (on a
+ * device with more CUs an automatic plan is cut to fewer wavefronts to fit:
+ * correct, but not bit-identical); a plan that needs more scratch (an
+ * explicit partition_tokens over a large batch) returns
+ * NXT_ATTN_E_UNSUPPORTED without launching.  Every call on one device
+ * shares that device's scratch, so the library orders them on the GPU: a
+ * call's stream waits for the device's previous no-alloc call (an event
+ * recorded after it; the first call on a device creates that event) unless
+ * that call went to the same queue.  The host does not block.  A call made
+ * while its stream is being captured goes into the caller's graph unordered:
+ * replays of graphs that hold no-alloc calls must not overlap one another or
+ * eager no-alloc calls on the same device (replay them on one stream, or
+ * wait for them). */
 int nxt_paged_attention_noalloc(void *out, const void *query, const void *key_cache,
                                 const void *value_cache, const int *block_tables,
                                 const int *seq_lens, int num_seqs, int num_heads,
@@ -161,7 +176,12 @@ const char *nxt_attn_last_error(void);
  * hook.  Meant for benchmarks and tracing. */
 void nxt_attn_set_trace_events(void *start_event, void *partition_done_event);
 
-/* Waits for and frees every cached split-K workspace of this process. */
+/* Waits for and frees every cached split-K and cascade workspace of this
+ * process, including the ones kept alive for captured graphs: call it only
+ * when no graph captured over an allocating entry point runs again.  The
+ * library also frees a stream's workspaces when it evicts the least
+ * recently used of more than 64 (device, stream) entries, and the
+ * hipStreamPerThread workspaces of a thread when that thread exits. */
 int nxt_attn_release_workspaces(void);
 
 /* Library version string, e.g. "xllm-hip-attn 0.1.0 gfx950". */

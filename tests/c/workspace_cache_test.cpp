@@ -14,9 +14,16 @@
 //   - a lease is smaller than requested, or its buffer is not live.
 // Threads share a stream handle, use the per-thread handle, grow their
 // workspaces with random sizes, and release by owner and by stream
-// concurrently with the calls.
+// concurrently with the calls.  Then, single-threaded:
+//   - graph capture: a capturing call that would need to grow is refused; a
+//     capturing call pins its buffer, which then survives growth, the
+//     owner- and stream-scoped releases and eviction, until release_all;
+//   - calls on 200 streams leave at most kMaxEntries entries (the least
+//     recently used are evicted, never while their buffer has pending work);
+//   - the per-thread handle's entries are gone once their threads exited.
 //
 //   g++ -std=c++17 -O2 -pthread -I xllms_amd/csrc tests/c/workspace_cache_test.cpp
+#include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 
@@ -43,16 +50,21 @@ struct Buffer {
 std::mutex g_mu;
 std::set<Buffer *> g_all;
 // queue -> pending uses (buffers) in enqueue order
-std::map<std::pair<void *, std::thread::id>, std::vector<Buffer *>> g_queues;
+thread_local bool t_capturing = false;
+// A queue: the handle, and for the per-thread handle the thread.
+using Queue = std::pair<void *, std::thread::id>;
+
+Queue queue_of(void *stream) {
+    return {stream, stream == kPerThread ? std::this_thread::get_id() : std::thread::id()};
+}
+
+// queue -> pending uses (buffers) in enqueue order
+std::map<Queue, std::vector<Buffer *>> g_queues;
 std::atomic<int> g_fail{0};
 thread_local int t_index = -1;
 
 void fail(const char *what) {
     if (g_fail.fetch_add(1) < 10) fprintf(stderr, "FAIL: %s\n", what);
-}
-
-std::pair<void *, std::thread::id> queue_of(void *stream) {
-    return {stream, stream == kPerThread ? std::this_thread::get_id() : std::thread::id()};
 }
 
 struct MockDev {
@@ -86,6 +98,7 @@ struct MockDev {
         return 0;
     }
     static bool per_thread(void *stream) { return stream == kPerThread; }
+    static bool capturing(void *) { return t_capturing; }
 };
 
 using Cache = xhip::WorkspaceCache<MockDev>;
@@ -163,16 +176,59 @@ int main() {
         });
     }
     for (auto &th : threads) th.join();
-    // per-thread handle: one entry per thread that used it, per kind
-    if (g_cache.release_owner(nullptr, true) != Cache::kOk) fail("release all");
+    // the per-thread handle's entries went with their threads; the shared
+    // handle keeps a split-K and a cascade entry
+    if (g_cache.entries() != 2) {
+        fprintf(stderr, "entries %zu, expected 2\n", g_cache.entries());
+        fail("entry count after the threads exited");
+    }
+
+    // graph capture
+    void *const cs = (void *)0x2000;
+    {
+        t_capturing = true;
+        Cache::Lease l0;
+        if (g_cache.acquire(0, cs, xhip::kWsSplitK, 4096, nullptr, &l0) != Cache::kCaptureGrow)
+            fail("a capturing call that needs a new workspace was not refused");
+        t_capturing = false;
+    }
+    Buffer *b1 = nullptr, *b2 = nullptr;
+    call(cs, xhip::kWsSplitK, 8192, nullptr);  // the warm-up call creates it
+    {
+        t_capturing = true;
+        Cache::Lease l1;
+        if (g_cache.acquire(0, cs, xhip::kWsSplitK, 4096, nullptr, &l1) != Cache::kOk)
+            fail("capturing call refused");
+        b1 = (Buffer *)l1.ptr();
+        t_capturing = false;
+    }
+    call(cs, xhip::kWsSplitK, 1 << 20, nullptr);  // grows: the graph's buffer stays
+    {
+        Cache::Lease l2;
+        (void)g_cache.acquire(0, cs, xhip::kWsSplitK, 16, nullptr, &l2);
+        b2 = (Buffer *)l2.ptr();
+    }
+    if (!b1 || !b2 || b1 == b2) fail("growth of a pinned workspace did not allocate a new buffer");
+    if (g_cache.release_owner(nullptr) != Cache::kOk) fail("release_owner");
+    g_cache.release_stream(0, cs);
+    {
+        std::lock_guard<std::mutex> g(g_mu);
+        if (!b1->live || !b2->live) fail("a buffer a captured graph holds was freed");
+    }
+    if (g_cache.kept_for_graphs() != 2) fail("pinned buffers not kept for the graphs");
+
+    // bound on the entries
+    for (int i = 0; i < 200; i++) call((void *)(uintptr_t)(0x10000 + 16 * i), xhip::kWsSplitK, 512, nullptr);
+    if (g_cache.entries() > Cache::kMaxEntries) {
+        fprintf(stderr, "entries %zu > %zu\n", g_cache.entries(), Cache::kMaxEntries);
+        fail("entry list unbounded");
+    }
+
+    if (g_cache.release_all() != Cache::kOk) fail("release all");
     for (Buffer *b : g_all)
         if (b->live) fail("a buffer is still live after releasing everything");
-    const size_t entries = g_cache.entries();
-    // shared handle: split-K + cascade; per-thread handle: one split-K per thread 3-5
-    if (entries != 5) {
-        fprintf(stderr, "entries %zu, expected 5\n", entries);
-        fail("entry count");
-    }
+    if (g_cache.entries() != 0 || g_cache.kept_for_graphs() != 0)
+        fail("entries or kept buffers left after release_all");
     printf("%s: %zu buffers allocated, %d failures\n", g_fail ? "FAILED" : "PASSED",
            g_all.size(), g_fail.load());
     return g_fail ? 1 : 0;

@@ -113,13 +113,38 @@ def test_workspace_cache_threads(tmp_path, sanitize):
     """The per-(device, stream) workspace cache under host threads, on a mock
     device that models queues of in-flight work (tests/c/workspace_cache_test.cpp):
     no device use-after-free on growth or release, no workspace shared across
-    the per-thread stream's queues, no interleaved enqueues on one handle."""
+    the per-thread stream's queues, no interleaved enqueues on one handle;
+    then graph-capture pinning, a reused stream handle, the entry bound and
+    the per-thread entries freed at thread exit."""
     exe = str(tmp_path / "workspace_cache_test")
     subprocess.run(["g++", "-std=c++17", "-O1", "-pthread", "-Wall", *sanitize,
                     f"-I{os.path.join(ROOT, 'xllms_amd', 'csrc')}", "-o", exe,
                     os.path.join(ROOT, "tests", "c", "workspace_cache_test.cpp")], check=True)
     r = subprocess.run([exe], capture_output=True, text=True, timeout=300)
     print(r.stdout, r.stderr)
+    assert r.returncode == 0 and "PASSED" in r.stdout
+    assert "WARNING: ThreadSanitizer" not in r.stderr
+
+
+@pytest.mark.parametrize("variant", [[], ["-fsanitize=thread", "-g"], ["-DPLANT_NO_WAIT"]],
+                         ids=["plain", "tsan", "planted-no-wait"])
+def test_noalloc_gate_threads(tmp_path, variant):
+    """The ordering of nxt_paged_attention_noalloc calls on one device
+    (xllms_amd/csrc/noalloc_gate.h) under host threads, on a mock device whose
+    queues and events carry vector clocks (tests/c/noalloc_gate_test.cpp):
+    every call's use of the shared scratch runs after the last one on every
+    other queue (shared, own, per-thread and null stream handles), captured
+    calls neither wait nor record, one event per device.  With the waits
+    planted out of the mock, the checker must report overlapping calls."""
+    exe = str(tmp_path / "noalloc_gate_test")
+    subprocess.run(["g++", "-std=c++17", "-O1", "-pthread", "-Wall", *variant,
+                    f"-I{os.path.join(ROOT, 'xllms_amd', 'csrc')}", "-o", exe,
+                    os.path.join(ROOT, "tests", "c", "noalloc_gate_test.cpp")], check=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=300)
+    print(r.stdout, r.stderr[-2000:])
+    if "-DPLANT_NO_WAIT" in variant:
+        assert r.returncode != 0 and "may overlap" in r.stderr
+        return
     assert r.returncode == 0 and "PASSED" in r.stdout
     assert "WARNING: ThreadSanitizer" not in r.stderr
 

@@ -116,3 +116,100 @@ def test_cascade_replays_in_a_graph(cuda, groups):
                                    dw.seq_lens, d_pg, d_pb, num_kv_heads=wl.num_kv_heads,
                                    scale=wl.scale, max_groups=groups, stream=stream)
     _replays(call, dw, _new_queries_and_lengths(wl, dw, floor))
+
+
+def test_captured_workspace_outlives_growth(cuda):
+    """A graph captured over nxt_paged_attention_ex holds its stream's
+    workspace: a larger eager call on that stream afterwards gets a new
+    buffer beside it (the old one is kept for the graph), and every replay
+    still computes what an eager call computes."""
+    import torch
+    small = W.small_case(num_seqs=8, H=32, KVH=8, D=128, kv_dtype=W.FP16, seed=61, max_len=600)
+    big = W.small_case(num_seqs=64, H=64, KVH=2, D=128, kv_dtype=W.FP16, seed=62,
+                       lens=[2000] * 64)
+    dws, dwb = W.upload(small), W.upload(big)
+    call_small, call_big = _decode_call(small, dws, "nxt_paged_attention_ex"), \
+        _decode_call(big, dwb, "nxt_paged_attention_ex")
+    s = torch.cuda.Stream()
+    out_g = torch.zeros_like(dws.out)
+    out_e = torch.zeros_like(dws.out)
+    with torch.cuda.stream(s):
+        call_small(out_g, s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s, capture_error_mode="relaxed"):
+        call_small(out_g, s)
+    torch.cuda.synchronize()
+    # grows s's workspace from the small plan's to the 32-head plan's (~65 MiB)
+    out_b = torch.zeros_like(dwb.out)
+    with torch.cuda.stream(s):
+        call_big(out_b, s)
+    torch.cuda.synchronize()
+    from oracle import oracle as O
+    from tests.helpers import assert_close
+    print("case big call after the capture", flush=True)
+    assert_close(out_b.float().cpu().numpy(), O.run_workload(big, precision="mt"), W.FP16,
+                 "big eager call")
+    mutate = _new_queries_and_lengths(small, dws)
+    rng = np.random.default_rng(9)
+    for rep in range(3):
+        mutate(rng, rep)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        out_e.zero_()
+        call_small(out_e, torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        print(f"case replay after growth {rep}", flush=True)
+        assert torch.equal(out_g, out_e), f"replay {rep} after growth differs from the eager call"
+    del g
+
+
+def test_capture_that_needs_a_new_workspace_is_refused(cuda):
+    """A call captured on a stream that has no workspace of the size it
+    needs returns NXT_ATTN_E_UNSUPPORTED and enqueues nothing (growing would
+    need a queue wait and an allocation inside the capture)."""
+    import torch
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+    raw = ctypes.c_void_p()
+    assert hip.hipStreamCreate(ctypes.byref(raw)) == 0
+    try:
+        wl = W.small_case(num_seqs=6, H=32, KVH=8, D=128, kv_dtype=W.FP16, seed=63,
+                          max_len=900)
+        dw = W.upload(wl)
+        dw.out.fill_(3.0)
+        sentinel = dw.out.clone()
+        s = torch.cuda.ExternalStream(raw.value)
+        torch.cuda.synchronize()
+        call = _decode_call(wl, dw, "nxt_paged_attention_ex")
+        lib = _lib.backend()
+        fn = lib.nxt_paged_attention_ex
+        g = torch.cuda.CUDAGraph()
+        print("case capture without a warm-up call", flush=True)
+        with torch.cuda.graph(g, stream=s, capture_error_mode="relaxed"):
+            dw.out.add_(0)
+            rc = fn(dw.out.data_ptr(), dw.query.data_ptr(), dw.key_cache.data_ptr(),
+                    dw.value_cache.data_ptr(), dw.block_tables.data_ptr(), dw.seq_lens.data_ptr(),
+                    wl.num_seqs, wl.num_heads, wl.head_size, wl.num_kv_heads,
+                    ctypes.c_float(wl.scale), wl.max_num_blocks_per_seq, wl.block_size,
+                    dw.key_cache.element_size(), dw.key_cache.stride(0), dw.key_cache.stride(1),
+                    s.cuda_stream, wl.kv_dtype, 0)
+        st, msg = PA.last_status()
+        assert rc == PA.NXT_ATTN_E_UNSUPPORTED and "capturing" in msg, (rc, msg)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(dw.out, sentinel)
+        del g
+        # outside the capture the same call works on that stream
+        with torch.cuda.stream(s):
+            call(dw.out, s)
+        torch.cuda.synchronize()
+        from oracle import oracle as O
+        from tests.helpers import assert_close
+        assert_close(dw.out.float().cpu().numpy(), O.run_workload(wl, precision="mt"), W.FP16,
+                     "eager call after the refused capture")
+    finally:
+        torch.cuda.synchronize()
+        assert hip.hipStreamDestroy(raw) == 0

@@ -19,6 +19,7 @@
 #include "paged_decode_launch.h"
 #include "paged_decode_params.h"
 #include "paged_decode_rows.h"
+#include "noalloc_gate.h"
 #include "paged_decode_scratch.h"
 #include "paged_kv_append.h"
 #include "workspace.h"
@@ -78,9 +79,35 @@ struct HipDev {
         return on_device(device, [ptr] { return hipFree(ptr); });
     }
     static bool per_thread(void *stream) { return stream == (void *)hipStreamPerThread; }
+    static bool capturing(void *stream) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess) {
+            (void)hipGetLastError();
+            return false;
+        }
+        return cs == hipStreamCaptureStatusActive;
+    }
 };
 
 using WsCache = xhip::WorkspaceCache<HipDev>;
+
+// Event calls of the no-alloc gate (noalloc_gate.h).
+struct HipGateDev {
+    static int create_event(void **ev) {
+        return hipEventCreateWithFlags((hipEvent_t *)ev, hipEventDisableTiming) == hipSuccess ? 0
+                                                                                              : 1;
+    }
+    static int record(void *ev, void *stream) {
+        return hipEventRecord((hipEvent_t)ev, (hipStream_t)stream) == hipSuccess ? 0 : 1;
+    }
+    static int wait(void *stream, void *ev) {
+        return hipStreamWaitEvent((hipStream_t)stream, (hipEvent_t)ev, 0) == hipSuccess ? 0 : 1;
+    }
+    static bool capturing(void *stream) { return HipDev::capturing(stream); }
+    static bool per_thread(void *stream) { return HipDev::per_thread(stream); }
+};
+using NoAllocGate = xhip::NoAllocGate<HipGateDev>;
+NoAllocGate g_noalloc_gate;
 using xhip::kWsCascade;
 using xhip::kWsSplitK;
 
@@ -97,6 +124,12 @@ int get_workspace(int device, hipStream_t stream, size_t bytes, WsCache::Lease *
         return set_status(NXT_ATTN_E_HIP, "hipStreamSynchronize before growing the workspace failed");
     if (rc == WsCache::kNoMemory)
         return set_status(NXT_ATTN_E_NOMEM, "workspace of %zu bytes: hipMalloc failed", bytes);
+    if (rc == WsCache::kCaptureGrow)
+        return set_status(NXT_ATTN_E_UNSUPPORTED,
+                          "stream is capturing and this call needs a %zu-byte workspace the stream "
+                          "does not have yet: make one call of this shape on the stream before "
+                          "the capture (or use nxt_paged_attention_noalloc)",
+                          bytes);
     return NXT_ATTN_OK;
 }
 
@@ -454,14 +487,31 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         // workspace: fp32 partials o, their (m, l), the unit prefix; under a
         // split segment launch, one partial per workgroup
         const size_t pre_bytes = seg_launch ? 0 : (size_t)(nseq + 1) * sizeof(int);
-        const long long slots = seg_launch ? (seg_split > 1 ? nseq * segs * seg_split : 0)
-                                           : 2 * waves;
+        long long slots = seg_launch ? (seg_split > 1 ? nseq * segs * seg_split : 0)
+                                     : 2 * waves;
         auto o_size = [&](long long n) {
             return ((size_t)n * tiling.head_tile * head_size * sizeof(float) + 255) & ~(size_t)255;
         };
         auto ml_size = [&](long long n) {
             return ((size_t)n * tiling.head_tile * 2 * sizeof(float) + 255) & ~(size_t)255;
         };
+        if (fixed && partition_tokens == 0 && !seg_launch &&
+            o_size(slots) + ml_size(slots) + pre_bytes > fixed->bytes) {
+            // An automatic plan larger than the fixed scratch (a device with
+            // more CUs than the scratch was sized for): fewer wavefronts, each
+            // with a longer range.  Correct, though its cut points (and so
+            // the last bits of the result) differ from the allocating entry
+            // points' plan.
+            const size_t per_wave =
+                2 * (size_t)tiling.head_tile * ((size_t)head_size + 2) * sizeof(float);
+            const int wpg = waves_per_group(mfma);
+            const size_t room = fixed->bytes > pre_bytes + 512 ? fixed->bytes - pre_bytes - 512 : 0;
+            long long w = (long long)(room / per_wave) / wpg * wpg;
+            if (w >= wpg && w < waves) {
+                waves = w;
+                slots = 2 * waves;
+            }
+        }
         if (fixed && o_size(slots) + ml_size(slots) + pre_bytes > fixed->bytes)
             return set_status(NXT_ATTN_E_UNSUPPORTED,
                               "this plan needs %zu bytes of split-K scratch; the allocation-free "
@@ -997,10 +1047,18 @@ __attribute__((visibility("default"))) int nxt_paged_attention_noalloc(
     if (e != hipSuccess)
         return set_status(NXT_ATTN_E_HIP, "scratch address of device %d: %s", device,
                           hipGetErrorString(e));
-    return run(out, query, key_cache, value_cache, block_tables, seq_lens, num_seqs, num_heads,
-               head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size, dtype_size,
-               kv_block_stride, kv_head_stride, stream, kv_dtype, partition_tokens, nullptr,
-               nullptr, &fixed);
+    // calls on one device run one after another on the GPU (noalloc_gate.h)
+    NoAllocGate::Pass pass;
+    if (g_noalloc_gate.enter(device, stream, &pass) != NoAllocGate::kOk)
+        return set_status(NXT_ATTN_E_HIP,
+                          "ordering after the device's previous no-alloc call failed");
+    const int rc = run(out, query, key_cache, value_cache, block_tables, seq_lens, num_seqs,
+                       num_heads, head_size, num_kv_heads, scale, max_num_blocks_per_seq,
+                       block_size, dtype_size, kv_block_stride, kv_head_stride, stream, kv_dtype,
+                       partition_tokens, nullptr, nullptr, &fixed);
+    if (pass.done() != NoAllocGate::kOk && rc == NXT_ATTN_OK)
+        return set_status(NXT_ATTN_E_HIP, "recording the no-alloc call's completion event failed");
+    return rc;
 }
 
 __attribute__((visibility("default"))) int nxt_paged_attention_auto_waves(
@@ -1204,7 +1262,7 @@ __attribute__((visibility("default"))) void nxt_attn_set_trace_events(void *star
 }
 
 __attribute__((visibility("default"))) int nxt_attn_release_workspaces(void) {
-    return g_ws.release_owner(nullptr, true) == WsCache::kOk ? NXT_ATTN_OK : NXT_ATTN_E_HIP;
+    return g_ws.release_all() == WsCache::kOk ? NXT_ATTN_OK : NXT_ATTN_E_HIP;
 }
 
 const void *xhip_set_workspace_owner(const void *owner) {

@@ -33,6 +33,7 @@ constexpr unsigned long long kWgTraceBufferWords = kWgTraceMergeBase + 2 * kWgTr
 
 #if defined(XHIP_WG_TRACE) && XHIP_WG_TRACE
 #define XHIP_TRACING 1
+#ifdef __HIPCC__
 namespace xhip {
 // The workgroup's record, in LDS until it exits.
 __device__ __forceinline__ unsigned long long *wg_trace_lds() {
@@ -40,6 +41,7 @@ __device__ __forceinline__ unsigned long long *wg_trace_lds() {
     return rec;
 }
 }  // namespace xhip
+#endif
 // at kernel entry: the record cleared, the entry stamped
 #define XHIP_WG_BEGIN(p)                                                                       \
     do {                                                                                       \
