@@ -635,12 +635,21 @@ def wg_trace_report(args, wl, lib, step, i0, stream, ms_per_step, alg_bytes, ent
     us = lambda x: (np.asarray(x, dtype=np.int64) - t0) / 100.0  # noqa: E731
     info = part[:, 3]
     role = (info >> 32) & 0xFF
-    entry_us, pro_us, exit_us = us(part[:, 0]), us(part[:, 1]), us(part[:, 2])
+    entry_us, exit_us = us(part[:, 0]), us(part[:, 2])
     groups = np.nonzero(used)[0]
+    # the segment kernel stamps wavefront 0's first and last tile in [7], [8]
+    # and has no prologue stamp; the MFMA kernels stamp every wavefront
+    segment = not (part[:, 4] > 0).any() and bool((part[:, 7] > 0).any())
     lines = []
     lines.append(f"# Per-workgroup timeline: {wl.name}" + (" (cascade)" if args.cascade else ""))
     lines.append("")
-    lines.append(f"Command: `python bench.py {' '.join(sys.argv[1:])}`")
+    argv = list(sys.argv[1:])
+    for i, a in enumerate(argv):  # the output path stands as <out>.md
+        if a == "--wg-trace" and i + 1 < len(argv):
+            argv[i + 1] = "<out>.md"
+        elif a.startswith("--wg-trace="):
+            argv[i] = "--wg-trace=<out>.md"
+    lines.append(f"Command: `python bench.py {' '.join(argv)}`")
     lines.append("")
     lines.append(f"Instrumented build `libxllm_hip_backend_trace.so` (XHIP_WG_TRACE, "
                  f"`xllms_amd/csrc/wg_trace.h`): s_memrealtime stamps (100 MHz) per workgroup "
@@ -656,19 +665,24 @@ def wg_trace_report(args, wl, lib, step, i0, stream, ms_per_step, alg_bytes, ent
     lines.append("|---|---|---|---|---|---|---|")
     for r in sorted(set(role.tolist())):
         sel = role == r
-        wf = part[sel][:, 4:16].reshape(-1, 4, 3)
-        ft = wf[:, :, 0].ravel()
-        le = wf[:, :, 1].ravel()
+        if segment:
+            ft, le = part[sel][:, 7], part[sel][:, 8]
+        else:
+            wf = part[sel][:, 4:16].reshape(-1, 4, 3)
+            ft = wf[:, :, 0].ravel()
+            le = wf[:, :, 1].ravel()
         ft_us, le_us = us(ft[ft > 0]), us(le[le > 0])
+        pro = part[sel][:, 1]
+        pro_us = us(pro[pro > 0])
         row = {"n": int(sel.sum()),
                "entry": [_pct(entry_us[sel], 50), _pct(entry_us[sel], 100)],
-               "prologue_done": [_pct(pro_us[sel], q) for q in (50, 90, 100)],
+               "prologue_done": [_pct(pro_us, q) for q in (50, 90, 100)],
                "first_tile": [_pct(ft_us, 50), _pct(ft_us, 100)],
                "last_tile_done": [_pct(le_us, q) for q in (10, 50, 90, 100)],
                "exit": [_pct(exit_us[sel], q) for q in (10, 50, 90, 100)]}
         summary[roles.get(r, str(r))] = row
         lines.append(f"| {roles.get(r, str(r))} | {row['n']} | {row['entry'][0]} / {row['entry'][1]} | "
-                     f"{' / '.join(map(str, row['prologue_done']))} | "
+                     f"{' / '.join(map(str, row['prologue_done'])) if row['prologue_done'][0] is not None else 'n/a'} | "
                      f"{row['first_tile'][0]} / {row['first_tile'][1]} | "
                      f"{' / '.join(map(str, row['last_tile_done']))} | "
                      f"{' / '.join(map(str, row['exit']))} |")
@@ -683,22 +697,27 @@ def wg_trace_report(args, wl, lib, step, i0, stream, ms_per_step, alg_bytes, ent
     lines.append("")
     lines.append("Exit by XCD (workgroup b runs on XCD b % 8), p50 / max: " + ", ".join(
         f"{x}: {_pct(exit_us[xcd == x], 50)} / {_pct(exit_us[xcd == x], 100)}" for x in range(8)))
-    # streaming rate per wavefront: tiles x bytes per tile / (last tile done - first tile)
-    tile_bytes = 16 * wl.head_size * wl.elem_bytes * 2
-    wf = part[:, 4:16].reshape(-1, 4, 3).reshape(-1, 3)
-    ok = (wf[:, 0] > 0) & (wf[:, 1] > wf[:, 0])
-    tiles = wf[ok, 2] & 0xFFFFFFFF
-    pieces = wf[ok, 2] >> 32
-    dur = (wf[ok, 1] - wf[ok, 0]) / 100.0
-    rate = tiles * tile_bytes / np.maximum(dur, 1e-3) / 1e3  # GB/s
-    lines.append("")
-    lines.append(f"Wavefronts with tiles: {int(ok.sum())}; tiles per wavefront p10 / p50 / max "
-                 f"{_pct(tiles, 10)} / {_pct(tiles, 50)} / {_pct(tiles, 100)}; pieces p50 / max "
-                 f"{_pct(pieces, 50)} / {_pct(pieces, 100)}; per-wavefront K/V rate (first tile "
-                 f"issued to last tile done) p10 / p50 / p90 {_pct(rate, 10)} / {_pct(rate, 50)} / "
-                 f"{_pct(rate, 90)} GB/s.")
-    summary["tiles_per_wave"] = [_pct(tiles, 10), _pct(tiles, 50), _pct(tiles, 100)]
-    summary["wave_rate_gbs"] = [_pct(rate, 10), _pct(rate, 50), _pct(rate, 90)]
+    if segment:
+        lines.append("")
+        lines.append("Segment kernel (one workgroup per segment or share of one): first tile and "
+                     "last tile done are wavefront 0's; no prologue stamp (no split-unit scan).")
+    else:
+        # streaming rate per wavefront: tiles x bytes per tile / (last tile done - first tile)
+        tile_bytes = 16 * wl.head_size * wl.elem_bytes * 2
+        wf = part[:, 4:16].reshape(-1, 4, 3).reshape(-1, 3)
+        ok = (wf[:, 0] > 0) & (wf[:, 1] > wf[:, 0])
+        tiles = wf[ok, 2] & 0xFFFFFFFF
+        pieces = wf[ok, 2] >> 32
+        dur = (wf[ok, 1] - wf[ok, 0]) / 100.0
+        rate = tiles * tile_bytes / np.maximum(dur, 1e-3) / 1e3  # GB/s
+        lines.append("")
+        lines.append(f"Wavefronts with tiles: {int(ok.sum())}; tiles per wavefront p10 / p50 / max "
+                     f"{_pct(tiles, 10)} / {_pct(tiles, 50)} / {_pct(tiles, 100)}; pieces p50 / max "
+                     f"{_pct(pieces, 50)} / {_pct(pieces, 100)}; per-wavefront K/V rate (first tile "
+                     f"issued to last tile done) p10 / p50 / p90 {_pct(rate, 10)} / {_pct(rate, 50)} / "
+                     f"{_pct(rate, 90)} GB/s.")
+        summary["tiles_per_wave"] = [_pct(tiles, 10), _pct(tiles, 50), _pct(tiles, 100)]
+        summary["wave_rate_gbs"] = [_pct(rate, 10), _pct(rate, 50), _pct(rate, 90)]
     if len(merge):
         me, mx = us(merge[:, 0]), us(merge[:, 1][merge[:, 1] > 0])
         summary["merge"] = {"entry": [_pct(me, 0), _pct(me, 50), _pct(me, 100)],
