@@ -60,6 +60,7 @@ class HipEvents:
         self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
         self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         self.hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.hip.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
         self.events = []
 
     def create(self) -> int:
@@ -81,6 +82,11 @@ class HipEvents:
         if rc != 0:
             raise RuntimeError(f"hipEventElapsedTime failed: {rc}")
         return ms.value
+
+    def sync(self, stream: int) -> None:
+        rc = self.hip.hipStreamSynchronize(stream)
+        if rc != 0:
+            raise RuntimeError(f"hipStreamSynchronize failed: {rc}")
 
     def destroy_all(self) -> None:
         for ev in self.events:
@@ -466,6 +472,99 @@ def bench_activation(args) -> int:
     return 0 if ok else 1
 
 
+def bare_decode_step_us(wl, steps: int, warmup: int) -> float:
+    """Step time of one nxt_paged_attention call over the workload, with its
+    inputs resident in HBM (>= 3 rotated K/V pools, HIP events around `steps`
+    back-to-back calls): the bare attention of a batch the serving path also
+    runs."""
+    import torch
+    from xllms_amd import paged_attention as PA
+    from xllms_amd import workloads as W
+    dw = W.upload(wl, "cuda")
+    pool_bytes = 2 * dw.key_cache.numel() * dw.key_cache.element_size()
+    pools = max(3, -(-768 * 2**20 // pool_bytes))
+    kp, vp = [dw.key_cache], [dw.value_cache]
+    for _ in range(pools - 1):
+        kp.append(dw.key_cache.clone())
+        vp.append(dw.value_cache.clone())
+    stream = torch.cuda.current_stream().cuda_stream
+    lib = PA._lib.backend()
+    fn = lib.nxt_paged_attention_ex
+    calls = [(dw.out.data_ptr(), dw.query.data_ptr(), k.data_ptr(), v.data_ptr(),
+              dw.block_tables.data_ptr(), dw.seq_lens.data_ptr(), wl.num_seqs, wl.num_heads,
+              wl.head_size, wl.num_kv_heads, ctypes.c_float(wl.scale), wl.max_num_blocks_per_seq,
+              wl.block_size, wl.elem_bytes, wl.kv_block_stride, wl.kv_head_stride, stream,
+              wl.kv_dtype, 0) for k, v in zip(kp, vp)]
+    for i in range(warmup):
+        fn(*calls[i % pools])
+    ev = HipEvents()
+    a, b = ev.create(), ev.create()
+    torch.cuda.synchronize()
+    ev.record(a, stream)
+    for i in range(steps):
+        fn(*calls[i % pools])
+    ev.record(b, stream)
+    torch.cuda.synchronize()
+    st, msg = PA.last_status()
+    if st != 0:
+        raise RuntimeError(f"bare decode step failed: {msg}")
+    us = ev.elapsed_ms(a, b) / steps * 1e3
+    ev.destroy_all()
+    del dw, kp, vp, calls
+    torch.cuda.empty_cache()
+    return us
+
+
+def launch_floor(wl1, reps: int = 200) -> dict:
+    """What a synchronous exec cannot go below on this runtime, timed on the
+    host from Python (each figure includes one ctypes call, ~0.5 us): one
+    near-empty kernel launch followed by hipStreamSynchronize, and one bare
+    nxt_paged_attention call over the one-sequence workload wl1 followed by
+    hipStreamSynchronize.  Medians of `reps`."""
+    import numpy as np
+    import torch
+    from xllms_amd import _lib
+    from xllms_amd import paged_attention as PA
+    from xllms_amd import workloads as W
+    stream = torch.cuda.current_stream().cuda_stream
+    ev = HipEvents()
+    probe = _lib.stream_probe()
+    dummy = torch.zeros(64, dtype=torch.int64, device="cuda")
+    sink = torch.empty(64 * 64, dtype=torch.int32, device="cuda")
+    def empty():
+        # no tiles: 16 workgroups that only store their word
+        if probe.xllm_stream_probe(dummy.data_ptr(), dummy.data_ptr(), dummy.data_ptr(), 0, 4096,
+                                   64, sink.data_ptr(), stream) != 0:
+            raise RuntimeError("xllm_stream_probe failed")
+    dw = W.upload(wl1, "cuda")
+    lib = PA._lib.backend()
+    a = (dw.out.data_ptr(), dw.query.data_ptr(), dw.key_cache.data_ptr(),
+         dw.value_cache.data_ptr(), dw.block_tables.data_ptr(), dw.seq_lens.data_ptr(),
+         wl1.num_seqs, wl1.num_heads, wl1.head_size, wl1.num_kv_heads, ctypes.c_float(wl1.scale),
+         wl1.max_num_blocks_per_seq, wl1.block_size, wl1.elem_bytes, wl1.kv_block_stride,
+         wl1.kv_head_stride, stream, wl1.kv_dtype, 0)
+    def attention():
+        lib.nxt_paged_attention_ex(*a)
+    out = {}
+    for key, fn in (("empty_launch_sync_us", empty), ("one_request_attention_sync_us", attention)):
+        for _ in range(20):
+            fn()
+            ev.sync(stream)
+        t = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ev.sync(stream)
+            t.append(time.perf_counter() - t0)
+        out[key] = round(float(np.median(t)) * 1e6, 1)
+    st, msg = PA.last_status()
+    if st != 0:
+        raise RuntimeError(f"attention call failed: {msg}")
+    out["one_request_tokens"] = int(wl1.seq_lens[0])
+    ev.destroy_all()
+    return out
+
+
 def bench_serve(args) -> int:
     """Decode steps through the plugin's model instance: the path the
     reference scheduler's poll reaches (src/core/scheduler.c:482-486,
@@ -540,6 +639,9 @@ def bench_serve(args) -> int:
 
     # one exec over the whole batch
     times = run_steps(lambda: m.exec_requests(batch))
+    # every step appends one token per request: the timed execs attend over
+    # the prompt lengths plus warmup + 1 .. warmup + steps tokens
+    mid_lens = lens + args.warmup + args.steps // 2 + 1
     per_request = None
     if args.per_request:
         # the reference scheduler's pattern: one instance_exec(.., 1) per
@@ -580,6 +682,23 @@ def bench_serve(args) -> int:
     exec_count = int(m.model.instances[0].exec_count)
     med = float(np.median(times))
     m.close()
+    del m
+    torch.cuda.empty_cache()
+    # The same batch's bare attention step (one nxt_paged_attention call over
+    # a synthetic batch of the timed execs' middle lengths; plain-decode
+    # configs), and the launch floor of a synchronous exec on this runtime.
+    bare = floor = None
+    if args.config != 5:
+        rng_b = np.random.default_rng(11)
+        wl_mid = W._make(f"{name}-serve-mid", 11, mid_lens, H=H, KVH=KVH, D=D, bs=bs,
+                         kv_dtype=kv_dtype, pool_factor=1, rng=rng_b, poison=False)
+        bare = {"step_us": round(bare_decode_step_us(wl_mid, 200, 200), 1),
+                "context_tokens": int(mid_lens.sum())}
+        log(f"[bench] bare attention step over the timed execs' middle lengths: {bare}")
+        wl1 = W._make(f"{name}-one-request", 12, [int(np.round(mid_lens.mean()))], H=H, KVH=KVH,
+                      D=D, bs=bs, kv_dtype=kv_dtype, pool_factor=1, rng=rng_b, poison=False)
+        floor = launch_floor(wl1)
+        log(f"[bench] launch floor (host-timed from Python): {floor}")
     log(f"[bench] serve {name}: {nreq} requests, prefill {t_prefill:.2f} s; decode exec median "
         f"{med * 1e6:.1f} us (min {min(times) * 1e6:.1f}, max {max(times) * 1e6:.1f}); "
         f"finite outputs: {ok}")
@@ -598,6 +717,10 @@ def bench_serve(args) -> int:
         "exec_us": {"median": round(med * 1e6, 1), "min": round(min(times) * 1e6, 1),
                     "max": round(max(times) * 1e6, 1)},
         "instance_exec_count": exec_count,
+        "context_tokens_at_timed_middle": int(mid_lens.sum()),
+        **({"bare_step_same_lengths": bare} if bare else {}),
+        **({"exec_over_bare_step": round(med * 1e6 / bare["step_us"], 3)} if bare else {}),
+        **({"launch_floor": floor} if floor else {}),
         **({"per_request": per_request} if per_request else {}),
         "check": {"outputs_finite": ok}}), flush=True)
     return 0 if ok else 1
