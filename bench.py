@@ -623,55 +623,59 @@ def bench_serve(args) -> int:
             m.bind(rid, tokens=[int(toks[i])], key=kv_new[0, i:i + 1], value=kv_new[1, i:i + 1],
                    query=q[i], output=out[i])
 
-    def run_steps(step_fn):
-        """Median host time of one decode step (the native calls only)."""
-        times = []
-        for step in range(args.warmup + args.steps):
-            bind_step()
-            t0 = time.perf_counter()
-            rc = step_fn()
-            dt = time.perf_counter() - t0
-            if rc != 0:
-                raise RuntimeError(f"exec failed at step {step}")
-            if step >= args.warmup:
-                times.append(dt)
-        return times
+    exec_fn, inst = m.dl.nxt_model_instance_exec, m.instance
+    one_args = [(one[4], one[3]) for one in singles]
 
-    # one exec over the whole batch
-    times = run_steps(lambda: m.exec_requests(batch))
-    # every step appends one token per request: the timed execs attend over
-    # the prompt lengths plus warmup + 1 .. warmup + steps tokens
-    mid_lens = lens + args.warmup + args.steps // 2 + 1
-    per_request = None
-    if args.per_request:
+    def sync_step():
         # the reference scheduler's pattern: one instance_exec(.., 1) per
-        # request (scheduler.c:477-488), each synchronous ...  (The loop calls
+        # request (scheduler.c:477-488), each synchronous.  (The loop calls
         # the C entry point with prebuilt arguments: the reference's
         # scheduler is C, and Python's per-call overhead, ~0.5 us, is not
         # part of the pattern.)
-        exec_fn, inst = m.dl.nxt_model_instance_exec, m.instance
-        one_args = [(one[4], one[3]) for one in singles]
+        for ptr, n in one_args:
+            rc = exec_fn(inst, ptr, n)
+            if rc != 0:
+                return rc
+        return 0
 
-        def sync_step():
-            for ptr, n in one_args:
-                rc = exec_fn(inst, ptr, n)
-                if rc != 0:
-                    return rc
-            return 0
-        t_sync = run_steps(sync_step)
-        # ... and the same calls in deferred mode, then one flush per step
-        assert m.set_deferred(True) == 0
+    def deferred_step():
+        # the same calls in deferred mode, then one flush
+        for ptr, n in one_args:
+            rc = exec_fn(inst, ptr, n)
+            if rc != 0:
+                return rc
+        return m.flush()
 
-        def deferred_step():
-            for ptr, n in one_args:
-                rc = exec_fn(inst, ptr, n)
-                if rc != 0:
-                    return rc
-            return m.flush()
-        t_def = run_steps(deferred_step)
-        assert m.set_deferred(False) == 0
+    # one exec over the whole batch; with --per-request the three modes take
+    # turns step by step, so each sees the same batch (every step appends a
+    # token per request)
+    modes = [("whole", lambda: m.exec_requests(batch))]
+    if args.per_request:
+        modes += [("synchronous", sync_step), ("deferred", deferred_step)]
+    timed = {key: [] for key, _ in modes}
+    for step in range(args.warmup + args.steps):
+        for key, fn in modes:
+            if key == "deferred":
+                assert m.set_deferred(True) == 0
+            bind_step()
+            t0 = time.perf_counter()
+            rc = fn()
+            dt = time.perf_counter() - t0
+            if key == "deferred":
+                assert m.set_deferred(False) == 0
+            if rc != 0:
+                raise RuntimeError(f"{key} exec failed at step {step}")
+            if step >= args.warmup:
+                timed[key].append(dt)
+    times = timed["whole"]
+    # the timed execs attend over the prompt lengths plus (phases per step) x
+    # (steps so far) + 1 tokens; the middle one:
+    mid_lens = lens + phases * (args.warmup + args.steps // 2) + 1
+    per_request = None
+    if args.per_request:
         per_request = {}
-        for key, t in (("synchronous", t_sync), ("deferred", t_def)):
+        for key in ("synchronous", "deferred"):
+            t = timed[key]
             md = float(np.median(t))
             per_request[key] = {"seqs_per_s": round(nreq / md, 1),
                                 "step_us": {"median": round(md * 1e6, 1),
@@ -687,18 +691,20 @@ def bench_serve(args) -> int:
     # The same batch's bare attention step (one nxt_paged_attention call over
     # a synthetic batch of the timed execs' middle lengths; plain-decode
     # configs), and the launch floor of a synchronous exec on this runtime.
-    bare = floor = None
+    # (Config 5's batch shares pages through the index, which a synthetic
+    # batch of the same lengths would not: no bare step there.)
+    bare = None
+    rng_b = np.random.default_rng(11)
     if args.config != 5:
-        rng_b = np.random.default_rng(11)
         wl_mid = W._make(f"{name}-serve-mid", 11, mid_lens, H=H, KVH=KVH, D=D, bs=bs,
                          kv_dtype=kv_dtype, pool_factor=1, rng=rng_b, poison=False)
         bare = {"step_us": round(bare_decode_step_us(wl_mid, 200, 200), 1),
                 "context_tokens": int(mid_lens.sum())}
         log(f"[bench] bare attention step over the timed execs' middle lengths: {bare}")
-        wl1 = W._make(f"{name}-one-request", 12, [int(np.round(mid_lens.mean()))], H=H, KVH=KVH,
-                      D=D, bs=bs, kv_dtype=kv_dtype, pool_factor=1, rng=rng_b, poison=False)
-        floor = launch_floor(wl1)
-        log(f"[bench] launch floor (host-timed from Python): {floor}")
+    wl1 = W._make(f"{name}-one-request", 12, [int(np.round(mid_lens.mean()))], H=H, KVH=KVH,
+                  D=D, bs=bs, kv_dtype=kv_dtype, pool_factor=1, rng=rng_b, poison=False)
+    floor = launch_floor(wl1)
+    log(f"[bench] launch floor (host-timed from Python): {floor}")
     log(f"[bench] serve {name}: {nreq} requests, prefill {t_prefill:.2f} s; decode exec median "
         f"{med * 1e6:.1f} us (min {min(times) * 1e6:.1f}, max {max(times) * 1e6:.1f}); "
         f"finite outputs: {ok}")
