@@ -655,14 +655,15 @@ __device__ __forceinline__ void absorb_partial(const DecodeParams &p, int slot, 
 // piece's loads, which share the memory counter; every wavefront ends with
 // one), measured at 8.6 us of a 76 us kernel.  Instead: a cut first piece
 // followed by more pieces goes to the wavefront's LDS slot; the last piece's
-// state stays in registers; at the end, from the workgroup's last wavefront
-// down to its first, a wavefront whose last piece continues into its right
-// neighbour absorbs that neighbour's slot, then either relays the merged
-// state to its own slot (its piece is a continuation from its left
-// neighbour) or, as the leftmost holder of the segment in the workgroup,
-// writes it: finished rows when the whole segment lay in the workgroup,
-// else one partial.  The first wavefront's cut first piece (its left
-// neighbour is in another workgroup) is written as a partial directly.
+// state stays in registers; at the end, a last piece that continues the
+// left neighbour's goes to the slot too, and after one workgroup barrier
+// the leftmost holder of each segment in the workgroup absorbs the slots of
+// the neighbours its piece continues into and writes it: finished rows when
+// the whole segment lay in the workgroup, else one partial.  (A sweep from
+// the last wavefront down to the first, one barrier per wavefront, kept the
+// workgroup ~1.8 us past its last tile, measured on MI355X.)  The first
+// wavefront's cut first piece (its left neighbour is in another workgroup)
+// is written as a partial directly.
 // Mode 2 (two row blocks) keeps one relay slot per workgroup: cut first
 // pieces followed by more pieces are written as partials by every
 // wavefront, and a left neighbour absorbs such a partial from memory (the
@@ -895,30 +896,30 @@ __device__ __forceinline__ void mfma_partition_body(
         }
     }
     if constexpr (FIX == 1) {
-        // From the workgroup's last wavefront down to its first (the
-        // wavefronts of a workgroup hold consecutive ranges).
+        // The wavefronts of a workgroup hold consecutive ranges.  First, a
+        // wavefront whose last piece continues its left neighbour's (cut at
+        // the start; its range is that one piece) puts the state in its slot,
+        // as a cut first piece followed by more pieces already did in the
+        // loop.  Then, after one barrier, the leftmost holder of each
+        // segment in the workgroup absorbs the slots of the neighbours its
+        // piece continues into, left to right, and writes the segment:
+        // finished rows when it lay in the workgroup, else one partial.
+        const bool cut_start = have_last && pc.t_begin > 0;
+        if (have_last && cut_start && wave > 0) {
+            fix_store<D>(sm.sw.fix[wave], lane, st[0]);
+            if (lane == 0) sm.sw.fix[wave].ends = pc.t_end >= pc.L ? 1 : 0;
+        }
         __syncthreads();
-        for (int i = NW - 1; i >= 0; i--) {
-            if (wave == i && have_last) {
-                const bool cut_start = pc.t_begin > 0;
-                bool ends = pc.t_end >= pc.L;
-                if (!ends && i < NW - 1) {
-                    // the right neighbour's first piece continues this
-                    // segment: its state is in its slot (stored during its
-                    // range, or relayed by it one step ago)
-                    fix_absorb<D>(sm.sw.fix[i + 1], lane, st[0]);
-                    ends = sm.sw.fix[i + 1].ends != 0;
-                }
-                if (cut_start && i > 0) {
-                    fix_store<D>(sm.sw.fix[i], lane, st[0]);
-                    if (lane == 0) sm.sw.fix[i].ends = ends ? 1 : 0;
-                } else if (!cut_start && ends) {
-                    mfma_write_rows<KV, D, R, HS>(p, pc, lane, st);
-                } else {
-                    mfma_write_partial<D, R, HS>(p, pc, lane, st);
-                }
+        if (have_last && !(cut_start && wave > 0)) {
+            bool ends = pc.t_end >= pc.L;
+            for (int j = wave + 1; !ends && j < NW; j++) {
+                fix_absorb<D>(sm.sw.fix[j], lane, st[0]);
+                ends = sm.sw.fix[j].ends != 0;
             }
-            __syncthreads();
+            if (!cut_start && ends)
+                mfma_write_rows<KV, D, R, HS>(p, pc, lane, st);
+            else
+                mfma_write_partial<D, R, HS>(p, pc, lane, st);
         }
     }
 }
