@@ -312,33 +312,36 @@ __device__ __forceinline__ void absorb_row(float lse, const f32x4 &row, float &m
     m = M;
 }
 
-// Where the state of a segment of batch p is: its partials (true, slots in
-// ps) when the partition left the segment cut, else its finished row.  seg
-// is the segment's index within its sequence; pair_ht >= 0: p's head tiles
-// are paired (DecodeParams::pair_tiles) and the state is head tile
-// pair_ht's.
-__device__ __forceinline__ bool segment_cut(const DecodeParams &p, int L, int seg, int pre_s,
-                                            int total, int waves, PartialSlots &ps,
-                                            int pair_ht = -1) {
+// The state of one float4 column of a segment of batch p: its partials when
+// the partition left the segment cut, else its finished row.  seg is the
+// segment's index within its sequence, hrow the column's head in the
+// segment's tile (GT heads), c the float4 column in the head; pair_ht >= 0:
+// p's head tiles are paired (DecodeParams::pair_tiles) and the column is in
+// head tile pair_ht.  HS: the states are fp16 (DecodeParams::out_h, ws_h).
+template <int GT, int D, bool HS>
+__device__ __forceinline__ void segment_state(const DecodeParams &p, int s, int L, int seg,
+                                              int pre_s, int total, int waves, size_t row, int hrow,
+                                              int c, float &m, float &l, f32x4 &acc,
+                                              int pair_ht = -1) {
     const int Ts = (L + 15) / 16;
     const int seg_start = pre_s + seg * segment_units(p, Ts);
-    return pair_ht >= 0
-               ? segment_partials_paired(seg_start, seg_start + p.seg_cost, Ts,
-                                         tiles_per_wave(total, waves >> 1, p.min_tiles_per_wave),
-                                         pair_ht, ps)
-               : segment_partials<kMfmaWavesPerGroup>(
-                     p, seg_start, seg_start + p.seg_cost, Ts,
-                     tiles_per_wave(total, waves, p.min_tiles_per_wave), ps);
-}
-
-// One float4 column c of the finished row `row` of batch p and its
-// log-sum-exp.  HS: fp16 states (DecodeParams::out_h).
-template <int D, bool HS>
-__device__ __forceinline__ void load_row_state(const DecodeParams &p, size_t row, int c, float &lse,
-                                               f32x4 &o) {
-    lse = p.out_lse[row];
-    o = HS ? unpack_h4(*(const u32x2 *)((const char *)p.out_h + (row * D + c * 4) * 2))
-           : *(const f32x4 *)(p.out_f32 + row * D + c * 4);
+    PartialSlots ps;
+    const bool cut =
+        pair_ht >= 0
+            ? segment_partials_paired(seg_start, seg_start + p.seg_cost, Ts,
+                                      tiles_per_wave(total, waves >> 1, p.min_tiles_per_wave),
+                                      pair_ht, ps)
+            : segment_partials<kMfmaWavesPerGroup>(
+                  p, seg_start, seg_start + p.seg_cost, Ts,
+                  tiles_per_wave(total, waves, p.min_tiles_per_wave), ps);
+    if (cut) {
+        merge_partials<GT, D, 8, HS>(p, ps, 0, 1, hrow * 2, hrow * D + c * 4, m, l, acc);
+    } else {
+        const float lse = p.out_lse[row];
+        const f32x4 o = HS ? unpack_h4(*(const u32x2 *)((const char *)p.out_h + (row * D + c * 4) * 2))
+                           : *(const f32x4 *)(p.out_f32 + row * D + c * 4);
+        absorb_row(lse, o, m, l, acc);
+    }
 }
 
 // Merge over every suffix segment (sequence s, kv head, head tile of GTS
@@ -386,40 +389,22 @@ __global__ __launch_bounds__(NT) void paged_decode_cascade_merge_kernel(
     const size_t srow0 = (size_t)s * ps.num_heads + (size_t)kvh * ps.group + g0;
     for (int col = threadIdx.x; col < ncols; col += NT) {
         const int h = col / C4, c = col - h * C4;
-        // Both states are located first and every load that needs no
-        // further lookup is issued before any is used: a finished row's with
-        // the other state's partials, so the column takes one round trip
-        // unless both states are cut.
-        PartialSlots sps, pps;
-        bool s_cut = false, p_has = false, p_cut = false;
-        float s_lse = -INFINITY, p_lse = -INFINITY;
-        f32x4 s_o = {0.0f, 0.0f, 0.0f, 0.0f}, p_o = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (Ls > 0) {
-            s_cut = segment_cut(ps, Ls, seg, pre_s, tot_s, (G - gp) * NW, sps);
-            if (!s_cut) load_row_state<D, HS>(ps, srow0 + h, c, s_lse, s_o);
-        }
-        int p_hrow = 0;
+        float m = -INFINITY, l = 0.0f;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (Ls > 0)
+            segment_state<GTS, D, HS>(ps, s, Ls, seg, pre_s, tot_s, (G - gp) * NW, srow0 + h, h,
+                                      c, m, l, acc);
         if (fb >= 0) {
             const int q = fb + g0 + h;
             const int v = q / rows, j = q - v * rows;
             const int Lv = v_lds ? l_vlen[v] : seq_len_of(pp, v);
             if (Lv > 0) {
                 const int htp = j / GTP;
-                p_has = true;
-                p_hrow = j - htp * GTP;
-                p_cut = segment_cut(pp, Lv, kvh, v_lds ? l_vpre[v] : pp.ws_prefix[v], tot_p,
-                                    gp * NW, pps, htp);
-                if (!p_cut)
-                    load_row_state<D, HS>(pp, (size_t)v * pp.num_heads + (size_t)kvh * rows + j,
-                                          c, p_lse, p_o);
+                const size_t prow = (size_t)v * pp.num_heads + (size_t)kvh * rows + j;
+                segment_state<GTP, D, HS>(pp, v, Lv, kvh, v_lds ? l_vpre[v] : pp.ws_prefix[v],
+                                          tot_p, gp * NW, prow, j - htp * GTP, c, m, l, acc, htp);
             }
         }
-        float m = -INFINITY, l = 0.0f;
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (p_cut) merge_partials<GTP, D, 8, HS>(pp, pps, 0, 1, p_hrow * 2, p_hrow * D + c * 4, m, l, acc);
-        if (s_cut) merge_partials<GTS, D, 8, HS>(ps, sps, 0, 1, h * 2, h * D + c * 4, m, l, acc);
-        if (Ls > 0 && !s_cut) absorb_row(s_lse, s_o, m, l, acc);
-        if (p_has && !p_cut) absorb_row(p_lse, p_o, m, l, acc);
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         char *orow = o_row(ps, s, kvh * ps.group + g0 + h, D, 2);
 #pragma unroll
