@@ -461,6 +461,21 @@ def test_config5_shared_prefix(cuda):
     print("config5", stats)
 
 
+@pytest.mark.parametrize("shape", [
+    # the reference bench's defaults, then its flags at other values
+    dict(),
+    dict(batch=4, ctx=3000, heads=64, kv_heads=8, kv_dtype=W.BF16),
+    dict(batch=32, ctx=77, heads=12, kv_heads=12, head_size=64, kv_dtype=W.FP32),
+])
+def test_reference_bench_shape(cuda, shape):
+    """The reference bench's workload (tests/test_attention_bench.c:34-41,
+    every sequence at the full context) with seeded data and a permuted
+    table, at its defaults and at other --batch/--ctx/--heads values."""
+    wl = W.ref_bench_shape(**shape)
+    print(f"case {wl.name}", flush=True)
+    assert_close(run_gpu(wl), oracle(wl), wl.kv_dtype, wl.name)
+
+
 # ------------------------------------------------------ error handling
 def test_unsupported_shapes_leave_output_untouched(cuda):
     import torch

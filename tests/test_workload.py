@@ -88,6 +88,32 @@ def test_config1_shape():
     assert wl.algorithmic_bytes() == wl.logical_bytes()
 
 
+def test_ref_bench_shape_defaults():
+    """The reference bench's defaults (tests/test_attention_bench.c:34-41):
+    16 sequences at the full 1024-token context, 32 q / 8 kv heads, d 128,
+    fp16, pages of 16; every page of the pool used exactly once, through a
+    permuted (not identity) table."""
+    wl = W.ref_bench_shape()
+    assert (wl.num_seqs, wl.num_heads, wl.num_kv_heads, wl.head_size, wl.block_size) == (16, 32, 8, 128, 16)
+    assert wl.kv_dtype == W.FP16 and math.isclose(wl.scale, 1 / math.sqrt(128), rel_tol=1e-6)
+    assert (wl.seq_lens == 1024).all()
+    used = _check_tables(wl, exact_pool=True)
+    assert wl.num_blocks == 16 * 64
+    assert used != list(range(wl.num_blocks))  # not the reference's identity table
+    assert wl.name == "refbench-b16-ctx1024-32x8-d128-fp16"
+    assert wl.algorithmic_bytes() == wl.logical_bytes()
+
+
+def test_ref_bench_shape_flags_and_refusals():
+    wl = W.ref_bench_shape(batch=3, ctx=100, heads=8, kv_heads=2, head_size=64, kv_dtype=W.BF16)
+    assert (wl.num_seqs, wl.num_heads, wl.num_kv_heads, wl.head_size) == (3, 8, 2, 64)
+    assert (wl.seq_lens == 100).all() and wl.kv_dtype == W.BF16
+    _check_tables(wl, exact_pool=True)
+    for bad in (dict(batch=0), dict(ctx=0), dict(heads=12, kv_heads=8), dict(head_size=-1)):
+        with pytest.raises(ValueError):
+            W.ref_bench_shape(**bad)
+
+
 def _finite16(bits):
     return (bits & 0x7C00) != 0x7C00
 
