@@ -568,6 +568,14 @@ __device__ __forceinline__ void fix_store(MfmaFixSlot<D> &slot, int lane, const 
     slot.l[lane] = st.l;
 }
 
+template <int D>
+__device__ __forceinline__ void fix_load(const MfmaFixSlot<D> &slot, int lane, MfmaState<D> &st) {
+#pragma unroll
+    for (int n = 0; n < MfmaGeometry<D>::kDimBlocks; n++) st.o[n] = slot.o[n][lane];
+    st.m = slot.m[lane];
+    st.l = slot.l[lane];
+}
+
 // st <- st (+) the state in slot (online log-sum-exp, per lane).
 template <int D>
 __device__ __forceinline__ void fix_absorb(const MfmaFixSlot<D> &slot, int lane, MfmaState<D> &st) {
@@ -663,7 +671,7 @@ __device__ __forceinline__ void absorb_partial(const DecodeParams &p, int slot, 
 // the last wavefront down to the first, one barrier per wavefront, kept the
 // workgroup ~1.8 us past its last tile, measured on MI355X.)  The first
 // wavefront's cut first piece (its left neighbour is in another workgroup)
-// is written as a partial directly.
+// is written as a partial after its range, from its slot.
 // Mode 2 (two row blocks) keeps one relay slot per workgroup: cut first
 // pieces followed by more pieces are written as partials by every
 // wavefront, and a left neighbour absorbs such a partial from memory (the
@@ -705,6 +713,8 @@ __device__ __forceinline__ void mfma_partition_body(
     MfmaState<D> st[R];   // the state of the piece being computed; after the loop, the last one's
     MfmaPiece pc;         // the piece being computed; after the loop, the last one
     bool have_last = false;  // FIX: the last piece is cut (its state is kept for the sweep)
+    MfmaPiece pc_first;      // FIX == 1, first wavefront: its cut first piece, saved in its slot
+    bool first_saved = false;
 #if XHIP_TRACING
     int n_tiles = 0, n_pieces = 0;
 #endif
@@ -814,12 +824,16 @@ __device__ __forceinline__ void mfma_partition_body(
             } else if constexpr (FIX == 1) {
                 if (has_next) {
                     // a cut piece with more pieces after it: the wavefront's
-                    // first piece, a continuation that ends its segment here
-                    if (wave > 0) {
-                        fix_store<D>(sm.sw.fix[wave], lane, st[0]);
-                        if (lane == 0) sm.sw.fix[wave].ends = 1;
-                    } else {
-                        mfma_write_partial<D, R, HS>(p, pc, lane, st);
+                    // first piece, a continuation that ends its segment here.
+                    // It goes to the wavefront's slot; the first wavefront's
+                    // (whose left neighbour is in another workgroup) is
+                    // written as a partial after the range, so that its
+                    // stores do not sit in front of the next piece's loads.
+                    fix_store<D>(sm.sw.fix[wave], lane, st[0]);
+                    if (lane == 0) sm.sw.fix[wave].ends = 1;
+                    if (wave == 0) {
+                        pc_first = pc;
+                        first_saved = true;
                     }
                 } else {
                     have_last = true;  // the sweep below decides where it goes
@@ -910,6 +924,11 @@ __device__ __forceinline__ void mfma_partition_body(
             if (lane == 0) sm.sw.fix[wave].ends = pc.t_end >= pc.L ? 1 : 0;
         }
         __syncthreads();
+        if (first_saved) {
+            MfmaState<D> sf[R];
+            fix_load<D>(sm.sw.fix[0], lane, sf[0]);
+            mfma_write_partial<D, R, HS>(p, pc_first, lane, sf);
+        }
         if (have_last && !(cut_start && wave > 0)) {
             bool ends = pc.t_end >= pc.L;
             for (int j = wave + 1; !ends && j < NW; j++) {
