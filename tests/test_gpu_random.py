@@ -101,12 +101,22 @@ def test_random_decode_matches_oracle(cuda, seed):
     print(f"case seed={seed} {dtype} d={D} bs={bs} H={H} KVH={KVH} seqs={len(lens)} "
           f"max_len={max(lens)} scale={wl.scale:.4f} partition={part} {entry}", flush=True)
     dw = W.upload(wl)
-    fn = getattr(_lib.backend(), entry)
-    rc = fn(dw.out.data_ptr(), dw.query.data_ptr(), dw.key_cache.data_ptr(),
+
+    def call(name):
+        return getattr(_lib.backend(), name)(
+            dw.out.data_ptr(), dw.query.data_ptr(), dw.key_cache.data_ptr(),
             dw.value_cache.data_ptr(), dw.block_tables.data_ptr(), dw.seq_lens.data_ptr(),
             wl.num_seqs, H, D, KVH, ctypes.c_float(wl.scale), wl.max_num_blocks_per_seq, bs,
             dw.key_cache.element_size(), dw.key_cache.stride(0), dw.key_cache.stride(1),
             torch.cuda.current_stream().cuda_stream, wl.kv_dtype, part)
+
+    rc = call(entry)
+    if entry == "nxt_paged_attention_noalloc" and part and rc == PA.NXT_ATTN_E_UNSUPPORTED:
+        # an explicit plan larger than the fixed scratch is refused, as
+        # documented; the allocating entry point takes it
+        assert "allocation-free entry point" in PA.last_status()[1], PA.last_status()
+        print(f"seed {seed}: explicit plan refused by the allocation-free entry point", flush=True)
+        rc = call("nxt_paged_attention_ex")
     assert rc == PA.NXT_ATTN_OK, PA.last_status()
     torch.cuda.synchronize()
     _check(dw.out.float().cpu().numpy(), wl, factor, f"seed {seed}")
