@@ -6,8 +6,9 @@
 // process ends.  Host code never uses the array's name as a device address:
 // the first call on a device (that device current) looks its address up with
 // hipGetSymbolAddress, and every later use goes through that pointer.
-// Every no-alloc call on one device shares the array: calls that overlap on
-// one device (other streams, other threads) race on it.
+// Every no-alloc call on one device shares the array, so the entry point
+// orders such calls on the GPU (noalloc_gate.h): two whose kernels overlapped
+// would race on it.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
