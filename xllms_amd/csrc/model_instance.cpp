@@ -129,6 +129,10 @@ struct InstanceState {
     HostBuf<char *> h_optr;
     HostBuf<char> h_pack;  // every array an exec uploads, 256-byte aligned parts
     DevBuf<char> d_pack;
+    // completion word of the execs (host-coherent pinned memory; see
+    // wait_exec) and the number the last exec's signal stored
+    unsigned *done = nullptr;
+    unsigned done_seq = 0;
 
     // Appends h's contents to h_pack at a 256-byte boundary; returns its
     // offset (h_pack.n becomes -1 when host memory runs out).
@@ -223,6 +227,8 @@ void destroy_state(InstanceState *st) {
     st->h_optr.release();
     st->h_pack.release();
     st->d_pack.release();
+    if (st->done) (void)hipHostFree(st->done);
+    st->done = nullptr;
     // the operator layer keeps split-K / cascade workspaces per stream:
     // free this stream's before the handle goes (it may be reused)
     if (st->stream) (void)xhip_release_stream_workspaces(st->device, st->stream);
@@ -262,6 +268,44 @@ struct PhaseTrace {
     const char *names[8];
     double us[8];
 };
+
+// XLLM_HIP_EXEC_SYNC=1 (read once): execs wait with hipStreamSynchronize
+// instead of the completion word.  A diagnostic switch, for comparing the two.
+bool exec_sync_forced() {
+    static const bool forced = [] {
+        const char *v = std::getenv("XLLM_HIP_EXEC_SYNC");
+        return v && v[0] == '1';
+    }();
+    return forced;
+}
+
+// Waits until the device has run everything this exec queued on the
+// instance's stream.  A one-thread kernel queued last stores the exec's
+// number to the host-coherent completion word (it starts only once the
+// exec's kernels have finished), and the host polls the word: measured on
+// MI355X the host sees it ~2 us before hipStreamSynchronize returns.  If the
+// signal cannot be queued, or the word has not changed after 2 ms (long
+// work, or a kernel that failed, after which the queue runs nothing more),
+// hipStreamSynchronize waits instead and reports the stream's error.
+hipError_t wait_exec(InstanceState *st) {
+    if (!st->done || exec_sync_forced()) return hipStreamSynchronize(st->stream);
+    unsigned v = st->done_seq + 1;
+    if (v == 0) v = 1;  // (the word starts at 0)
+    if (xhip::launch_exec_signal(st->done, v, st->stream) != hipSuccess) {
+        (void)hipGetLastError();
+        return hipStreamSynchronize(st->stream);
+    }
+    st->done_seq = v;
+    using clock = std::chrono::steady_clock;
+    const clock::time_point t0 = clock::now();
+    while (__atomic_load_n(st->done, __ATOMIC_ACQUIRE) != v) {
+#if defined(__x86_64__)
+        __builtin_ia32_pause();
+#endif
+        if (clock::now() - t0 > std::chrono::milliseconds(2)) return hipStreamSynchronize(st->stream);
+    }
+    return hipSuccess;
+}
 
 struct Item {
     std::string id;
@@ -345,6 +389,8 @@ XMI_EXPORT int nxt_model_instance_init(NxtModelInstance *instance) {
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&st->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipMalloc(&st->key_cache, cache_bytes);
     if (e == hipSuccess) e = hipMalloc(&st->value_cache, cache_bytes);
+    if (e == hipSuccess) e = hipHostMalloc((void **)&st->done, 64, hipHostMallocCoherent);
+    if (e == hipSuccess) *st->done = 0;
     if (e != hipSuccess) {
         destroy_state(st);
         return fail("instance init: %s (K/V caches of %zu bytes each)", hipGetErrorString(e),
@@ -646,9 +692,10 @@ int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<st
     }
 
     tr.mark("launch");
-    // 4. wait for the device, then end the released requests (polling
-    //    hipStreamQuery instead took 6-8 us longer per exec)
-    e = hipStreamSynchronize(st->stream);
+    // 4. wait for the device (wait_exec: the completion word; polling
+    //    hipStreamQuery instead of hipStreamSynchronize took 6-8 us longer per
+    //    exec), then end the released requests
+    e = wait_exec(st);
     if (e != hipSuccess && rc == 0) rc = fail("exec: %s", hipGetErrorString(e));
     for (const Item &it : items) {
         st->bound.erase(it.id);

@@ -49,4 +49,8 @@ hipError_t launch_stage_copy(void *dst, const void *host_src, size_t bytes, hipS
 hipError_t launch_stage_copy_append(void *dst, const void *host_src, size_t bytes,
                                     const KvAppendParams &p, hipStream_t stream);
 
+// Queues a one-thread kernel that stores `value` to `word` (host-coherent
+// pinned memory) with system scope, after everything queued on `stream`.
+hipError_t launch_exec_signal(unsigned *word, unsigned value, hipStream_t stream);
+
 }  // namespace xhip

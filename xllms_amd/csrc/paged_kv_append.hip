@@ -163,4 +163,19 @@ hipError_t launch_stage_copy_append(void *dst, const void *host_src, size_t byte
     return hipGetLastError();
 }
 
+// Completion word of a model-instance exec: one thread stores `value` to a
+// host-coherent word with system scope.  Queued after an exec's launches it
+// runs once they have all finished, and the host sees the word change
+// ~2 us before hipStreamSynchronize on the same stream returns (measured on
+// MI355X: a small kernel plus this signal and a host poll 9.3 us, the
+// kernel plus hipStreamSynchronize 11.5 us).
+__global__ __launch_bounds__(64) void exec_signal_kernel(unsigned *word, unsigned value) {
+    if (threadIdx.x == 0) __hip_atomic_store(word, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+hipError_t launch_exec_signal(unsigned *word, unsigned value, hipStream_t stream) {
+    exec_signal_kernel<<<1, 64, 0, stream>>>(word, value);
+    return hipGetLastError();
+}
+
 }  // namespace xhip
