@@ -578,8 +578,9 @@ def bench_serve(args) -> int:
     are outside the timed region; the native exec call is timed with the host
     clock.  XLLM_HIP_EXEC_TRACE=1 prints each exec's phase times.  With
     --per-request the same steps also run as one instance_exec(.., 1) per
-    request, synchronously (the reference scheduler's pattern) and in
-    deferred mode with one flush per step."""
+    request in deferred mode with one flush per step (taking turns with the
+    whole-batch execs), and then as many steps run as one synchronous
+    instance_exec(.., 1) per request (the reference scheduler's pattern)."""
     import numpy as np
     import torch
     from xllms_amd import backend as B
@@ -646,41 +647,52 @@ def bench_serve(args) -> int:
                 return rc
         return m.flush()
 
-    # one exec over the whole batch; with --per-request the three modes take
-    # turns step by step, so each sees the same batch (every step appends a
-    # token per request)
-    modes = [("whole", lambda: m.exec_requests(batch))]
+    # One exec over the whole batch per step; with --per-request the deferred
+    # mode takes turns with it step by step (both see the same batch), and
+    # then as many steps run synchronously, one exec per request, on their
+    # own: so each is timed in its steady state (a one-request exec right
+    # after a batched exec of the same sequence first uploads that
+    # sequence's device record; in a scheduler's loop of one-request execs
+    # the records stay current).  Every step appends a token per request, so
+    # the synchronous steps attend over somewhat longer contexts.
+    blocks = [[("whole", lambda: m.exec_requests(batch))]]
     if args.per_request:
-        modes += [("synchronous", sync_step), ("deferred", deferred_step)]
-    timed = {key: [] for key, _ in modes}
-    for step in range(args.warmup + args.steps):
-        for key, fn in modes:
-            if key == "deferred":
-                assert m.set_deferred(True) == 0
-            bind_step()
-            t0 = time.perf_counter()
-            rc = fn()
-            dt = time.perf_counter() - t0
-            if key == "deferred":
-                assert m.set_deferred(False) == 0
-            if rc != 0:
-                raise RuntimeError(f"{key} exec failed at step {step}")
-            if step >= args.warmup:
-                timed[key].append(dt)
+        blocks[0].append(("deferred", deferred_step))
+        blocks.append([("synchronous", sync_step)])
+    timed = {key: [] for block in blocks for key, _ in block}
+    for block in blocks:
+        for step in range(args.warmup + args.steps):
+            for key, fn in block:
+                if key == "deferred":
+                    assert m.set_deferred(True) == 0
+                bind_step()
+                t0 = time.perf_counter()
+                rc = fn()
+                dt = time.perf_counter() - t0
+                if key == "deferred":
+                    assert m.set_deferred(False) == 0
+                if rc != 0:
+                    raise RuntimeError(f"{key} exec failed at step {step}")
+                if step >= args.warmup:
+                    timed[key].append(dt)
     times = timed["whole"]
-    # the timed execs attend over the prompt lengths plus (phases per step) x
-    # (steps so far) + 1 tokens; the middle one:
-    mid_lens = lens + phases * (args.warmup + args.steps // 2) + 1
+    # the whole-batch execs attend over the prompt lengths plus (modes taking
+    # turns) x (steps so far) + 1 tokens; the middle one:
+    turns = len(blocks[0])
+    mid_lens = lens + turns * (args.warmup + args.steps // 2) + 1
     per_request = None
     if args.per_request:
         per_request = {}
         for key in ("synchronous", "deferred"):
             t = timed[key]
             md = float(np.median(t))
+            mode_mid = (lens + 2 * (args.warmup + args.steps) + args.warmup + args.steps // 2 + 1
+                        if key == "synchronous" else mid_lens + 1)
             per_request[key] = {"seqs_per_s": round(nreq / md, 1),
                                 "step_us": {"median": round(md * 1e6, 1),
                                             "min": round(min(t) * 1e6, 1),
-                                            "max": round(max(t) * 1e6, 1)}}
+                                            "max": round(max(t) * 1e6, 1)},
+                                "context_tokens_at_timed_middle": int(mode_mid.sum())}
         log(f"[bench] per-request execs: {per_request}")
     ok = bool(torch.isfinite(out.float()).all())
     exec_count = int(m.model.instances[0].exec_count)

@@ -210,3 +210,52 @@ def test_deferred_scheduler_pattern(cuda):
     assert m.close() == 0
     c.check(rids, binds, "flushed by fini")
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype,D", [(W.FP16, 128), (W.FP16, 64), (W.FP32, 128), (W.FP16, 96)],
+                         ids=["fp16-d128", "fp16-d64", "fp32-d128", "fp16-d96"])
+def test_one_request_decode_steps(cuda, dtype, D):
+    """The scheduler's steady state: one instance_exec(.., 1) per running
+    request, step after step.  Head sizes 32, 64 and 128 take the one-request
+    path that keeps each sequence's length and block table on the device and
+    folds the new token in at the merge (96: the general exec).  Prompts of
+    15, 16, 17, 31 and 33 tokens put the new tokens on both sides of page
+    boundaries; a whole-batch exec in between leaves the device copies stale
+    (the next one-request exec uploads them again); a released request's
+    handle goes to a new one.  Every output against the oracle."""
+    import torch
+    rng = np.random.default_rng(5)
+    H, KVH, bs = 16, 4, 16
+    ref = Driver.__new__(Driver)
+    ref.KVH, ref.H, ref.D, ref.bs = KVH, H, D, bs
+    ref.scale = 1.0 / np.sqrt(D)
+    ref.live, ref._rows = {}, {}
+    code = B.NXT_TYPE_FP32 if dtype == W.FP32 else B.NXT_TYPE_FP16
+    m = B.DecodeModel(num_blocks=256, num_kv_heads=KVH, block_size=bs, head_size=D,
+                      num_heads=H, dtype=code, max_batch_size=8, max_blocks_per_seq=16)
+    assert m.status == 0
+    c = Client(m, ref, dtype)
+    rids = [f"s{i}" for i in range(5)]
+    for n, rid in zip([15, 16, 17, 31, 33], rids):
+        b = c.bind(rid, list(rng.integers(0, 60, n)), rng)
+        assert m.exec([rid]) == 0
+        c.check([rid], {rid: b}, f"prefill {rid}")
+    for step in range(40):
+        binds = {rid: c.bind(rid, [int(rng.integers(0, 60))], rng) for rid in rids}
+        if step == 17:
+            assert m.exec(rids) == 0
+        else:
+            for rid in rids:
+                assert m.exec([rid]) == 0
+        c.check(rids, binds, f"step {step}")
+        if step == 25:
+            gone = rids.pop(1)
+            c.bind(gone, [], rng, release=True, attend=False)
+            assert m.exec([gone]) == 0
+            del c.hist[gone]
+            b = c.bind("new", list(rng.integers(0, 60, 20)), rng)
+            assert m.exec(["new"]) == 0
+            c.check(["new"], {"new": b}, "admitted after a release")
+            rids.append("new")
+    assert m.close() == 0
+    torch.cuda.synchronize()

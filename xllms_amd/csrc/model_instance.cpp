@@ -133,6 +133,34 @@ struct InstanceState {
     // wait_exec) and the number the last exec's signal stored
     unsigned *done = nullptr;
     unsigned done_seq = 0;
+    // One-request decode steps (fast_step): each sequence's length and block
+    // table kept on the device between execs, in a record of rec_ints ints
+    // per sequence handle ([0] the length, the table from kRecHead on), and
+    // the number of tokens the record holds (-1: none), on the host.
+    static constexpr int kRecHead = 4;
+    DevBuf<int32_t> d_recs;
+    std::vector<int32_t> dev_len;
+    size_t rec_ints = 0;
+    DevBuf<float> d_state;      // fp32 rows [num_heads][head_size], then their lse [num_heads]
+    HostBuf<int32_t> h_rec;     // staging of one record
+
+    void forget_device_row(int32_t seq) {
+        if (seq >= 0 && (size_t)seq < dev_len.size()) dev_len[(size_t)seq] = -1;
+    }
+    // Records for handles [0, n): grown by doubling; a new buffer holds
+    // none (the old records are dropped with it).
+    bool ensure_recs(int32_t n) {
+        if ((size_t)n <= dev_len.size()) return true;
+        size_t cap = dev_len.empty() ? 64 : dev_len.size();
+        while (cap < (size_t)n) cap *= 2;
+        d_recs.release();
+        if (!d_recs.reserve(cap * rec_ints)) {
+            dev_len.clear();
+            return false;
+        }
+        dev_len.assign(cap, -1);
+        return true;
+    }
 
     // Appends h's contents to h_pack at a 256-byte boundary; returns its
     // offset (h_pack.n becomes -1 when host memory runs out).
@@ -227,6 +255,9 @@ void destroy_state(InstanceState *st) {
     st->h_optr.release();
     st->h_pack.release();
     st->d_pack.release();
+    st->d_recs.release();
+    st->d_state.release();
+    st->h_rec.release();
     if (st->done) (void)hipHostFree(st->done);
     st->done = nullptr;
     // the operator layer keeps split-K / cascade workspaces per stream:
@@ -391,6 +422,10 @@ XMI_EXPORT int nxt_model_instance_init(NxtModelInstance *instance) {
     if (e == hipSuccess) e = hipMalloc(&st->value_cache, cache_bytes);
     if (e == hipSuccess) e = hipHostMalloc((void **)&st->done, 64, hipHostMallocCoherent);
     if (e == hipSuccess) *st->done = 0;
+    if (e == hipSuccess && !st->d_state.reserve((size_t)s.num_heads * (s.head_size + 1)))
+        e = hipErrorOutOfMemory;
+    // a record: the head, then a table row, in whole 256-byte units
+    st->rec_ints = ((size_t)InstanceState::kRecHead + (size_t)s.max_blocks + 63) & ~(size_t)63;
     if (e != hipSuccess) {
         destroy_state(st);
         return fail("instance init: %s (K/V caches of %zu bytes each)", hipGetErrorString(e),
@@ -501,35 +536,70 @@ XMI_EXPORT int nxt_model_instance_set_deferred(NxtModelInstance *instance, int o
 
 namespace {
 
-// One exec of the requests `ids` (in order): the whole-batch decode step.
-int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<std::string> &ids) {
+// One-request decode steps -- the reference scheduler's instance_exec(.., 1)
+// for a running request: one token appended, a query to attend with, a head
+// size the new-token fold supports.
+bool fast_ok(const InstanceState *st, const std::vector<Item> &items) {
+    if (items.size() != 1) return false;
+    const Item &it = items[0];
+    const int d = st->spec.head_size;
+    return it.seq >= 0 && it.io.num_tokens == 1 && it.io.query && it.io.output && st->d_state.p &&
+           (d == 32 || d == 64 || d == 128);
+}
+
+// A one-request decode step without the staging launch: the sequence's
+// length and block table are already on the device (its record, uploaded
+// by one staging copy when it does not hold exactly the tokens before this
+// one), the attention runs over those cached tokens, and its merge folds in
+// the new token from the request's bound rows and then stores them to the
+// token's cache slot, the new page id to the record when the token opens a
+// page, and the new length (xhip_paged_attention_fold_new).
+int fast_step(InstanceState *st, Item &it) {
     const ModelSpec &s = st->spec;
-    const uint32_t request_count = (uint32_t)ids.size();
-    const auto t0 = std::chrono::steady_clock::now();
-    PhaseTrace tr(t0);
-    if ((int)request_count > s.max_batch)
-        return fail("exec: %u requests > max_batch_size %d", request_count, s.max_batch);
-
-    // every request bound, each once (a bound entry carries the stamp of the
-    // exec that took it)
-    std::vector<Item> items;
-    items.reserve(request_count);
-    const uint64_t stamp = ++st->exec_stamp;
-    for (uint32_t i = 0; i < request_count; ++i) {
-        const std::string &id = ids[i];
-        auto b = st->bound.find(id);
-        if (b == st->bound.end()) return fail("exec: request %s has no bound buffers", id.c_str());
-        if (b->second.exec_stamp == stamp)
-            return fail("exec: request %s twice in one batch", id.c_str());
-        b->second.exec_stamp = stamp;
-        auto q = st->seqs.find(id);
-        items.push_back({id, b->second.io, q == st->seqs.end() ? -1 : q->second});
-        if (items.back().seq < 0 && b->second.io.num_tokens == 0)
-            return fail("exec: new request %s without tokens", id.c_str());
+    int32_t slot = -1;
+    const int r = nxt_kv_seq_append(st->index, it.seq, it.io.token_ids, 1, &slot);
+    if (r != NXT_KV_OK) return fail("exec: appending to %s failed (%d)", it.id.c_str(), r);
+    const int L = nxt_kv_seq_len(st->index, it.seq);  // with the new token
+    const int width = (L + s.block_size - 1) / s.block_size;
+    if (!st->ensure_recs(it.seq + 1)) return fail("exec: out of device memory");
+    int32_t *rec = st->d_recs.p + (size_t)it.seq * st->rec_ints;
+    if (st->dev_len[(size_t)it.seq] != L - 1) {
+        st->dev_len[(size_t)it.seq] = -1;
+        const size_t n = ((size_t)InstanceState::kRecHead + (size_t)width + 3) & ~(size_t)3;
+        if (!st->h_rec.reserve(n)) return fail("exec: out of host memory");
+        std::memset(st->h_rec.p, 0, n * sizeof(int32_t));
+        int32_t len_now = 0;
+        if (nxt_kv_batch_tables(st->index, &it.seq, 1, width,
+                                st->h_rec.p + InstanceState::kRecHead, &len_now) != NXT_KV_OK ||
+            len_now != L)
+            return fail("exec: block table of %s", it.id.c_str());
+        st->h_rec.p[0] = L - 1;
+        const hipError_t e = xhip::launch_stage_copy(rec, st->h_rec.p, n * sizeof(int32_t),
+                                                     st->stream);
+        if (e != hipSuccess) return fail("exec: record upload: %s", hipGetErrorString(e));
     }
-    if (hipSetDevice(st->device) != hipSuccess) return fail("exec: hipSetDevice failed");
+    const int last = L - 1;  // the new token's position
+    int *entry = last % s.block_size == 0
+                     ? rec + InstanceState::kRecHead + last / s.block_size
+                     : nullptr;
+    const int kbs = s.num_kv_heads * s.block_size * s.head_size;
+    const int khs = s.block_size * s.head_size;
+    const int a = xhip_paged_attention_fold_new(
+        it.io.output, it.io.query, st->key_cache, st->value_cache,
+        rec + InstanceState::kRecHead, rec, st->d_state.p,
+        st->d_state.p + (size_t)s.num_heads * s.head_size, it.io.key, it.io.value, entry, rec,
+        slot, slot / s.block_size, L, s.num_heads, s.head_size, s.num_kv_heads, s.scale, width,
+        s.block_size, kbs, khs, s.kv_dtype, st->stream);
+    if (a != NXT_ATTN_OK) return fail("exec: attention: %s", nxt_attn_last_error());
+    st->dev_len[(size_t)it.seq] = L;
+    return 0;
+}
 
-    tr.mark("validate");
+// The general exec (admissions, appends, any batch): index work on the host,
+// one staging launch for every array the launches read (with the new rows'
+// K/V write), the copies of partly shared pages and the attention.
+int slow_step(InstanceState *st, std::vector<Item> &items, PhaseTrace &tr) {
+    const ModelSpec &s = st->spec;
     // 1. sequences: admissions and appends; the K/V rows to write and copy
     const size_t kv_row = (size_t)s.num_kv_heads * s.head_size * s.elem_bytes;
     st->h_slots.n = st->h_src.n = st->h_dst.n = st->h_kptr.n = st->h_vptr.n = 0;
@@ -552,6 +622,7 @@ int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<st
             }
             it.seq = a.seq;
             st->seqs[it.id] = a.seq;
+            st->forget_device_row(a.seq);  // (a reused handle)
             // the prompt becomes shareable at once: later admissions (also in
             // this exec: their copies run after this exec's writes) find it
             nxt_kv_seq_cache(st->index, a.seq);
@@ -691,16 +762,52 @@ int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<st
         if (a != NXT_ATTN_OK) rc = fail("exec: attention: %s", nxt_attn_last_error());
     }
 
+    return rc;
+}
+
+// One exec of the requests `ids` (in order): the whole-batch decode step.
+int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<std::string> &ids) {
+    const ModelSpec &s = st->spec;
+    const uint32_t request_count = (uint32_t)ids.size();
+    const auto t0 = std::chrono::steady_clock::now();
+    PhaseTrace tr(t0);
+    if ((int)request_count > s.max_batch)
+        return fail("exec: %u requests > max_batch_size %d", request_count, s.max_batch);
+
+    // every request bound, each once (a bound entry carries the stamp of the
+    // exec that took it)
+    std::vector<Item> items;
+    items.reserve(request_count);
+    const uint64_t stamp = ++st->exec_stamp;
+    for (uint32_t i = 0; i < request_count; ++i) {
+        const std::string &id = ids[i];
+        auto b = st->bound.find(id);
+        if (b == st->bound.end()) return fail("exec: request %s has no bound buffers", id.c_str());
+        if (b->second.exec_stamp == stamp)
+            return fail("exec: request %s twice in one batch", id.c_str());
+        b->second.exec_stamp = stamp;
+        auto q = st->seqs.find(id);
+        items.push_back({id, b->second.io, q == st->seqs.end() ? -1 : q->second});
+        if (items.back().seq < 0 && b->second.io.num_tokens == 0)
+            return fail("exec: new request %s without tokens", id.c_str());
+    }
+    if (hipSetDevice(st->device) != hipSuccess) return fail("exec: hipSetDevice failed");
+
+    tr.mark("validate");
+    int rc = fast_ok(st, items) ? fast_step(st, items[0]) : slow_step(st, items, tr);
     tr.mark("launch");
-    // 4. wait for the device (wait_exec: the completion word; polling
-    //    hipStreamQuery instead of hipStreamSynchronize took 6-8 us longer per
-    //    exec), then end the released requests
-    e = wait_exec(st);
+    // wait for the device (wait_exec: the completion word; polling
+    // hipStreamQuery instead of hipStreamSynchronize took 6-8 us longer per
+    // exec), then end the released requests
+    const hipError_t e = wait_exec(st);
     if (e != hipSuccess && rc == 0) rc = fail("exec: %s", hipGetErrorString(e));
+    if (rc != 0)  // what the device holds of the exec's sequences is unknown
+        for (const Item &it : items) st->forget_device_row(it.seq);
     for (const Item &it : items) {
         st->bound.erase(it.id);
         if (rc == 0 && it.io.release && it.seq >= 0) {
             nxt_kv_seq_release(st->index, it.seq, 1);
+            st->forget_device_row(it.seq);  // its handle may be reused
             st->seqs.erase(it.id);
         }
     }

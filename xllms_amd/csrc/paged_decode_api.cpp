@@ -327,6 +327,16 @@ struct RowPtrs {
     char *const *o;
 };
 
+// New-token fold of a one-sequence launch (DecodeParams::nt_fold): the
+// sequence's cached tokens are attended in partial-output mode (po), and the
+// merge folds in the new token and writes `out`.
+struct NewTokenFold {
+    const void *k, *v;  // the token's rows, [num_kv_heads][head_size], device
+    int *table;         // block-table entry that receives `page` (null: none)
+    int *lens;          // length entry that receives `len`
+    int slot, page, len;
+};
+
 // The fields of a launch's DecodeParams that come straight from its batch.
 void fill_batch(DecodeParams &p, const void *query, const void *key_cache, const void *value_cache,
                 const int *block_tables, const int *seq_lens, int nseq, int num_heads,
@@ -357,7 +367,8 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         int num_kv_heads, float scale, int max_num_blocks_per_seq, int block_size, int dtype_size,
         int kv_block_stride, int kv_head_stride, nxt_stream_t stream_handle, int kv_dtype,
         int partition_tokens, const PartialOut *po = nullptr, const PrefixFold *fold = nullptr,
-        const FixedWs *fixed = nullptr, const RowPtrs *rows = nullptr) {
+        const FixedWs *fixed = nullptr, const RowPtrs *rows = nullptr,
+        const NewTokenFold *nt = nullptr) {
     // ---- argument checks (host only; nothing is read from the device)
     if (kv_dtype != NXT_KV_FP16 && kv_dtype != NXT_KV_BF16 && kv_dtype != NXT_KV_FP32)
         return set_status(NXT_ATTN_E_UNSUPPORTED, "kv_dtype %d is not FP16/BF16/FP32", kv_dtype);
@@ -393,6 +404,10 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
     HeadTiling tiling;
     if (!head_tiling(group, mfma, head_size, &tiling))
         return set_status(NXT_ATTN_E_UNSUPPORTED, "GQA group %d > %d", group, max_group(mfma));
+    if (nt && (num_seqs != 1 || !po || !out || rows || fold || partition_tokens ||
+               !(head_size == 32 || head_size == 64 || head_size == 128) || !nt->k || !nt->v ||
+               !nt->lens))
+        return set_status(NXT_ATTN_E_INVALID, "bad new-token fold launch");
     if (num_seqs == 0) return ok();
     const void *out_any = po ? (const void *)po->out_f32 : rows ? (const void *)rows->o : out;
     const void *q_any = rows ? (const void *)rows->q : query;
@@ -579,6 +594,17 @@ int run(void *out, const void *query, const void *key_cache, const void *value_c
         p.merge_per_segment =
             ((long long)nseq * segs >= 2LL * cus || (long long)nseq * segs * chunks > 4LL * cus) ? 1
                                                                                                 : 0;
+        if (nt) {  // the fold lives in the chunk-grid merge
+            p.merge_per_segment = 0;
+            p.nt_fold = 1;
+            p.nt_k = nt->k;
+            p.nt_v = nt->v;
+            p.nt_table = nt->table;
+            p.nt_lens = nt->lens;
+            p.nt_slot = nt->slot;
+            p.nt_page = nt->page;
+            p.nt_len = nt->len;
+        }
 
         switch (kv_dtype) {
         case NXT_KV_FP16:
@@ -1203,6 +1229,24 @@ __attribute__((visibility("hidden"))) int xhip_paged_attention_rows(
                num_heads, head_size, num_kv_heads, scale, max_num_blocks_per_seq, block_size,
                elem_bytes(kv_dtype), kv_block_stride, kv_head_stride, stream, kv_dtype, 0,
                nullptr, nullptr, nullptr, &rows);
+}
+
+__attribute__((visibility("hidden"))) int xhip_paged_attention_fold_new(
+    void *out, const void *query, const void *key_cache, const void *value_cache,
+    const int *block_table, const int *seq_len, float *state_rows, float *state_lse,
+    const void *new_k, const void *new_v, int *new_table_entry, int *new_len_entry, int new_slot,
+    int new_page, int new_len, int num_heads, int head_size, int num_kv_heads, float scale,
+    int max_num_blocks_per_seq, int block_size, int kv_block_stride, int kv_head_stride,
+    int kv_dtype, nxt_stream_t stream) {
+    if (!state_rows || !state_lse || new_slot < 0 || new_page < 0 || new_len < 1)
+        return set_status(NXT_ATTN_E_INVALID, "bad new-token fold arguments");
+    const PartialOut po{state_rows, state_lse, 0, 0};
+    const NewTokenFold nt{new_k, new_v, new_table_entry, new_len_entry, new_slot, new_page,
+                          new_len};
+    return run(out, query, key_cache, value_cache, block_table, seq_len, 1, num_heads, head_size,
+               num_kv_heads, scale, max_num_blocks_per_seq, block_size, elem_bytes(kv_dtype),
+               kv_block_stride, kv_head_stride, stream, kv_dtype, 0, &po, nullptr, nullptr,
+               nullptr, &nt);
 }
 
 __attribute__((visibility("hidden"))) int xhip_paged_attention_cascade_rows(

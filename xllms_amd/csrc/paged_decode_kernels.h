@@ -1025,6 +1025,66 @@ __device__ __forceinline__ void write_empty_column(const DecodeParams &p, int s,
     }
 }
 
+// Four consecutive elements of a row (element type), as fp32.
+template <int KV>
+__device__ __forceinline__ f32x4 load4_elem(const char *row, int i) {
+    if constexpr (KV == KV_F32) {
+        return *(const f32x4 *)(row + (size_t)i * 4);
+    } else {
+        const u32x2 w = *(const u32x2 *)(row + (size_t)i * 2);
+        const f32x2 a = unpack16<KV>(w.x), b = unpack16<KV>(w.y);
+        return f32x4{a.x, a.y, b.x, b.y};
+    }
+}
+
+// New-token fold (DecodeParams::nt_fold) of output float4 column c (dims
+// 4c..4c+3) of query head `head` (kv head kvh) of sequence s, whose state
+// over the cached tokens is (m, l, acc) (log2 units; acc = l * the row):
+// the new token's score, q . k_new over the head's C4 = D/4 columns held by
+// an aligned group of C4 consecutive lanes (xor butterfly), then the online
+// log-sum-exp update with v_new.  Returns the finished column.
+template <int KV, int D>
+__device__ __forceinline__ f32x4 fold_new_token(const DecodeParams &p, int s, int kvh, int head,
+                                                int c, float m, float l, f32x4 acc) {
+    constexpr int C4 = D / 4;
+    constexpr int EB = KV == KV_F32 ? 4 : 2;
+    static_assert((C4 & (C4 - 1)) == 0 && C4 <= 32, "a head's columns in one aligned lane group");
+    const f32x4 q = load4_elem<KV>(q_row(p, s, head, D, EB), 4 * c);
+    const f32x4 k = load4_elem<KV>((const char *)p.nt_k + (size_t)kvh * D * EB, 4 * c);
+    const f32x4 v = load4_elem<KV>((const char *)p.nt_v + (size_t)kvh * D * EB, 4 * c);
+    float dot = q.x * k.x + q.y * k.y + q.z * k.z + q.w * k.w;
+#pragma unroll
+    for (int off = 1; off < C4; off <<= 1) dot += __shfl_xor(dot, off);
+    const float sc = dot * p.scale_log2;
+    const float M = fmaxf(m, sc);
+    const float a = fast_exp2(m - M), b = fast_exp2(sc - M);
+    return (acc * a + v * b) * (1.0f / (l * a + b));
+}
+
+// New-token fold: the token's K/V rows of kv head kvh into its cache slot
+// (16-byte chunks, threads of one workgroup), and, by one thread of the
+// launch, the sequence's new page id and length.
+template <int D, int EB>
+__device__ __forceinline__ void store_new_token(const DecodeParams &p, int kvh, bool lead) {
+    constexpr int kChunks = D * EB / 16;
+    const int page = p.nt_slot >> p.bs_shift;
+    const int off = p.nt_slot & (p.block_size - 1);
+    const size_t at = ((size_t)page * p.kv_block_stride + (size_t)kvh * p.kv_head_stride +
+                       (size_t)off * D) * EB;
+    const size_t src = (size_t)kvh * D * EB;
+    for (int i = threadIdx.x; i < 2 * kChunks; i += blockDim.x) {
+        const bool is_v = i >= kChunks;
+        const int ch = is_v ? i - kChunks : i;
+        const char *from = (const char *)(is_v ? p.nt_v : p.nt_k) + src + (size_t)ch * 16;
+        char *to = (char *)(is_v ? p.v : p.k) + at + (size_t)ch * 16;
+        *(u32x4 *)to = *(const u32x4 *)from;
+    }
+    if (lead && threadIdx.x == 0) {
+        if (p.nt_table) *p.nt_table = p.nt_page;
+        *p.nt_lens = p.nt_len;
+    }
+}
+
 // Merge kernel: one workgroup per (segment, chunk of kMergeCols output
 // float4 columns), where a segment is (sequence, kv head, head tile) and the
 // columns run over (head h < nh, dims 4c..4c+3).  It writes zeros for an
@@ -1054,18 +1114,40 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
     const int nh = min(GT, p.group - g0);
     const int ncols = nh * C4;
     const int col0 = blockIdx.y * kMergeCols;
+    constexpr int EB = KV == KV_F32 ? 4 : 2;
+    // the new-token fold needs a head's columns in one aligned lane group
+    constexpr bool kFold = (C4 & (C4 - 1)) == 0 && C4 <= 32;
+    if (kFold && p.nt_fold && blockIdx.y == 0 && ht == 0)
+        store_new_token<D, EB>(p, kvh, blockIdx.x == 0);
     if (col0 >= ncols) return;
     const int tid = threadIdx.x;
     // the three scalars the merge needs, requested together (the empty asm
     // keeps the compiler from sinking the prefix loads past the L == 0 exit,
-    // which would cost a second round trip)
-    const int L = seq_len_of(p, s);
+    // which would cost a second round trip).  Under the new-token fold the
+    // cached length is nt_len - 1 (this launch stores nt_len to the lengths
+    // the partition kernel read).
+    const int L = kFold && p.nt_fold ? p.nt_len - 1 : seq_len_of(p, s);
     const int total = p.ws_prefix[p.num_seqs];
     const int pre_s = p.ws_prefix[s];
     asm volatile("" ::"s"(total), "s"(pre_s));
     const size_t qrow0 = ((size_t)s * p.num_heads + (size_t)kvh * p.group + g0) * D;
 
     if (L == 0) {
+        if constexpr (kFold) {
+            if (p.nt_fold) {  // no cached token: the output is the new token's V
+                const int col = col0 + tid;
+                if (tid < kMergeCols && col < ncols) {
+                    const int h = col / C4, c = col - h * C4;
+                    const f32x4 o = fold_new_token<KV, D>(p, s, kvh, kvh * p.group + g0 + h, c,
+                                                          -INFINITY, 0.0f,
+                                                          f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                    char *orow = o_row(p, s, kvh * p.group + g0 + h, D, EB);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) store_elem<KV>(orow, c * 4 + e, o[e]);
+                }
+                return;
+            }
+        }
         if (tid < kMergeCols && col0 + tid < ncols && !p.skip_empty)
             write_empty_column<KV, D>(p, s, kvh, g0, qrow0, col0 + tid);
         return;
@@ -1074,8 +1156,26 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
     const int Ts = (L + TT - 1) / TT;
     const int seg_start = pre_s + seg * segment_units(p, Ts);  // in split units
     PartialSlots ps;
-    if (!segment_partials<kMfmaWavesPerGroup>(p, seg_start, seg_start + p.seg_cost, Ts, tpw, ps))
+    if (!segment_partials<kMfmaWavesPerGroup>(p, seg_start, seg_start + p.seg_cost, Ts, tpw, ps)) {
+        if constexpr (kFold) {
+            if (p.nt_fold) {
+                // a segment the partition kernel finished: its row and
+                // log-sum-exp (partial-output mode), folded with the new token
+                const int col = col0 + tid;
+                if (tid < kMergeCols && col < ncols) {
+                    const int h = col / C4, c = col - h * C4;
+                    const float lse = p.out_lse[qrow0 / D + h];
+                    const f32x4 row = *(const f32x4 *)(p.out_f32 + qrow0 + (size_t)h * D + c * 4);
+                    const f32x4 o = fold_new_token<KV, D>(p, s, kvh, kvh * p.group + g0 + h, c,
+                                                          lse, lse == -INFINITY ? 0.0f : 1.0f, row);
+                    char *orow = o_row(p, s, kvh * p.group + g0 + h, D, EB);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) store_elem<KV>(orow, c * 4 + e, o[e]);
+                }
+            }
+        }
         return;
+    }
 
     const int cl = tid % kMergeCols;
     const int psplit = tid / kMergeCols;
@@ -1103,6 +1203,15 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
         aa = aa * a + s_acc[k][cl] * b;
         mm = M;
     }
+    if constexpr (kFold) {
+        if (p.nt_fold) {
+            const f32x4 o = fold_new_token<KV, D>(p, s, kvh, kvh * p.group + g0 + h, c, mm, ll, aa);
+            char *orow = o_row(p, s, kvh * p.group + g0 + h, D, EB);
+#pragma unroll
+            for (int e = 0; e < 4; e++) store_elem<KV>(orow, c * 4 + e, o[e]);
+            return;
+        }
+    }
     const float inv = ll > 0.0f ? 1.0f / ll : 0.0f;
     const size_t base = qrow0 + (size_t)h * D + c * 4;
     if (p.out_f32) {
@@ -1110,7 +1219,7 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
         if (c == 0) p.out_lse[qrow0 / D + h] = ll > 0.0f ? mm + log2f(ll) : -INFINITY;
         return;
     }
-    char *orow = o_row(p, s, kvh * p.group + g0 + h, D, KV == KV_F32 ? 4 : 2);
+    char *orow = o_row(p, s, kvh * p.group + g0 + h, D, EB);
 #pragma unroll
     for (int e = 0; e < 4; e++) store_elem<KV>(orow, c * 4 + e, aa[e] * inv);
 }

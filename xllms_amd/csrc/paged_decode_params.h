@@ -149,6 +149,24 @@ struct DecodeParams {
     const float *fold_lse;
     int fold_rows;
     int fold_kr;
+    // New-token fold (the serving path's one-request decode step, one
+    // sequence): the partition kernel attends over the sequence's cached
+    // tokens in partial-output mode, and the merge kernel (chunk grid) takes
+    // every segment's state -- the finished row and its log-sum-exp, or its
+    // partials -- folds in the step's new token, whose rows ([num_kv_heads]
+    // [head_size], element type) are at nt_k / nt_v instead of in the cache
+    // (score q . k_new, the online log-sum-exp update with v_new), and writes
+    // the output rows to `out`.  The merge also writes the token's K/V rows
+    // to its cache slot nt_slot, nt_page to *nt_table when the token opens a
+    // page (nt_table not null), and nt_len to *nt_lens.
+    int nt_fold;
+    const void *nt_k;
+    const void *nt_v;
+    int *nt_table;
+    int *nt_lens;
+    int nt_slot;
+    int nt_page;
+    int nt_len;
     // Per-workgroup timestamps (wg_trace.h): written only by the kernels of
     // the instrumented measurement build (XHIP_WG_TRACE); null otherwise.
     unsigned long long *wg_trace;

@@ -29,6 +29,23 @@ __attribute__((visibility("hidden"))) int xhip_paged_attention_cascade_rows(
     int num_heads, int head_size, int num_kv_heads, float scale, int max_num_blocks_per_seq,
     int block_size, int kv_block_stride, int kv_head_stride, int kv_dtype, nxt_stream_t stream);
 
+/* One sequence's decode step whose new token is not in the cache yet (the
+ * model instance's one-request exec): attends over the seq_len[0] cached
+ * tokens (block_table: the sequence's row) into the fp32 states state_rows
+ * [num_heads][head_size] / state_lse [num_heads], folds in the new token's
+ * rows new_k / new_v ([num_kv_heads][head_size]) and writes `out`
+ * ([num_heads][head_size]); the same launches then store the token's rows
+ * to cache slot new_slot, new_page to *new_table_entry (if not NULL) and
+ * new_len (= seq_len[0] + 1) to *new_len_entry, which may be seq_len itself.
+ * head_size 32, 64 or 128. */
+__attribute__((visibility("hidden"))) int xhip_paged_attention_fold_new(
+    void *out, const void *query, const void *key_cache, const void *value_cache,
+    const int *block_table, const int *seq_len, float *state_rows, float *state_lse,
+    const void *new_k, const void *new_v, int *new_table_entry, int *new_len_entry, int new_slot,
+    int new_page, int new_len, int num_heads, int head_size, int num_kv_heads, float scale,
+    int max_num_blocks_per_seq, int block_size, int kv_block_stride, int kv_head_stride,
+    int kv_dtype, nxt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
