@@ -417,8 +417,11 @@ __device__ __forceinline__ char *o_row(const DecodeParams &p, int s, int h, int 
                     : (char *)p.out + ((size_t)s * p.num_heads + h) * D * eb;
 }
 
-// Clamped length of sequence s.
+// Clamped length of sequence s.  Under the new-token fold
+// (DecodeParams::nt_fold) the one sequence's cached length comes by value,
+// nt_len - 1: no memory round trip.
 __device__ __forceinline__ int seq_len_of(const DecodeParams &p, int s) {
+    if (p.nt_fold) return p.nt_len - 1;
     const int L = p.seq_lens[s];
     return L < 0 ? 0 : (L > p.max_ctx ? p.max_ctx : L);
 }
@@ -1037,28 +1040,41 @@ __device__ __forceinline__ f32x4 load4_elem(const char *row, int i) {
     }
 }
 
-// New-token fold (DecodeParams::nt_fold) of output float4 column c (dims
-// 4c..4c+3) of query head `head` (kv head kvh) of sequence s, whose state
-// over the cached tokens is (m, l, acc) (log2 units; acc = l * the row):
-// the new token's score, q . k_new over the head's C4 = D/4 columns held by
-// an aligned group of C4 consecutive lanes (xor butterfly), then the online
-// log-sum-exp update with v_new.  Returns the finished column.
+// The new token's inputs of output float4 column c (dims 4c..4c+3) of query
+// head `head` (kv head kvh) of sequence s: the query's four values and the
+// token's K and V (DecodeParams::nt_fold).  Loaded when the merge starts, so
+// that their round trip overlaps the partials'.
+struct FoldIn {
+    f32x4 q, k, v;
+};
+
 template <int KV, int D>
-__device__ __forceinline__ f32x4 fold_new_token(const DecodeParams &p, int s, int kvh, int head,
-                                                int c, float m, float l, f32x4 acc) {
-    constexpr int C4 = D / 4;
+__device__ __forceinline__ FoldIn fold_load(const DecodeParams &p, int s, int kvh, int head, int c) {
     constexpr int EB = KV == KV_F32 ? 4 : 2;
+    FoldIn f;
+    f.q = load4_elem<KV>(q_row(p, s, head, D, EB), 4 * c);
+    f.k = load4_elem<KV>((const char *)p.nt_k + (size_t)kvh * D * EB, 4 * c);
+    f.v = load4_elem<KV>((const char *)p.nt_v + (size_t)kvh * D * EB, 4 * c);
+    return f;
+}
+
+// New-token fold of one output column whose state over the cached tokens is
+// (m, l, acc) (log2 units; acc = l * the row): the new token's score, q .
+// k_new over the head's C4 = D/4 columns held by an aligned group of C4
+// consecutive lanes (xor butterfly), then the online log-sum-exp update with
+// v_new.  Returns the finished column.
+template <int D>
+__device__ __forceinline__ f32x4 fold_new_token(const DecodeParams &p, const FoldIn &f, float m,
+                                                float l, f32x4 acc) {
+    constexpr int C4 = D / 4;
     static_assert((C4 & (C4 - 1)) == 0 && C4 <= 32, "a head's columns in one aligned lane group");
-    const f32x4 q = load4_elem<KV>(q_row(p, s, head, D, EB), 4 * c);
-    const f32x4 k = load4_elem<KV>((const char *)p.nt_k + (size_t)kvh * D * EB, 4 * c);
-    const f32x4 v = load4_elem<KV>((const char *)p.nt_v + (size_t)kvh * D * EB, 4 * c);
-    float dot = q.x * k.x + q.y * k.y + q.z * k.z + q.w * k.w;
+    float dot = f.q.x * f.k.x + f.q.y * f.k.y + f.q.z * f.k.z + f.q.w * f.k.w;
 #pragma unroll
     for (int off = 1; off < C4; off <<= 1) dot += __shfl_xor(dot, off);
     const float sc = dot * p.scale_log2;
     const float M = fmaxf(m, sc);
     const float a = fast_exp2(m - M), b = fast_exp2(sc - M);
-    return (acc * a + v * b) * (1.0f / (l * a + b));
+    return (acc * a + f.v * b) * (1.0f / (l * a + b));
 }
 
 // New-token fold: the token's K/V rows of kv head kvh into its cache slot
@@ -1121,14 +1137,27 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
         store_new_token<D, EB>(p, kvh, blockIdx.x == 0);
     if (col0 >= ncols) return;
     const int tid = threadIdx.x;
+    // the new-token fold's threads: the first kMergeCols, one per column
+    FoldIn fi;
+    if constexpr (kFold) {
+        if (p.nt_fold && tid < kMergeCols && col0 + tid < ncols) {
+            const int h = (col0 + tid) / C4;
+            fi = fold_load<KV, D>(p, s, kvh, kvh * p.group + g0 + h, col0 + tid - h * C4);
+        }
+    }
     // the three scalars the merge needs, requested together (the empty asm
     // keeps the compiler from sinking the prefix loads past the L == 0 exit,
-    // which would cost a second round trip).  Under the new-token fold the
-    // cached length is nt_len - 1 (this launch stores nt_len to the lengths
-    // the partition kernel read).
-    const int L = kFold && p.nt_fold ? p.nt_len - 1 : seq_len_of(p, s);
-    const int total = p.ws_prefix[p.num_seqs];
-    const int pre_s = p.ws_prefix[s];
+    // which would cost a second round trip).  Under the new-token fold (one
+    // sequence, its cached length by value) they need no load at all.
+    const int L = seq_len_of(p, s);
+    int total, pre_s;
+    if (kFold && p.nt_fold) {
+        total = segs * segment_units(p, (L + TT - 1) / TT);
+        pre_s = 0;
+    } else {
+        total = p.ws_prefix[p.num_seqs];
+        pre_s = p.ws_prefix[s];
+    }
     asm volatile("" ::"s"(total), "s"(pre_s));
     const size_t qrow0 = ((size_t)s * p.num_heads + (size_t)kvh * p.group + g0) * D;
 
@@ -1138,9 +1167,8 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
                 const int col = col0 + tid;
                 if (tid < kMergeCols && col < ncols) {
                     const int h = col / C4, c = col - h * C4;
-                    const f32x4 o = fold_new_token<KV, D>(p, s, kvh, kvh * p.group + g0 + h, c,
-                                                          -INFINITY, 0.0f,
-                                                          f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                    const f32x4 o = fold_new_token<D>(p, fi, -INFINITY, 0.0f,
+                                                      f32x4{0.0f, 0.0f, 0.0f, 0.0f});
                     char *orow = o_row(p, s, kvh * p.group + g0 + h, D, EB);
 #pragma unroll
                     for (int e = 0; e < 4; e++) store_elem<KV>(orow, c * 4 + e, o[e]);
@@ -1166,8 +1194,8 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
                     const int h = col / C4, c = col - h * C4;
                     const float lse = p.out_lse[qrow0 / D + h];
                     const f32x4 row = *(const f32x4 *)(p.out_f32 + qrow0 + (size_t)h * D + c * 4);
-                    const f32x4 o = fold_new_token<KV, D>(p, s, kvh, kvh * p.group + g0 + h, c,
-                                                          lse, lse == -INFINITY ? 0.0f : 1.0f, row);
+                    const f32x4 o =
+                        fold_new_token<D>(p, fi, lse, lse == -INFINITY ? 0.0f : 1.0f, row);
                     char *orow = o_row(p, s, kvh * p.group + g0 + h, D, EB);
 #pragma unroll
                     for (int e = 0; e < 4; e++) store_elem<KV>(orow, c * 4 + e, o[e]);
@@ -1205,7 +1233,7 @@ __global__ __launch_bounds__(kMergeCols * kMergeSplit) void paged_decode_merge_k
     }
     if constexpr (kFold) {
         if (p.nt_fold) {
-            const f32x4 o = fold_new_token<KV, D>(p, s, kvh, kvh * p.group + g0 + h, c, mm, ll, aa);
+            const f32x4 o = fold_new_token<D>(p, fi, mm, ll, aa);
             char *orow = o_row(p, s, kvh * p.group + g0 + h, D, EB);
 #pragma unroll
             for (int e = 0; e < 4; e++) store_elem<KV>(orow, c * 4 + e, o[e]);

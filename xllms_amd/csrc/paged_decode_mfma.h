@@ -258,7 +258,8 @@ struct CascadeLdsPlan {
 template <int SRC>
 __device__ __forceinline__ int src_len(const DecodeParams &p, const int *__restrict__ lens, int s,
                                        const CascadeLdsPlan *cp) {
-    if constexpr (SRC == kSrcBatch) return min(max(lens[s], 0), p.max_ctx);
+    if constexpr (SRC == kSrcBatch)
+        return p.nt_fold ? p.nt_len - 1 : min(max(lens[s], 0), p.max_ctx);
     else if constexpr (SRC == kSrcSuffix) return __builtin_amdgcn_readfirstlane(cp->slen[s]);
     else return __builtin_amdgcn_readfirstlane(cp->vlen[s]);
 }
