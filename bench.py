@@ -242,26 +242,43 @@ def partition_kernel_name(wl) -> str:
 
 
 def cpu_baseline(wl, budget_s: float) -> dict:
-    """Time the oracle on the host: all threads, then one thread, each on as
-    many whole copies of the batch (or leading sequences) as fit the budget."""
+    """Time the oracle on the host: all threads, then one thread, each on a
+    sample of about budget_s / 2 seconds, as many whole copies of the batch
+    as fit, or else its leading sequences.  The sample is sized from a probe
+    on leading sequences that grows until it takes >= 50 ms, by tokens (a
+    batch whose first sequences are short, like config 5's, would otherwise
+    be sampled far past the budget).  The rate is in this batch's sequences
+    per second: the sample's tokens per second over the batch's tokens per
+    sequence (for whole copies, exactly sequences per second)."""
+    import numpy as np
     from oracle import oracle as O
     threads = O.lib().oracle_num_threads()
+    cum = np.cumsum(np.maximum(np.asarray(wl.seq_lens, dtype=np.int64), 0))
+    total = max(1, int(cum[-1]))
+    tok_per_seq = total / wl.num_seqs
     res = {}
     for name, prec, nthr in (("all", "mt", threads), ("single", "f32", 1)):
-        # probe with the first few sequences to size the sample
-        t0 = time.perf_counter()
-        probe = min(wl.num_seqs, 4)
-        O.run_workload(wl, precision=prec, threads=nthr, seqs=slice(0, probe))
-        dt = max(time.perf_counter() - t0, 1e-6)
-        per_seq = dt / probe
-        nseq = int(max(1, min(wl.num_seqs, budget_s / 2 / per_seq)))
-        reps = 1 if nseq < wl.num_seqs else int(max(1, budget_s / 2 / (per_seq * wl.num_seqs)))
+        k = 1
+        while True:
+            t0 = time.perf_counter()
+            O.run_workload(wl, precision=prec, threads=nthr, seqs=slice(0, k))
+            dt = max(time.perf_counter() - t0, 1e-6)
+            if dt >= 0.05 or k >= wl.num_seqs:
+                break
+            k = min(wl.num_seqs, 4 * k)
+        per_tok = dt / max(1, int(cum[k - 1]))
+        budget_tok = budget_s / 2 / per_tok
+        if budget_tok >= total:
+            nseq, reps = wl.num_seqs, int(max(1, budget_tok // total))
+        else:
+            nseq, reps = int(max(1, np.searchsorted(cum, budget_tok, side="right"))), 1
         t0 = time.perf_counter()
         for _ in range(reps):
             O.run_workload(wl, precision=prec, threads=nthr, seqs=slice(0, nseq))
         dt = time.perf_counter() - t0
-        res[name] = {"seqs": nseq * reps, "seconds": dt, "threads": nthr,
-                     "seqs_per_s": nseq * reps / dt}
+        toks = int(cum[nseq - 1]) * reps
+        res[name] = {"seqs": nseq * reps, "tokens": toks, "seconds": dt, "threads": nthr,
+                     "seqs_per_s": toks / dt / tok_per_seq}
     return res
 
 
@@ -1135,9 +1152,12 @@ def main() -> int:
                "cores": c["all"]["threads"], "kind": "port",
                "sample": (f"oracle/paged_attention_oracle.c (C restatement of text_gen.c:1284-1310"
                           f" over the operator-API buffers, gcc -O2, OpenMP over (seq, head)) on "
-                          f"{c['all']['seqs']} sequences of this batch in {c['all']['seconds']:.1f}s"),
+                          f"{c['all']['seqs']} sequences of this batch ({c['all']['tokens']} "
+                          f"context tokens) in {c['all']['seconds']:.1f}s; seqs/s by tokens over "
+                          f"the batch's tokens per sequence"),
                "single_thread": {"value": round(c["single"]["seqs_per_s"], 3), "cores": 1,
-                                 "sample": f"{c['single']['seqs']} sequences in "
+                                 "sample": f"{c['single']['seqs']} sequences "
+                                           f"({c['single']['tokens']} tokens) in "
                                            f"{c['single']['seconds']:.1f}s"},
                "gbs_all_threads": round(c["all"]["seqs_per_s"] * alg_bytes / wl.num_seqs / 1e9, 2),
                "tokens_per_seq": round(tok_per_seq, 1)}
