@@ -259,3 +259,70 @@ def test_one_request_decode_steps(cuda, dtype, D):
             rids.append("new")
     assert m.close() == 0
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_exec_patterns(cuda, seed):
+    """Seeded random serving sessions: head size (32, 64, 96, 128), element
+    type (fp16, fp32), block size (16, 32) and GQA shape drawn; prompts that
+    share a system prefix or not; every step one new token per live request,
+    run as one whole-batch exec, as one exec per request, or as a random
+    split into smaller batches; now and then a request ends and a new one is
+    admitted (its handle reused).  One-request execs take the path that keeps
+    each sequence's table and length on the device where the head size
+    allows, and every mix of the patterns must leave those copies right.
+    Every output against the oracle."""
+    import torch
+    rng = np.random.default_rng(7000 + seed)
+    D = int(rng.choice([32, 64, 96, 128]))
+    dtype = W.FP32 if rng.random() < 0.3 else W.FP16
+    bs = int(rng.choice([16, 32]))
+    H, KVH = [(8, 2), (16, 4), (8, 8)][int(rng.integers(0, 3))]
+    ref = Driver.__new__(Driver)
+    ref.KVH, ref.H, ref.D, ref.bs = KVH, H, D, bs
+    ref.scale = 1.0 / np.sqrt(D)
+    ref.live, ref._rows = {}, {}
+    code = B.NXT_TYPE_FP32 if dtype == W.FP32 else B.NXT_TYPE_FP16
+    m = B.DecodeModel(num_blocks=512, num_kv_heads=KVH, block_size=bs, head_size=D,
+                      num_heads=H, dtype=code, max_batch_size=8, max_blocks_per_seq=160 // bs)
+    assert m.status == 0
+    c = Client(m, ref, dtype)
+    system = list(rng.integers(0, 50, int(rng.integers(1, 40))))
+    count = [0]
+
+    def admit():
+        rid = f"q{count[0]}"
+        count[0] += 1
+        tail = list(rng.integers(0, 50, int(rng.integers(1, 30))))
+        prompt = system + tail if rng.random() < 0.5 else tail
+        b = c.bind(rid, prompt, rng)
+        assert m.exec([rid]) == 0
+        c.check([rid], {rid: b}, f"seed {seed}: admit {rid}")
+        return rid
+
+    live = [admit() for _ in range(int(rng.integers(2, 6)))]
+    print(f"case seed={seed} d={D} {'fp32' if dtype == W.FP32 else 'fp16'} bs={bs} H={H} "
+          f"KVH={KVH} requests={len(live)}", flush=True)
+    for step in range(30):
+        binds = {rid: c.bind(rid, [int(rng.integers(0, 50))], rng) for rid in live}
+        pattern = int(rng.integers(0, 3))
+        if pattern == 0:
+            assert m.exec(live) == 0
+        elif pattern == 1:
+            for rid in live:
+                assert m.exec([rid]) == 0
+        else:
+            order = list(rng.permutation(live))
+            while order:
+                k = int(rng.integers(1, len(order) + 1))
+                assert m.exec(order[:k]) == 0
+                order = order[k:]
+        c.check(live, binds, f"seed {seed}: step {step} pattern {pattern}")
+        if rng.random() < 0.15 and len(live) > 1:
+            gone = live.pop(int(rng.integers(0, len(live))))
+            c.bind(gone, [], rng, release=True, attend=False)
+            assert m.exec([gone]) == 0
+            del c.hist[gone]
+            live.append(admit())
+    assert m.close() == 0
+    torch.cuda.synchronize()
