@@ -138,6 +138,11 @@ struct InstanceState {
     // per sequence handle ([0] the length, the table from kRecHead on), and
     // the number of tokens the record holds (-1: none), on the host.
     static constexpr int kRecHead = 4;
+    // a record holds at most this many table entries (a model whose table
+    // width is the whole pool would otherwise make every record that wide);
+    // longer sequences take the general exec
+    static constexpr int kRecMaxBlocks = 4096;
+    int rec_blocks = 0;
     DevBuf<int32_t> d_recs;
     std::vector<int32_t> dev_len;
     size_t rec_ints = 0;
@@ -425,7 +430,8 @@ XMI_EXPORT int nxt_model_instance_init(NxtModelInstance *instance) {
     if (e == hipSuccess && !st->d_state.reserve((size_t)s.num_heads * (s.head_size + 1)))
         e = hipErrorOutOfMemory;
     // a record: the head, then a table row, in whole 256-byte units
-    st->rec_ints = ((size_t)InstanceState::kRecHead + (size_t)s.max_blocks + 63) & ~(size_t)63;
+    st->rec_blocks = std::min(s.max_blocks, InstanceState::kRecMaxBlocks);
+    st->rec_ints = ((size_t)InstanceState::kRecHead + (size_t)st->rec_blocks + 63) & ~(size_t)63;
     if (e != hipSuccess) {
         destroy_state(st);
         return fail("instance init: %s (K/V caches of %zu bytes each)", hipGetErrorString(e),
@@ -543,8 +549,12 @@ bool fast_ok(const InstanceState *st, const std::vector<Item> &items) {
     if (items.size() != 1) return false;
     const Item &it = items[0];
     const int d = st->spec.head_size;
-    return it.seq >= 0 && it.io.num_tokens == 1 && it.io.query && it.io.output && st->d_state.p &&
-           (d == 32 || d == 64 || d == 128);
+    if (it.seq < 0 || it.io.num_tokens != 1 || !it.io.query || !it.io.output || !st->d_state.p ||
+        !(d == 32 || d == 64 || d == 128))
+        return false;
+    // the sequence with its new token fits a record
+    const long long len = (long long)nxt_kv_seq_len(st->index, it.seq) + 1;
+    return len <= (long long)st->rec_blocks * st->spec.block_size;
 }
 
 // A one-request decode step without the staging launch: the sequence's
