@@ -566,17 +566,19 @@ bool fast_ok(const InstanceState *st, const std::vector<Item> &items) {
 // page, and the new length (xhip_paged_attention_fold_new).
 int fast_step(InstanceState *st, Item &it) {
     const ModelSpec &s = st->spec;
+    const int L = nxt_kv_seq_len(st->index, it.seq) + 1;  // with the new token
+    const int width = (L + s.block_size - 1) / s.block_size;
+    const size_t n = ((size_t)InstanceState::kRecHead + (size_t)width + 3) & ~(size_t)3;
+    // (what can run out, before the index takes the token: after that its
+    // rows must reach the cache)
+    if (!st->ensure_recs(it.seq + 1)) return fail("exec: out of device memory");
+    if (!st->h_rec.reserve(n)) return fail("exec: out of host memory");
     int32_t slot = -1;
     const int r = nxt_kv_seq_append(st->index, it.seq, it.io.token_ids, 1, &slot);
     if (r != NXT_KV_OK) return fail("exec: appending to %s failed (%d)", it.id.c_str(), r);
-    const int L = nxt_kv_seq_len(st->index, it.seq);  // with the new token
-    const int width = (L + s.block_size - 1) / s.block_size;
-    if (!st->ensure_recs(it.seq + 1)) return fail("exec: out of device memory");
     int32_t *rec = st->d_recs.p + (size_t)it.seq * st->rec_ints;
     if (st->dev_len[(size_t)it.seq] != L - 1) {
         st->dev_len[(size_t)it.seq] = -1;
-        const size_t n = ((size_t)InstanceState::kRecHead + (size_t)width + 3) & ~(size_t)3;
-        if (!st->h_rec.reserve(n)) return fail("exec: out of host memory");
         std::memset(st->h_rec.p, 0, n * sizeof(int32_t));
         int32_t len_now = 0;
         if (nxt_kv_batch_tables(st->index, &it.seq, 1, width,
