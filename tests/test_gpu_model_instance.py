@@ -326,3 +326,78 @@ def test_random_exec_patterns(cuda, seed):
             live.append(admit())
     assert m.close() == 0
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype,D,bs", [(W.FP16, 128, 16), (W.FP32, 64, 32), (W.FP16, 96, 16)],
+                         ids=["fp16-d128-bs16", "fp32-d64-bs32", "fp16-d96-bs16"])
+def test_batch_tables_kept_on_device(cuda, dtype, D, bs):
+    """Whole-batch execs keep the batch's block tables on the device: an exec
+    over the same requests in the same order, whose sequences grew only by
+    its own appends, stores just the entries of the pages those appends
+    opened.  Steps append 1 to 40 tokens per request (pages opened on every
+    kind of boundary, and rows outgrowing their spare entries, which uploads
+    the tables again); between them, requests grow outside the batch (a
+    K/V-only exec, a one-request exec), the order changes and changes back,
+    a deferred-mode flush runs the same batch, and a released request's
+    handle goes to a new one.  Every output against the oracle."""
+    import torch
+    rng = np.random.default_rng(17)
+    H, KVH = 16, 4
+    ref = Driver.__new__(Driver)
+    ref.KVH, ref.H, ref.D, ref.bs = KVH, H, D, bs
+    ref.scale = 1.0 / np.sqrt(D)
+    ref.live, ref._rows = {}, {}
+    code = B.NXT_TYPE_FP32 if dtype == W.FP32 else B.NXT_TYPE_FP16
+    m = B.DecodeModel(num_blocks=1024, num_kv_heads=KVH, block_size=bs, head_size=D,
+                      num_heads=H, dtype=code, max_batch_size=8,
+                      max_blocks_per_seq=2048 // bs)
+    assert m.status == 0
+    c = Client(m, ref, dtype)
+    rids = [f"t{i}" for i in range(5)]
+    for n, rid in zip([1, bs - 1, bs, bs + 1, 3 * bs + 7], rids):
+        b = c.bind(rid, list(rng.integers(0, 60, n)), rng)
+        assert m.exec([rid]) == 0
+        c.check([rid], {rid: b}, f"prefill {rid}")
+    order = list(rids)
+    for step in range(48):
+        # (the first 20 steps grow fast, so rows outgrow their spare entries)
+        grow = [int(rng.choice([20, 40] if step < 20 else [1, 1, 2, 7, 20, 40])) for _ in order]
+        binds = {rid: c.bind(rid, list(rng.integers(0, 60, k)), rng)
+                 for rid, k in zip(order, grow)}
+        if step < 20:
+            assert m.exec(order) == 0
+        elif step % 12 == 5:  # the same batch through deferred mode's flush
+            assert m.set_deferred(True) == 0
+            for rid in order:
+                assert m.exec([rid]) == 0
+            assert m.flush() == 0
+            assert m.set_deferred(False) == 0
+        else:
+            assert m.exec(order) == 0
+        c.check(order, binds, f"step {step} grow {grow}")
+        if step < 20:
+            continue
+        if step % 12 == 3:  # one request grows outside the batch: K/V only
+            rid = order[int(rng.integers(0, len(order)))]
+            c.bind(rid, list(rng.integers(0, 60, 3)), rng, attend=False)
+            assert m.exec([rid]) == 0
+        elif step % 12 == 7:  # ... or by a one-request decode step
+            rid = order[int(rng.integers(0, len(order)))]
+            b = c.bind(rid, [int(rng.integers(0, 60))], rng)
+            assert m.exec([rid]) == 0
+            c.check([rid], {rid: b}, f"step {step}: one-request exec of {rid}")
+        elif step % 12 == 9:  # another order, and back two steps later
+            order = list(rng.permutation(order))
+        elif step % 12 == 11:
+            order = sorted(order, key=lambda r: (len(r), r))
+        if step == 30:
+            gone = order.pop(2)
+            c.bind(gone, [], rng, release=True, attend=False)
+            assert m.exec([gone]) == 0
+            del c.hist[gone]
+            b = c.bind("late", list(rng.integers(0, 60, 2 * bs + 3)), rng)
+            assert m.exec(["late"]) == 0
+            c.check(["late"], {"late": b}, "admitted after a release")
+            order.insert(2, "late")
+    assert m.close() == 0
+    torch.cuda.synchronize()

@@ -148,9 +148,25 @@ struct InstanceState {
     size_t rec_ints = 0;
     DevBuf<float> d_state;      // fp32 rows [num_heads][head_size], then their lse [num_heads]
     HostBuf<int32_t> h_rec;     // staging of one record
+    // The general exec's block tables, kept on the device between execs:
+    // the last attention batch's sequences (bt_seqs, in batch order), their
+    // tables in rows of bt_stride entries (bt_dev) and the length each row
+    // covers (bt_len).  An exec over the same sequences in the same order,
+    // each grown since only by this exec's own appends, uploads the entries
+    // of the pages those appends opened (h_upd: (index, page) pairs) instead
+    // of every table.  Rows are built with kTableSlack spare entries.
+    static constexpr int kTableSlack = 16;
+    std::vector<int32_t> bt_seqs, bt_len;
+    int bt_stride = 0;
+    bool bt_valid = false;
+    DevBuf<int32_t> bt_dev;
+    HostBuf<int32_t> h_upd;
 
     void forget_device_row(int32_t seq) {
         if (seq >= 0 && (size_t)seq < dev_len.size()) dev_len[(size_t)seq] = -1;
+        // (an admission that reuses the handle, a release or a failure)
+        if (bt_valid && std::find(bt_seqs.begin(), bt_seqs.end(), seq) != bt_seqs.end())
+            bt_valid = false;
     }
     // Records for handles [0, n): grown by doubling; a new buffer holds
     // none (the old records are dropped with it).
@@ -263,6 +279,8 @@ void destroy_state(InstanceState *st) {
     st->d_recs.release();
     st->d_state.release();
     st->h_rec.release();
+    st->bt_dev.release();
+    st->h_upd.release();
     if (st->done) (void)hipHostFree(st->done);
     st->done = nullptr;
     // the operator layer keeps split-K / cascade workspaces per stream:
@@ -347,6 +365,11 @@ struct Item {
     std::string id;
     NxtDecodeIo io;
     int32_t seq;  // -1: admitted by this exec
+    // (general exec) the sequence's length before this exec's tokens (-1:
+    // admitted by it), and its pages opened by them: entries [open0, open0 +
+    // nopen) of the exec's (table entry, page) list
+    int32_t len0 = -1;
+    size_t open0 = 0, nopen = 0;
 };
 
 int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<std::string> &ids);
@@ -616,10 +639,14 @@ int slow_step(InstanceState *st, std::vector<Item> &items, PhaseTrace &tr) {
     const size_t kv_row = (size_t)s.num_kv_heads * s.head_size * s.elem_bytes;
     st->h_slots.n = st->h_src.n = st->h_dst.n = st->h_kptr.n = st->h_vptr.n = 0;
     std::vector<int32_t> mapping, src, dst, slots;
+    std::vector<std::pair<int32_t, int32_t>> opened;  // (table entry, page) of the appends
     int rc = 0;
     for (Item &it : items) {
         const int n = it.io.num_tokens;
-        if (n == 0) continue;
+        if (n == 0) {
+            it.len0 = nxt_kv_seq_len(st->index, it.seq);
+            continue;
+        }
         slots.assign((size_t)n, -1);
         if (it.seq < 0) {
             mapping.resize((size_t)n);
@@ -649,6 +676,14 @@ int slow_step(InstanceState *st, std::vector<Item> &items, PhaseTrace &tr) {
                 rc = fail("exec: appending to %s failed (%d)", it.id.c_str(), r);
                 break;
             }
+            it.len0 = nxt_kv_seq_len(st->index, it.seq) - n;
+            it.open0 = opened.size();
+            for (int t = 0; t < n; ++t) {
+                const int pos = it.len0 + t;
+                if (pos % s.block_size == 0)
+                    opened.push_back({pos / s.block_size, slots[(size_t)t] / s.block_size});
+            }
+            it.nopen = opened.size() - it.open0;
         }
         for (int t = 0; t < n; ++t) {
             if (slots[(size_t)t] < 0) continue;
@@ -659,10 +694,13 @@ int slow_step(InstanceState *st, std::vector<Item> &items, PhaseTrace &tr) {
     }
 
     tr.mark("index");
-    // 2. the attention batch: requests with a query, their tables and groups
+    // 2. the attention batch: requests with a query, their lengths, tables
+    //    (the device-resident ones updated, or all of them uploaded) and groups
     st->h_seqs.n = st->h_qptr.n = st->h_optr.n = 0;
-    st->h_bt.n = st->h_lens.n = st->h_group.n = st->h_pblocks.n = 0;
-    int width = 1, ng = 0;
+    st->h_bt.n = st->h_lens.n = st->h_group.n = st->h_pblocks.n = st->h_upd.n = 0;
+    int width = 1, ng = 0, stride = 0;
+    bool update = false;  // the device-resident tables are updated, not uploaded
+    if (rc == 0 && !st->h_lens.reserve(items.size())) rc = fail("exec: out of host memory");
     if (rc == 0) {
         for (const Item &it : items) {
             if (!it.io.query) continue;
@@ -670,18 +708,56 @@ int slow_step(InstanceState *st, std::vector<Item> &items, PhaseTrace &tr) {
             st->h_qptr.push((const char *)it.io.query);
             st->h_optr.push((char *)it.io.output);
             const int len = nxt_kv_seq_len(st->index, it.seq);
+            st->h_lens.p[st->h_lens.n++] = len;
             width = std::max(width, (len + s.block_size - 1) / s.block_size);
         }
         const int B = (int)st->h_seqs.n;
-        if (B > 0) {
-            if (!st->h_bt.reserve((size_t)B * width) || !st->h_lens.reserve((size_t)B) ||
-                !st->h_group.reserve((size_t)B) || !st->h_pblocks.reserve((size_t)B / 2 + 1)) {
+        update = st->bt_valid && B > 0 && (size_t)B == st->bt_seqs.size() &&
+                 std::equal(st->bt_seqs.begin(), st->bt_seqs.end(), st->h_seqs.p) &&
+                 width <= st->bt_stride;
+        if (update) {
+            // every row covers its sequence up to this exec's tokens
+            int i = 0;
+            for (const Item &it : items) {
+                if (!it.io.query) continue;
+                if (it.len0 != st->bt_len[(size_t)i++]) {
+                    update = false;
+                    break;
+                }
+            }
+        }
+        if (B > 0 && update) {
+            stride = st->bt_stride;
+            if (!st->h_upd.reserve(2 * opened.size() + 2)) {
                 rc = fail("exec: out of host memory");
             } else {
-                st->h_bt.n = (size_t)B * width;
-                st->h_lens.n = st->h_group.n = (size_t)B;
-                nxt_kv_batch_tables(st->index, st->h_seqs.p, B, width, st->h_bt.p, st->h_lens.p);
-                tr.mark("tables");
+                int i = 0;
+                for (const Item &it : items) {
+                    if (!it.io.query) continue;
+                    for (size_t k = it.open0; k < it.open0 + it.nopen; ++k) {
+                        st->h_upd.p[st->h_upd.n++] = i * stride + opened[k].first;
+                        st->h_upd.p[st->h_upd.n++] = opened[k].second;
+                    }
+                    ++i;
+                }
+            }
+        } else if (B > 0) {
+            stride = std::min(((width + InstanceState::kTableSlack + 15) / 16) * 16,
+                              std::max(s.max_blocks, width));
+            if (!st->h_bt.reserve((size_t)B * stride) ||
+                !st->bt_dev.reserve((size_t)B * stride + 64)) {
+                rc = fail("exec: out of memory");
+            } else {
+                st->h_bt.n = (size_t)B * stride;
+                nxt_kv_batch_tables(st->index, st->h_seqs.p, B, stride, st->h_bt.p, st->h_lens.p);
+            }
+        }
+        tr.mark(update ? "updates" : "tables");
+        if (rc == 0 && B > 0) {
+            if (!st->h_group.reserve((size_t)B) || !st->h_pblocks.reserve((size_t)B / 2 + 1)) {
+                rc = fail("exec: out of host memory");
+            } else {
+                st->h_group.n = (size_t)B;
                 nxt_kv_batch_prefix_groups(st->index, st->h_seqs.p, B, st->h_group.p,
                                            st->h_pblocks.p, &ng);
                 st->h_pblocks.n = (size_t)std::max(ng, 1);
@@ -695,12 +771,15 @@ int slow_step(InstanceState *st, std::vector<Item> &items, PhaseTrace &tr) {
     //    this exec writes), the query gather, the attention, the output scatter
     hipError_t e = hipSuccess;
     st->h_pack.n = 0;
+    // (the tables first: the staging launch puts the pack's first
+    // head_bytes into bt_dev and the rest into d_pack)
+    st->pack(st->h_bt);
+    const size_t head_bytes = st->h_bt.n ? (st->h_pack.n + 255) & ~(size_t)255 : 0;
     const size_t o_slots = st->pack(st->h_slots), o_kptr = st->pack(st->h_kptr),
                  o_vptr = st->pack(st->h_vptr), o_src = st->pack(st->h_src),
-                 o_dst = st->pack(st->h_dst), o_bt = st->pack(st->h_bt),
-                 o_lens = st->pack(st->h_lens), o_group = st->pack(st->h_group),
-                 o_pblocks = st->pack(st->h_pblocks), o_qptr = st->pack(st->h_qptr),
-                 o_optr = st->pack(st->h_optr);
+                 o_dst = st->pack(st->h_dst), o_lens = st->pack(st->h_lens),
+                 o_group = st->pack(st->h_group), o_pblocks = st->pack(st->h_pblocks),
+                 o_qptr = st->pack(st->h_qptr), o_optr = st->pack(st->h_optr);
     tr.mark("pack");
     // The rows of requests admitted or extended before a failure are still
     // written: the index already holds their tokens.
@@ -720,28 +799,39 @@ int slow_step(InstanceState *st, std::vector<Item> &items, PhaseTrace &tr) {
     // The staging copy, and in the same launch the new tokens' K/V rows,
     // whose slots and row pointers that launch reads from the host-pinned
     // pack (launch_stage_copy_append).
+    xhip::StageTables tables;
+    tables.head = st->bt_dev.p;
+    tables.head_bytes = (long long)head_bytes;
+    tables.pairs = st->h_upd.p;
+    tables.count = (int)(st->h_upd.n / 2);
+    tables.table = st->bt_dev.p;
     if (st->h_pack.n == (size_t)-1) {
         rc = fail("exec: out of host memory");
+    } else if (head_bytes && st->h_pack.n <= head_bytes) {
+        rc = fail("exec: staging layout");  // (the lengths always follow the tables)
     } else if (st->h_pack.n > 0) {
-        if (!st->d_pack.reserve((st->h_pack.n + 15) & ~(size_t)15)) {
+        const size_t bytes = (st->h_pack.n + 15) & ~(size_t)15;
+        if (!st->d_pack.reserve(bytes - head_bytes)) {
             rc = fail("exec: out of device memory");
         } else {
-            const size_t bytes = (st->h_pack.n + 15) & ~(size_t)15;
             if (st->h_slots.n) {
                 xhip::KvAppendParams w = p;
                 w.slots = (const int *)(hp + o_slots);
                 w.key_rows = (const char *const *)(hp + o_kptr);
                 w.value_rows = (const char *const *)(hp + o_vptr);
                 w.num_tokens = (int)st->h_slots.n;
-                e = xhip::launch_stage_copy_append(st->d_pack.p, hp, bytes, w, st->stream);
+                e = xhip::launch_stage_copy_append(st->d_pack.p, hp, bytes, w, st->stream,
+                                                   &tables);
             } else {
-                e = xhip::launch_stage_copy(st->d_pack.p, hp, bytes, st->stream);
+                e = xhip::launch_stage_copy(st->d_pack.p, hp, bytes, st->stream, &tables);
             }
             staged = e == hipSuccess;
         }
     }
+    // device address of the part at pack offset `off` (every part but the
+    // tables lies past head_bytes)
     char *const dp = st->d_pack.p;
-    auto at = [dp](size_t off) { return (void *)(dp + off); };
+    auto at = [dp, head_bytes](size_t off) { return (void *)(dp + (off - head_bytes)); };
     if (staged && e == hipSuccess && st->h_src.n) {
         xhip::KvAppendParams c = p;
         c.key = st->key_cache;
@@ -758,22 +848,32 @@ int slow_step(InstanceState *st, std::vector<Item> &items, PhaseTrace &tr) {
         // rows in place, through the staged row pointer tables
         const int kbs = s.num_kv_heads * s.block_size * s.head_size;
         const int khs = s.block_size * s.head_size;
-        const int *bt = (const int *)at(o_bt), *lens = (const int *)at(o_lens);
+        const int *bt = st->bt_dev.p, *lens = (const int *)at(o_lens);
         const char *const *qr = (const char *const *)at(o_qptr);
         char *const *orw = (char *const *)at(o_optr);
         const int a =
             ng > 0 ? xhip_paged_attention_cascade_rows(
                          qr, orw, st->key_cache, st->value_cache, bt, lens,
                          (const int *)at(o_group), (const int *)at(o_pblocks), ng, B, s.num_heads,
-                         s.head_size, s.num_kv_heads, s.scale, width, s.block_size, kbs, khs,
+                         s.head_size, s.num_kv_heads, s.scale, stride, s.block_size, kbs, khs,
                          s.kv_dtype, st->stream)
                    : xhip_paged_attention_rows(qr, orw, st->key_cache, st->value_cache, bt, lens,
                                                B, s.num_heads, s.head_size, s.num_kv_heads,
-                                               s.scale, width, s.block_size, kbs, khs, s.kv_dtype,
-                                               st->stream);
+                                               s.scale, stride, s.block_size, kbs, khs,
+                                               s.kv_dtype, st->stream);
         if (a != NXT_ATTN_OK) rc = fail("exec: attention: %s", nxt_attn_last_error());
     }
-
+    // what the device-resident tables now hold
+    if (B > 0 || rc != 0) {
+        st->bt_valid = rc == 0 && staged;
+        if (st->bt_valid) {
+            if (!update) {
+                st->bt_seqs.assign(st->h_seqs.p, st->h_seqs.p + B);
+                st->bt_stride = stride;
+            }
+            st->bt_len.assign(st->h_lens.p, st->h_lens.p + B);
+        }
+    }
     return rc;
 }
 

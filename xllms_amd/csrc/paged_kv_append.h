@@ -39,15 +39,32 @@ struct KvAppendParams {
 
 hipError_t launch_kv_append(const KvAppendParams &p, hipStream_t stream);
 
+// Block-table work of a staging launch (the model instance's tables kept on
+// the device between execs): the first head_bytes of the staged bytes go to
+// `head` (a whole upload of the tables) instead of the destination, whose
+// first byte then receives staged byte head_bytes; and `count` (index,
+// value) int pairs, host-pinned, are stored as table[index] = value (the
+// entries of pages opened since the last upload).
+struct StageTables {
+    void *head;
+    long long head_bytes;  // a multiple of 16
+    const int *pairs;
+    int count;
+    int *table;
+};
+
 // Copies `bytes` (a multiple of 16; both addresses 16-byte aligned) from
-// host-pinned memory to device memory with a kernel on `stream`.
-hipError_t launch_stage_copy(void *dst, const void *host_src, size_t bytes, hipStream_t stream);
+// host-pinned memory to device memory with a kernel on `stream`, with the
+// table work of `t` when set.
+hipError_t launch_stage_copy(void *dst, const void *host_src, size_t bytes, hipStream_t stream,
+                             const StageTables *t = nullptr);
 
 // launch_stage_copy and launch_kv_append(p) in one launch; p's per-token
 // arrays (slots, key_rows, value_rows; src_slots unused) must be readable
 // by the device where they are, e.g. in the host-pinned source being copied.
 hipError_t launch_stage_copy_append(void *dst, const void *host_src, size_t bytes,
-                                    const KvAppendParams &p, hipStream_t stream);
+                                    const KvAppendParams &p, hipStream_t stream,
+                                    const StageTables *t = nullptr);
 
 // Queues a one-thread kernel that stores `value` to `word` (host-coherent
 // pinned memory) with system scope, after everything queued on `stream`.

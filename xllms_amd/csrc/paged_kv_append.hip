@@ -103,21 +103,59 @@ hipError_t launch_kv_append(const KvAppendParams &params, hipStream_t stream) {
 // each exec's arrays this way instead of with a DMA copy: a small copy went
 // through the DMA engine in ~6.7 us plus its submission, this kernel's reads
 // take one host-link round trip.
-__global__ __launch_bounds__(256) void stage_copy_kernel(const u32x4 *__restrict__ src,
-                                                         u32x4 *__restrict__ dst, long long n16) {
-    const long long stride = (long long)gridDim.x * blockDim.x;
-    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
-        dst[i] = src[i];
+//
+// One thread's share of a staging copy: 16-byte chunk i of the staged
+// bytes, to the tables' head or to dst; the first workgroup also stores the
+// table entries.
+__device__ __forceinline__ void stage_chunks(const u32x4 *__restrict__ src, u32x4 *__restrict__ dst,
+                                             long long n16, unsigned blocks,
+                                             const StageTables &t) {
+    const long long stride = (long long)blocks * 256;
+    const long long head16 = t.head_bytes / 16;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride) {
+        const u32x4 v = src[i];
+        if (i < head16)
+            ((u32x4 *)t.head)[i] = v;
+        else
+            dst[i - head16] = v;
+    }
+    if (blockIdx.x == 0)
+        for (int j = threadIdx.x; j < t.count; j += 256) t.table[t.pairs[2 * j]] = t.pairs[2 * j + 1];
 }
 
-hipError_t launch_stage_copy(void *dst, const void *host_src, size_t bytes, hipStream_t stream) {
-    if (bytes == 0) return hipSuccess;
+__global__ __launch_bounds__(256) void stage_copy_kernel(const u32x4 *__restrict__ src,
+                                                         u32x4 *__restrict__ dst, long long n16,
+                                                         const StageTables t) {
+    stage_chunks(src, dst, n16, gridDim.x, t);
+}
+
+static StageTables no_tables() {
+    StageTables t;
+    t.head = nullptr;
+    t.head_bytes = 0;
+    t.pairs = nullptr;
+    t.count = 0;
+    t.table = nullptr;
+    return t;
+}
+
+static bool tables_ok(const StageTables &t, size_t bytes) {
+    return t.head_bytes >= 0 && (size_t)t.head_bytes <= bytes && (t.head_bytes & 15) == 0 &&
+           (t.head_bytes == 0 || t.head) && t.count >= 0 && (t.count == 0 || (t.pairs && t.table));
+}
+
+hipError_t launch_stage_copy(void *dst, const void *host_src, size_t bytes, hipStream_t stream,
+                             const StageTables *tables) {
+    const StageTables t = tables ? *tables : no_tables();
+    if (bytes == 0 && t.count == 0) return hipSuccess;
     if ((bytes | (uintptr_t)dst | (uintptr_t)host_src) & 15) return hipErrorInvalidValue;
+    if (!tables_ok(t, bytes)) return hipErrorInvalidValue;
     const long long n16 = (long long)(bytes / 16);
     long long blocks = (n16 + 255) / 256;
     if (blocks > 1024) blocks = 1024;
+    if (blocks < 1) blocks = 1;
     stage_copy_kernel<<<(unsigned)blocks, 256, 0, stream>>>((const u32x4 *)host_src, (u32x4 *)dst,
-                                                             n16);
+                                                             n16, t);
     return hipGetLastError();
 }
 
@@ -130,26 +168,28 @@ hipError_t launch_stage_copy(void *dst, const void *host_src, size_t bytes, hipS
 __global__ __launch_bounds__(256) void stage_append_kernel(const u32x4 *__restrict__ src,
                                                            u32x4 *__restrict__ dst, long long n16,
                                                            unsigned copy_blocks,
-                                                           const KvAppendParams p) {
+                                                           const KvAppendParams p,
+                                                           const StageTables t) {
     if (blockIdx.x < copy_blocks) {
-        const long long stride = (long long)copy_blocks * 256;
-        for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride)
-            dst[i] = src[i];
+        stage_chunks(src, dst, n16, copy_blocks, t);
         return;
     }
     append_chunk(p, (blockIdx.x - copy_blocks) * 256 + threadIdx.x);
 }
 
 hipError_t launch_stage_copy_append(void *dst, const void *host_src, size_t bytes,
-                                    const KvAppendParams &params, hipStream_t stream) {
+                                    const KvAppendParams &params, hipStream_t stream,
+                                    const StageTables *tables) {
     KvAppendParams p = params;
+    const StageTables t = tables ? *tables : no_tables();
     const long long per_token = (long long)p.num_kv_heads * p.row_chunks;
     const long long chunks = (long long)p.num_tokens * per_token;
     if (bytes == 0 || chunks <= 0 || chunks > (1LL << 24)) {  // (the separate launches)
-        hipError_t e = launch_stage_copy(dst, host_src, bytes, stream);
+        hipError_t e = launch_stage_copy(dst, host_src, bytes, stream, tables);
         return e != hipSuccess ? e : launch_kv_append(params, stream);
     }
     if ((bytes | (uintptr_t)dst | (uintptr_t)host_src) & 15) return hipErrorInvalidValue;
+    if (!tables_ok(t, bytes)) return hipErrorInvalidValue;
     p.row_div = div_magic((uint32_t)p.row_chunks);
     p.head_div = div_magic((uint32_t)p.num_kv_heads);
     p.tok0 = 0;
@@ -159,7 +199,7 @@ hipError_t launch_stage_copy_append(void *dst, const void *host_src, size_t byte
     if (copy_blocks > 1024) copy_blocks = 1024;
     const long long blocks = copy_blocks + (chunks + 255) / 256;
     stage_append_kernel<<<(unsigned)blocks, 256, 0, stream>>>(
-        (const u32x4 *)host_src, (u32x4 *)dst, n16, (unsigned)copy_blocks, p);
+        (const u32x4 *)host_src, (u32x4 *)dst, n16, (unsigned)copy_blocks, p, t);
     return hipGetLastError();
 }
 
