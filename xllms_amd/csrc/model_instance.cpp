@@ -155,9 +155,11 @@ struct InstanceState {
     // each grown since only by this exec's own appends, uploads the entries
     // of the pages those appends opened (h_upd: (index, page) pairs) instead
     // of every table.  Rows are built with kTableSlack spare entries.
+    // The batch's prefix groups (nxt_kv_batch_prefix_groups) go with them:
+    // appends never share pages, so they change only with the batch.
     static constexpr int kTableSlack = 16;
-    std::vector<int32_t> bt_seqs, bt_len;
-    int bt_stride = 0;
+    std::vector<int32_t> bt_seqs, bt_len, bt_group, bt_pblocks;
+    int bt_stride = 0, bt_ng = 0;
     bool bt_valid = false;
     DevBuf<int32_t> bt_dev;
     HostBuf<int32_t> h_upd;
@@ -756,6 +758,13 @@ int slow_step(InstanceState *st, std::vector<Item> &items, PhaseTrace &tr) {
         if (rc == 0 && B > 0) {
             if (!st->h_group.reserve((size_t)B) || !st->h_pblocks.reserve((size_t)B / 2 + 1)) {
                 rc = fail("exec: out of host memory");
+            } else if (update) {
+                ng = st->bt_ng;
+                st->h_group.n = st->bt_group.size();
+                st->h_pblocks.n = st->bt_pblocks.size();
+                std::memcpy(st->h_group.p, st->bt_group.data(), st->h_group.n * sizeof(int32_t));
+                std::memcpy(st->h_pblocks.p, st->bt_pblocks.data(),
+                            st->h_pblocks.n * sizeof(int32_t));
             } else {
                 st->h_group.n = (size_t)B;
                 nxt_kv_batch_prefix_groups(st->index, st->h_seqs.p, B, st->h_group.p,
@@ -870,6 +879,9 @@ int slow_step(InstanceState *st, std::vector<Item> &items, PhaseTrace &tr) {
             if (!update) {
                 st->bt_seqs.assign(st->h_seqs.p, st->h_seqs.p + B);
                 st->bt_stride = stride;
+                st->bt_group.assign(st->h_group.p, st->h_group.p + st->h_group.n);
+                st->bt_pblocks.assign(st->h_pblocks.p, st->h_pblocks.p + st->h_pblocks.n);
+                st->bt_ng = ng;
             }
             st->bt_len.assign(st->h_lens.p, st->h_lens.p + B);
         }
@@ -908,6 +920,9 @@ int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<st
     tr.mark("validate");
     int rc = fast_ok(st, items) ? fast_step(st, items[0]) : slow_step(st, items, tr);
     tr.mark("launch");
+    // the bindings are consumed (the items hold what the exec needs), while
+    // the device works
+    for (const Item &it : items) st->bound.erase(it.id);
     // wait for the device (wait_exec: the completion word; polling
     // hipStreamQuery instead of hipStreamSynchronize took 6-8 us longer per
     // exec), then end the released requests
@@ -916,7 +931,6 @@ int exec_ids(NxtModelInstance *instance, InstanceState *st, const std::vector<st
     if (rc != 0)  // what the device holds of the exec's sequences is unknown
         for (const Item &it : items) st->forget_device_row(it.seq);
     for (const Item &it : items) {
-        st->bound.erase(it.id);
         if (rc == 0 && it.io.release && it.seq >= 0) {
             nxt_kv_seq_release(st->index, it.seq, 1);
             st->forget_device_row(it.seq);  // its handle may be reused
