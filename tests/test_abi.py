@@ -126,6 +126,31 @@ def test_workspace_cache_threads(tmp_path, sanitize):
     assert "WARNING: ThreadSanitizer" not in r.stderr
 
 
+@pytest.mark.parametrize("variant", [[], ["-fsanitize=address,undefined", "-g"],
+                                     ["-DPLANT_DROP_UPDATES"], ["-DPLANT_NO_FORGET"]],
+                         ids=["plain", "asan-ubsan", "planted-drop-updates", "planted-no-forget"])
+def test_resident_batch_tables(tmp_path, variant):
+    """The model instance's block tables kept on the device between execs
+    (xllms_amd/csrc/batch_tables.h), on a host model of the KV index and of the
+    device rows (tests/c/batch_tables_test.cpp): 400 random sessions of
+    same-order batches growing by 1-40 tokens, requests growing outside the
+    batch, reorders, subsets, failed execs, releases and admissions that reuse
+    handles; after every exec each row holds its sequence's pages, then -1.
+    With the in-place updates or the release / admission notices planted out
+    of the model, the checker must report stale rows."""
+    exe = str(tmp_path / "batch_tables_test")
+    subprocess.run(["g++", "-std=c++17", "-O1", "-Wall", *variant,
+                    f"-I{os.path.join(ROOT, 'xllms_amd', 'csrc')}", "-o", exe,
+                    os.path.join(ROOT, "tests", "c", "batch_tables_test.cpp")], check=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=300)
+    print(r.stdout, r.stderr[-2000:])
+    if any(v.startswith("-DPLANT") for v in variant):
+        assert r.returncode != 0 and "stale rows" in r.stderr
+        return
+    assert r.returncode == 0 and "PASSED" in r.stdout
+    assert "runtime error" not in r.stderr and "AddressSanitizer" not in r.stderr
+
+
 @pytest.mark.parametrize("variant", [[], ["-fsanitize=thread", "-g"], ["-DPLANT_NO_WAIT"]],
                          ids=["plain", "tsan", "planted-no-wait"])
 def test_noalloc_gate_threads(tmp_path, variant):

@@ -16,6 +16,7 @@
 #include <unordered_map>
 #include <vector>
 
+#include "batch_tables.h"
 #include "paged_kv_append.h"
 #include "paged_decode_rows.h"
 #include "workspace.h"
@@ -148,27 +149,18 @@ struct InstanceState {
     size_t rec_ints = 0;
     DevBuf<float> d_state;      // fp32 rows [num_heads][head_size], then their lse [num_heads]
     HostBuf<int32_t> h_rec;     // staging of one record
-    // The general exec's block tables, kept on the device between execs:
-    // the last attention batch's sequences (bt_seqs, in batch order), their
-    // tables in rows of bt_stride entries (bt_dev) and the length each row
-    // covers (bt_len).  An exec over the same sequences in the same order,
-    // each grown since only by this exec's own appends, uploads the entries
-    // of the pages those appends opened (h_upd: (index, page) pairs) instead
-    // of every table.  Rows are built with kTableSlack spare entries.
-    // The batch's prefix groups (nxt_kv_batch_prefix_groups) go with them:
-    // appends never share pages, so they change only with the batch.
-    static constexpr int kTableSlack = 16;
-    std::vector<int32_t> bt_seqs, bt_len, bt_group, bt_pblocks;
-    int bt_stride = 0, bt_ng = 0;
-    bool bt_valid = false;
+    // The general exec's block tables, kept on the device between execs
+    // (bt_dev, rows of bt.stride entries; bt: what they hold, and when an
+    // exec may update them in place, batch_tables.h), the (index, page)
+    // pairs of one exec's update (h_upd), and the batch's lengths before its
+    // appends (h_len0).
+    xhip::ResidentTables bt;
     DevBuf<int32_t> bt_dev;
-    HostBuf<int32_t> h_upd;
+    HostBuf<int32_t> h_upd, h_len0;
 
     void forget_device_row(int32_t seq) {
         if (seq >= 0 && (size_t)seq < dev_len.size()) dev_len[(size_t)seq] = -1;
-        // (an admission that reuses the handle, a release or a failure)
-        if (bt_valid && std::find(bt_seqs.begin(), bt_seqs.end(), seq) != bt_seqs.end())
-            bt_valid = false;
+        bt.forget(seq);  // (an admission that reuses the handle, a release or a failure)
     }
     // Records for handles [0, n): grown by doubling; a new buffer holds
     // none (the old records are dropped with it).
@@ -283,6 +275,7 @@ void destroy_state(InstanceState *st) {
     st->h_rec.release();
     st->bt_dev.release();
     st->h_upd.release();
+    st->h_len0.release();
     if (st->done) (void)hipHostFree(st->done);
     st->done = nullptr;
     // the operator layer keeps split-K / cascade workspaces per stream:
@@ -702,8 +695,10 @@ int slow_step(InstanceState *st, std::vector<Item> &items, PhaseTrace &tr) {
     st->h_bt.n = st->h_lens.n = st->h_group.n = st->h_pblocks.n = st->h_upd.n = 0;
     int width = 1, ng = 0, stride = 0;
     bool update = false;  // the device-resident tables are updated, not uploaded
-    if (rc == 0 && !st->h_lens.reserve(items.size())) rc = fail("exec: out of host memory");
+    if (rc == 0 && (!st->h_lens.reserve(items.size()) || !st->h_len0.reserve(items.size())))
+        rc = fail("exec: out of host memory");
     if (rc == 0) {
+        st->h_len0.n = 0;
         for (const Item &it : items) {
             if (!it.io.query) continue;
             st->h_seqs.push(it.seq);
@@ -711,25 +706,13 @@ int slow_step(InstanceState *st, std::vector<Item> &items, PhaseTrace &tr) {
             st->h_optr.push((char *)it.io.output);
             const int len = nxt_kv_seq_len(st->index, it.seq);
             st->h_lens.p[st->h_lens.n++] = len;
+            st->h_len0.p[st->h_len0.n++] = it.len0;
             width = std::max(width, (len + s.block_size - 1) / s.block_size);
         }
         const int B = (int)st->h_seqs.n;
-        update = st->bt_valid && B > 0 && (size_t)B == st->bt_seqs.size() &&
-                 std::equal(st->bt_seqs.begin(), st->bt_seqs.end(), st->h_seqs.p) &&
-                 width <= st->bt_stride;
+        update = st->bt.can_update(st->h_seqs.p, st->h_len0.p, B, width);
         if (update) {
-            // every row covers its sequence up to this exec's tokens
-            int i = 0;
-            for (const Item &it : items) {
-                if (!it.io.query) continue;
-                if (it.len0 != st->bt_len[(size_t)i++]) {
-                    update = false;
-                    break;
-                }
-            }
-        }
-        if (B > 0 && update) {
-            stride = st->bt_stride;
+            stride = st->bt.stride;
             if (!st->h_upd.reserve(2 * opened.size() + 2)) {
                 rc = fail("exec: out of host memory");
             } else {
@@ -737,15 +720,14 @@ int slow_step(InstanceState *st, std::vector<Item> &items, PhaseTrace &tr) {
                 for (const Item &it : items) {
                     if (!it.io.query) continue;
                     for (size_t k = it.open0; k < it.open0 + it.nopen; ++k) {
-                        st->h_upd.p[st->h_upd.n++] = i * stride + opened[k].first;
+                        st->h_upd.p[st->h_upd.n++] = st->bt.index(i, opened[k].first);
                         st->h_upd.p[st->h_upd.n++] = opened[k].second;
                     }
                     ++i;
                 }
             }
         } else if (B > 0) {
-            stride = std::min(((width + InstanceState::kTableSlack + 15) / 16) * 16,
-                              std::max(s.max_blocks, width));
+            stride = xhip::ResidentTables::upload_stride(width, s.max_blocks);
             if (!st->h_bt.reserve((size_t)B * stride) ||
                 !st->bt_dev.reserve((size_t)B * stride + 64)) {
                 rc = fail("exec: out of memory");
@@ -759,11 +741,11 @@ int slow_step(InstanceState *st, std::vector<Item> &items, PhaseTrace &tr) {
             if (!st->h_group.reserve((size_t)B) || !st->h_pblocks.reserve((size_t)B / 2 + 1)) {
                 rc = fail("exec: out of host memory");
             } else if (update) {
-                ng = st->bt_ng;
-                st->h_group.n = st->bt_group.size();
-                st->h_pblocks.n = st->bt_pblocks.size();
-                std::memcpy(st->h_group.p, st->bt_group.data(), st->h_group.n * sizeof(int32_t));
-                std::memcpy(st->h_pblocks.p, st->bt_pblocks.data(),
+                ng = st->bt.num_groups;
+                st->h_group.n = st->bt.group.size();
+                st->h_pblocks.n = st->bt.pblocks.size();
+                std::memcpy(st->h_group.p, st->bt.group.data(), st->h_group.n * sizeof(int32_t));
+                std::memcpy(st->h_pblocks.p, st->bt.pblocks.data(),
                             st->h_pblocks.n * sizeof(int32_t));
             } else {
                 st->h_group.n = (size_t)B;
@@ -873,19 +855,9 @@ int slow_step(InstanceState *st, std::vector<Item> &items, PhaseTrace &tr) {
         if (a != NXT_ATTN_OK) rc = fail("exec: attention: %s", nxt_attn_last_error());
     }
     // what the device-resident tables now hold
-    if (B > 0 || rc != 0) {
-        st->bt_valid = rc == 0 && staged;
-        if (st->bt_valid) {
-            if (!update) {
-                st->bt_seqs.assign(st->h_seqs.p, st->h_seqs.p + B);
-                st->bt_stride = stride;
-                st->bt_group.assign(st->h_group.p, st->h_group.p + st->h_group.n);
-                st->bt_pblocks.assign(st->h_pblocks.p, st->h_pblocks.p + st->h_pblocks.n);
-                st->bt_ng = ng;
-            }
-            st->bt_len.assign(st->h_lens.p, st->h_lens.p + B);
-        }
-    }
+    if (B > 0 || rc != 0)
+        st->bt.commit(rc == 0 && staged, !update, st->h_seqs.p, st->h_lens.p, B, stride,
+                      st->h_group.p, st->h_group.n, st->h_pblocks.p, st->h_pblocks.n, ng);
     return rc;
 }
 
